@@ -1,0 +1,342 @@
+"""bench.py — fused logprob/entropy forward + backward on one MI355X.
+
+Metric: fwd/bwd ms + HBM TB/s (% of peak) at B*S=1024,
+V=152064 bf16 (config C2).  A step is one forward and one backward launch of
+the fused kernels over that batch, through the library's C ABI (via
+kernel_opt._C), with inputs resident in HBM.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2]
+                    [--no-cpu-baseline] [--flush]
+
+Prints ONE JSON line.  `value` = achieved algorithmic HBM bandwidth over the
+whole step (fwd bytes + bwd bytes) / (fwd + bwd time), in TB/s.
+
+Algorithmic bytes per launch (s = bytes per logit, N rows, V vocab):
+    forward  = N*V*s + 8N (targets) + 12N (logp, entropy, lse)
+    backward = 2*N*V*s + 8N (targets) + 16N (lse, entropy, g_logp, g_ent)
+(g_lse is None in these workloads, so it is not read.)
+
+The roofline object reports the dominant kernel (the backward: it moves
+twice the forward's bytes).  Kernel times come from HIP events recorded on
+the stream the kernels run on, around each launch, averaged over the timed
+steps.
+
+The cpu_baseline leg times the reference's CPU eager path (TRL
+selective_log_softmax + entropy_from_logits forward, restated in
+oracle/eager_ref.py, plus PyTorch autograd through the eager formulas for
+the backward) on a bounded sample of rows of the same workload, on this
+machine's cores, and scales it to the full batch.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "fused-logprob-entropy-cuda-kernel-for-llm-post-training_amd")
+for _p in (PKG_DIR, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+HBM_PEAK_TBPS = 8.0
+ROW_BLOCK = 256  # rows per seeded generator block
+
+# BASELINE.json configs.  Seeds are per config; each block of ROW_BLOCK rows
+# draws from its own generator seeded with seed * 1_000_003 + block, so any
+# row subset can be regenerated on its own.
+CONFIGS = {
+    "C1": dict(dtype=torch.float32, shape=(2, 128, 32000), sigma=2.0, seed=1001,
+               g_logp=1.0 / 256, g_ent=0.01 / 256),
+    "C2": dict(dtype=torch.bfloat16, shape=(4, 256, 152064), sigma=2.0, seed=1002,
+               g_logp=-1.0 / 1024, g_ent=-0.01 / 1024),
+    "C3": dict(dtype=torch.float16, shape=(8, 1024, 128256), sigma=3.0, seed=1003,
+               spike=18.0, p_target_spike=0.6, g_logp=-1.0 / 8192, g_ent=-0.01 / 8192),
+    "C4": dict(dtype=torch.bfloat16, shape=(16, 2048, 151936), sigma=2.5, seed=1004,
+               mask_p=0.7),
+    "C5": dict(dtype=torch.float32, shape=(4, 2048, 262144), sigma=1.5, seed=1005,
+               parent_len=2049, g_logp=-1.0 / 8192, g_ent=-0.01 / 8192),
+}
+
+
+def _gen(device, seed):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def make_inputs(name: str, device="cuda", n_rows: int | None = None):
+    """Synthetic inputs of config `name` (first `n_rows` rows if given).
+
+    Returns dict(logits, targets, g_logp, g_ent, parent?) on `device`.
+    logits is [B, S, V] (C5: the non-contiguous slice parent[:, :-1, :]);
+    when n_rows is given the leading dims collapse to [n_rows, V] (C5 keeps
+    its strided layout by slicing whole batch elements).
+    """
+    cfg = CONFIGS[name]
+    B, S, V = cfg["shape"]
+    N = B * S
+    dtype = cfg["dtype"]
+    device = torch.device(device)
+    if name == "C5":
+        L = cfg["parent_len"]
+        b_keep = B if n_rows is None else max(1, math.ceil(n_rows / S))
+        parent = torch.zeros(b_keep, L, V, dtype=dtype, device=device)
+        rows_view = parent[:, :-1, :]
+        flat_rows = [(b, s) for b in range(b_keep) for s in range(S)]
+        n = len(flat_rows)
+        for blk in range(0, n, ROW_BLOCK):
+            g = _gen(device, cfg["seed"] * 1_000_003 + blk // ROW_BLOCK)
+            cnt = min(ROW_BLOCK, n - blk)
+            vals = torch.randn(cnt, V, generator=g, device=device) * cfg["sigma"]
+            for i in range(cnt):
+                b, s = flat_rows[blk + i]
+                rows_view[b, s].copy_(vals[i])
+        logits = rows_view
+        tg = _gen(device, cfg["seed"] * 7 + 1)
+        targets = torch.randint(0, V, (b_keep, S), generator=tg, device=device)
+        if n_rows is not None and n_rows < b_keep * S:
+            pass  # whole batch elements are kept so the strided layout stays
+        n = b_keep * S
+        grads = _grads(cfg, n, device)
+        return dict(logits=logits, targets=targets, parent=parent,
+                    **{k: (v.view(b_keep, S) if v is not None else None) for k, v in grads.items()})
+
+    n = N if n_rows is None else n_rows
+    logits = torch.empty(n, V, dtype=dtype, device=device)
+    targets = torch.empty(n, dtype=torch.int64, device=device)
+    for blk in range(0, n, ROW_BLOCK):
+        cnt = min(ROW_BLOCK, n - blk)
+        g = _gen(device, cfg["seed"] * 1_000_003 + blk // ROW_BLOCK)
+        vals = torch.randn(cnt, V, generator=g, device=device) * cfg["sigma"]
+        tgt = torch.randint(0, V, (cnt,), generator=g, device=device)
+        if "spike" in cfg:
+            spike_idx = torch.randint(0, V, (cnt,), generator=g, device=device)
+            vals[torch.arange(cnt, device=device), spike_idx] += cfg["spike"]
+            use_spike = torch.rand(cnt, generator=g, device=device) < cfg["p_target_spike"]
+            tgt = torch.where(use_spike, spike_idx, tgt)
+        logits[blk:blk + cnt] = vals.to(dtype)
+        targets[blk:blk + cnt] = tgt
+    grads = _grads(cfg, n, device)
+    if n_rows is None:
+        logits = logits.view(B, S, V)
+        targets = targets.view(B, S)
+        grads = {k: (v.view(B, S) if v is not None else None) for k, v in grads.items()}
+    return dict(logits=logits, targets=targets, **grads)
+
+
+def _grads(cfg, n, device):
+    if "mask_p" in cfg:
+        # loss = -mean(mask * (logp + 0.01 * H)) over all B*S tokens
+        B, S, _ = cfg["shape"]
+        g = _gen(device, cfg["seed"] * 7 + 2)
+        mask = (torch.rand(n, generator=g, device=device) < cfg["mask_p"]).float()
+        return dict(g_logp=-mask / (B * S), g_ent=-0.01 * mask / (B * S))
+    return dict(g_logp=torch.full((n,), cfg["g_logp"], device=device),
+                g_ent=torch.full((n,), cfg["g_ent"], device=device))
+
+
+def algorithmic_bytes(n_rows: int, vocab: int, elem_bytes: int):
+    fwd = n_rows * vocab * elem_bytes + 8 * n_rows + 12 * n_rows
+    bwd = 2 * n_rows * vocab * elem_bytes + 8 * n_rows + 16 * n_rows
+    return fwd, bwd
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the reference's CPU eager path on a bounded row sample.
+# ---------------------------------------------------------------------------
+def cpu_baseline(name: str, sample_rows: int, logits_gpu, targets_gpu, g_logp, g_ent):
+    from oracle import eager_ref
+
+    cfg = CONFIGS[name]
+    V = cfg["shape"][2]
+    N = logits_gpu.numel() // V
+    rows = min(sample_rows, N)
+    x = logits_gpu.reshape(-1, V)[:rows].detach().cpu().contiguous()
+    t = targets_gpu.reshape(-1)[:rows].cpu()
+    gl = g_logp.reshape(-1)[:rows].cpu()
+    ge = g_ent.reshape(-1)[:rows].cpu()
+    threads = torch.get_num_threads()
+
+    def fwd():
+        lp = eager_ref.trl_selective_log_softmax(x.unsqueeze(0), t.unsqueeze(0))
+        h = eager_ref.trl_entropy_from_logits(x.unsqueeze(0))
+        return lp, h
+
+    def fwd_bwd():
+        xr = x.clone().requires_grad_(True)
+        lp, h, _ = eager_ref.ref_forward_pt(xr, t)
+        (lp * gl + h * ge).sum().backward()
+        return xr.grad
+
+    fwd()  # warm-up
+    t0 = time.perf_counter()
+    fwd()
+    t_fwd = time.perf_counter() - t0
+    fwd_bwd()
+    t0 = time.perf_counter()
+    fwd_bwd()
+    t_fb = time.perf_counter() - t0
+    scale = N / rows
+    return dict(fwd_ms=t_fwd * scale * 1e3, fwd_bwd_ms=t_fb * scale * 1e3, rows=rows,
+                threads=threads)
+
+
+# ---------------------------------------------------------------------------
+# GPU timing
+# ---------------------------------------------------------------------------
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
+    ap.add_argument("--flush", action="store_true",
+                    help="write a 1 GiB buffer before every launch (cold Infinity Cache)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=16,
+                    help="rows of the workload the CPU baseline times")
+    ap.add_argument("--fwd-config", default=None, help="waves,unroll,splits,nt")
+    ap.add_argument("--bwd-config", default=None, help="waves,unroll,splits,nt")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(rows are independent, so data-parallel ranks would each run this same "
+              "kernel on their own batch with no exchange)", file=sys.stderr)
+        return 2
+
+    from kernel_opt import _C
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    name = args.config
+    cfg = CONFIGS[name]
+    inp = make_inputs(name, dev)
+    logits, targets = inp["logits"], inp["targets"]
+    g_logp, g_ent = inp["g_logp"].contiguous(), inp["g_ent"].contiguous()
+    V = logits.size(-1)
+    N = logits.numel() // V
+    esz = logits.element_size()
+    logp = torch.empty(targets.shape, dtype=torch.float32, device=dev)
+    ent = torch.empty_like(logp)
+    lse = torch.empty_like(logp)
+    d_logits = torch.empty(logits.shape, dtype=logits.dtype, device=dev)
+    fcfg = tuple(int(v) for v in args.fwd_config.split(",")) if args.fwd_config else None
+    bcfg = tuple(int(v) for v in args.bwd_config.split(",")) if args.bwd_config else None
+    flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev) if args.flush else None
+
+    def fwd():
+        _C.fwd_launch(logits, targets, logp, ent, lse, config=fcfg)
+
+    def bwd():
+        _C.bwd_launch(logits, targets, lse, ent, g_logp, g_ent, None, d_logits, config=bcfg)
+
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(args.warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
+    torch.cuda.synchronize()
+    t_wall0 = time.perf_counter()
+    for k in range(K):
+        if flush_buf is not None:
+            flush_buf.fill_(k & 0xFF)
+        ev[k][0].record(stream)
+        fwd()
+        ev[k][1].record(stream)
+        if flush_buf is not None:
+            flush_buf.fill_((k + 1) & 0xFF)
+        ev[k][2].record(stream)
+        bwd()
+        ev[k][3].record(stream)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall0
+
+    fwd_ms = [e[0].elapsed_time(e[1]) for e in ev]
+    bwd_ms = [e[2].elapsed_time(e[3]) for e in ev]
+    fwd_avg = sum(fwd_ms) / K
+    bwd_avg = sum(bwd_ms) / K
+    fwd_med = sorted(fwd_ms)[K // 2]
+    bwd_med = sorted(bwd_ms)[K // 2]
+    fb, bb = algorithmic_bytes(N, V, esz)
+    fwd_tbps = fb / (fwd_avg * 1e-3) / 1e12
+    bwd_tbps = bb / (bwd_avg * 1e-3) / 1e12
+    step_ms = fwd_avg + bwd_avg
+    step_tbps = (fb + bb) / (step_ms * 1e-3) / 1e12
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        c = cpu_baseline(name, args.cpu_rows, logits, targets, g_logp, g_ent)
+        cpu = {
+            "value": (fb + bb) / ((c["fwd_ms"] + c["fwd_bwd_ms"]) * 1e-3) / 1e12,
+            "unit": "TB/s",
+            "cores": c["threads"],
+            "kind": "port",
+            "sample": (f"{c['rows']} of {N} rows of {name}, timed once after one warm-up and "
+                       f"scaled by {N}/{c['rows']}: TRL-eager forward (restated) "
+                       f"{c['fwd_ms']:.1f} ms, eager fwd+autograd bwd {c['fwd_bwd_ms']:.1f} ms "
+                       f"for the full batch"),
+            "fwd_ms": c["fwd_ms"],
+            "fwd_bwd_ms": c["fwd_bwd_ms"],
+        }
+
+    B, S, _ = cfg["shape"]
+    fwd_used = fcfg or _C.default_config("fwd", logits.dtype, N, V)
+    bwd_used = bcfg or _C.default_config("bwd", logits.dtype, N, V)
+    out = {
+        "metric": "fwd/bwd ms + HBM TB/s (% of peak) at B*S=1024, V=152064 bf16",
+        "value": round(step_tbps, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[
+            logits.dtype],
+        "data": "synthetic",
+        "config": {"workload": f"{name}: logits [{B},{S},{V}] "
+                               f"{str(logits.dtype).replace('torch.', '')}, fwd+bwd",
+                   "global_batch": B, "seq_len": S, "vocab": V, "n_rows": N,
+                   "parallelism": "single-gpu",
+                   "infinity_cache": "flushed" if args.flush else "warm"},
+        "fwd_ms": round(fwd_avg, 5),
+        "bwd_ms": round(bwd_avg, 5),
+        "fwd_ms_median": round(fwd_med, 5),
+        "bwd_ms_median": round(bwd_med, 5),
+        "fwd_tbps": round(fwd_tbps, 4),
+        "bwd_tbps": round(bwd_tbps, 4),
+        "fwd_pct_peak": round(100 * fwd_tbps / HBM_PEAK_TBPS, 2),
+        "bwd_pct_peak": round(100 * bwd_tbps / HBM_PEAK_TBPS, 2),
+        "fwd_launch": dict(zip(("waves", "unroll", "splits", "nontemporal"), fwd_used)),
+        "bwd_launch": dict(zip(("waves", "unroll", "splits", "nontemporal"), bwd_used)),
+        "wall_s_timed": round(t_wall, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "klp_bwd_kernel",
+            "achieved": round(bb / (bwd_avg * 1e-3) / 1e9, 1),
+            "peak": HBM_PEAK_TBPS * 1000,
+            "unit": "GB/s",
+            "frac": round(bwd_tbps / HBM_PEAK_TBPS, 4),
+            "traffic": None,
+            "algorithmic_bytes": bb,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

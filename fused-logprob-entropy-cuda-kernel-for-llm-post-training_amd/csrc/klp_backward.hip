@@ -1,0 +1,170 @@
+// klp_backward.hip — backward kernel for gfx950 (replaces the reference's
+// fused_logprob_entropy_v1_backward_kernel, csrc/fused_logprob.cu:243-282).
+//
+// For every element of a row:
+//   lp = x - lse,  p = exp(lp),
+//   d  = p * (c0 - g_ent * lp) + (v == t ? g_logp : 0),
+//   c0 = g_lse - g_logp - g_ent * H          (hoisted per row, as at :271)
+// One 16-byte load and one 16-byte store per 16 bytes of logits; nothing else
+// touches memory except eight per-row scalars.
+//
+// p is computed as 2^(x*log2e - lse*log2e) with lse*log2e split into a
+// rounded head and its exact fma remainder, so the exponent carries one
+// rounding.  A -inf logit gets a gradient of exactly 0 (p = 0), where the
+// reference's 0 * inf gives NaN; lp is clamped for that.
+#include "klp_device.h"
+#include "klp_launch.h"
+
+namespace klp {
+
+struct RowGrad {
+    float lse, lse_hi, lse_lo, g_ent, g_logp, c0;
+};
+
+__device__ __forceinline__ float grad_one(float x, const RowGrad& g) {
+    const float lp = fmax_nan(x - g.lse, kNegBig);
+    const float arg = fmaf(x, kLog2e, -g.lse_hi) - g.lse_lo;
+    const float p = exp2_hw(arg);
+    return p * fmaf(-g.g_ent, lp, g.c0);
+}
+
+template <int DT, int WAVES, int U, bool kNT>
+__global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
+    typedef typename Traits<DT>::elem elem;
+    constexpr int NTHREADS = WAVES * 64;
+    constexpr int EPV = Traits<DT>::kPerVec;
+    constexpr int ESZ = 16 / EPV;
+
+    const int tid = threadIdx.x;
+    int64_t row;
+    int split;
+    block_to_row_split(blockIdx.x, p.splits, row, split);
+    if (row >= p.n_rows) return;
+
+    const int64_t vocab = p.vocab;
+    const elem* rp = static_cast<const elem*>(p.logits) + row_offset(p.rm, row);
+    elem* dp = static_cast<elem*>(p.d_logits) + row * vocab;
+    const int64_t tgt = p.targets[row];
+
+    RowGrad g;
+    g.lse = p.lse[row];
+    const float ent = p.entropy[row];
+    g.g_logp = p.g_logp ? p.g_logp[row] : 0.0f;
+    g.g_ent = p.g_ent ? p.g_ent[row] : 0.0f;
+    const float g_lse = p.g_lse ? p.g_lse[row] : 0.0f;
+    g.c0 = g_lse - g.g_logp - g.g_ent * ent;
+    g.lse_hi = g.lse * kLog2e;
+    g.lse_lo = fmaf(g.lse, kLog2e, -g.lse_hi);
+
+    const uintptr_t in_addr = reinterpret_cast<uintptr_t>(rp);
+    const uintptr_t out_addr = reinterpret_cast<uintptr_t>(dp);
+    if (((in_addr ^ out_addr) & 15u) != 0) {
+        // Input and output rows sit at different offsets within 16 bytes, so
+        // they cannot both be read/written as aligned vectors: scalar path.
+        const int64_t per = (vocab + p.splits - 1) / p.splits;
+        int64_t b = static_cast<int64_t>(split) * per;
+        int64_t e = b + per;
+        if (e > vocab) e = vocab;
+        for (int64_t v = b + tid; v < e; v += NTHREADS) {
+            float d = grad_one(to_f32<DT>(rp[v]), g);
+            if (v == tgt) d += g.g_logp;
+            dp[v] = from_f32<DT>(d);
+        }
+        return;
+    }
+
+    int64_t head = static_cast<int64_t>(((16u - (in_addr & 15u)) & 15u) / ESZ);
+    if (head > vocab) head = vocab;
+    const int64_t nvec = (vocab - head) / EPV;
+    const int64_t tail_begin = head + nvec * EPV;
+
+    if (split == 0) {
+        const int64_t n_edge = head + (vocab - tail_begin);
+        if (tid < n_edge) {
+            const int64_t v = (tid < head) ? tid : tail_begin + (tid - head);
+            float d = grad_one(to_f32<DT>(rp[v]), g);
+            if (v == tgt) d += g.g_logp;
+            dp[v] = from_f32<DT>(d);
+        }
+    }
+
+    const u32x4* vin = reinterpret_cast<const u32x4*>(rp + head);
+    u32x4* vout = reinterpret_cast<u32x4*>(dp + head);
+    const int64_t per = (nvec + p.splits - 1) / p.splits;
+    int64_t vb = static_cast<int64_t>(split) * per;
+    int64_t ve = vb + per;
+    if (vb > nvec) vb = nvec;
+    if (ve > nvec) ve = nvec;
+
+    // Vector index holding the target's one-hot term (or -1).
+    const int64_t t_rel = tgt - head;
+    const int64_t t_vec = (tgt >= head && tgt < tail_begin) ? t_rel / EPV : -1;
+    const int t_lane_elem = (t_vec >= 0) ? static_cast<int>(t_rel - t_vec * EPV) : 0;
+
+    for (int64_t i0 = vb; i0 < ve; i0 += static_cast<int64_t>(NTHREADS) * U) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t idx = i0 + tid + u * NTHREADS;
+            if (idx < ve) v[u] = load16<kNT>(vin + idx);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t idx = i0 + tid + u * NTHREADS;
+            if (idx < ve) {
+                float x[EPV];
+                unpack<DT>(v[u], x);
+#pragma unroll
+                for (int j = 0; j < EPV; ++j) x[j] = grad_one(x[j], g);
+                if (idx == t_vec) {
+#pragma unroll
+                    for (int j = 0; j < EPV; ++j)
+                        if (j == t_lane_elem) x[j] += g.g_logp;
+                }
+                vout[idx] = pack<DT>(x);
+            }
+        }
+    }
+}
+
+template <int DT, int WAVES, int U, bool kNT>
+static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
+    const int64_t blocks = (p.splits == 1) ? p.n_rows : ((p.n_rows + 7) / 8) * 8 * p.splits;
+    hipLaunchKernelGGL((klp_bwd_kernel<DT, WAVES, U, kNT>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(WAVES * 64), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_bwd_dt(const BwdParams& p, const BwdConfig& c, hipStream_t stream) {
+#define KLP_BWD_CASE(W, U, NT)                                           \
+    if (c.waves == W && c.unroll == U && c.nontemporal == NT)            \
+        return launch_bwd_t<DT, W, U, NT>(p, stream);
+    KLP_BWD_CASE(4, 2, true)
+    KLP_BWD_CASE(4, 4, true)
+    KLP_BWD_CASE(8, 2, true)
+    KLP_BWD_CASE(8, 4, true)
+    KLP_BWD_CASE(4, 2, false)
+    KLP_BWD_CASE(4, 4, false)
+    KLP_BWD_CASE(8, 2, false)
+    KLP_BWD_CASE(8, 4, false)
+#undef KLP_BWD_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, hipStream_t stream) {
+    switch (dtype) {
+        case kBF16: return launch_bwd_dt<kBF16>(p, c, stream);
+        case kFP16: return launch_bwd_dt<kFP16>(p, c, stream);
+        case kFP32: return launch_bwd_dt<kFP32>(p, c, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool bwd_config_supported(const BwdConfig& c) {
+    const bool w = (c.waves == 4 || c.waves == 8);
+    const bool u = (c.unroll == 2 || c.unroll == 4);
+    return w && u;
+}
+
+}  // namespace klp

@@ -1,0 +1,282 @@
+// klp_device.h — device-side building blocks for the gfx950 kernels:
+// dtype traits, 128-bit vector unpack/pack, row addressing, the online
+// (max, sum-exp, sum-shifted-x*exp) state and its associative combine, and
+// the wave64 reduction.
+//
+// Arithmetic is done in base 2 so that each element costs one v_exp_f32:
+//   y = x * log2(e),   o = RN(m * log2(e))   (m = running max of x),
+//   z = sum 2^(y - o),
+//   t = sum (y - o) * 2^(y - o)          (<= 0).
+// The reference carries the same three quantities in base e
+// (csrc/fused_logprob.cu:13-27, PartialState :135-139); the final formulas
+// below convert back to nats.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace klp {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kLn2 = 0.69314718055994530942f;
+// Finite stand-in for -inf exponents: 2^kNegBig == 0 and kNegBig * 0 == 0,
+// where -inf * 0 would be NaN.
+constexpr float kNegBig = -1.0e30f;
+
+enum : int { kBF16 = 0, kFP16 = 1, kFP32 = 2 };
+
+template <int DT> struct Traits;
+template <> struct Traits<kBF16> {
+    typedef uint16_t elem;
+    static constexpr int kPerVec = 8;
+    static constexpr uint32_t kNegInfWord = 0xFF80FF80u;
+};
+template <> struct Traits<kFP16> {
+    typedef uint16_t elem;
+    static constexpr int kPerVec = 8;
+    static constexpr uint32_t kNegInfWord = 0xFC00FC00u;
+};
+template <> struct Traits<kFP32> {
+    typedef uint32_t elem;
+    static constexpr int kPerVec = 4;
+    static constexpr uint32_t kNegInfWord = 0xFF800000u;
+};
+
+// ---------------------------------------------------------------------------
+// Conversions.  Up-conversion is exact.  Down-conversion rounds to nearest
+// even and keeps fp16 subnormals (v_cvt_pk_bf16_f32 / v_cvt_f16_f32 under the
+// default MODE register), matching __float2bfloat16 / __float2half in the
+// reference (csrc/fused_logprob.cu:53-67).
+// ---------------------------------------------------------------------------
+template <int DT> __device__ __forceinline__ float to_f32(typename Traits<DT>::elem e);
+template <> __device__ __forceinline__ float to_f32<kBF16>(uint16_t e) {
+    return __uint_as_float(static_cast<uint32_t>(e) << 16);
+}
+template <> __device__ __forceinline__ float to_f32<kFP16>(uint16_t e) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, e));
+}
+template <> __device__ __forceinline__ float to_f32<kFP32>(uint32_t e) {
+    return __uint_as_float(e);
+}
+
+template <int DT> __device__ __forceinline__ typename Traits<DT>::elem from_f32(float x);
+template <> __device__ __forceinline__ uint16_t from_f32<kBF16>(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+}
+template <> __device__ __forceinline__ uint16_t from_f32<kFP16>(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+template <> __device__ __forceinline__ uint32_t from_f32<kFP32>(float x) {
+    return __float_as_uint(x);
+}
+
+// 16 bytes -> Traits<DT>::kPerVec floats, element order = memory order.
+template <int DT> __device__ __forceinline__ void unpack(const u32x4 v, float* x);
+template <> __device__ __forceinline__ void unpack<kBF16>(const u32x4 v, float* x) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        x[2 * j] = __uint_as_float(v[j] << 16);
+        x[2 * j + 1] = __uint_as_float(v[j] & 0xFFFF0000u);
+    }
+}
+template <> __device__ __forceinline__ void unpack<kFP16>(const u32x4 v, float* x) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f32x2 f = __builtin_convertvector(__builtin_bit_cast(f16x2, v[j]), f32x2);
+        x[2 * j] = f.x;
+        x[2 * j + 1] = f.y;
+    }
+}
+template <> __device__ __forceinline__ void unpack<kFP32>(const u32x4 v, float* x) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = __uint_as_float(v[j]);
+}
+
+// kPerVec floats -> 16 bytes, round to nearest even.
+template <int DT> __device__ __forceinline__ u32x4 pack(const float* x);
+template <> __device__ __forceinline__ u32x4 pack<kBF16>(const float* x) {
+    u32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f32x2 f = {x[2 * j], x[2 * j + 1]};
+        r[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+    }
+    return r;
+}
+template <> __device__ __forceinline__ u32x4 pack<kFP16>(const float* x) {
+    u32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f32x2 f = {x[2 * j], x[2 * j + 1]};
+        r[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+    }
+    return r;
+}
+template <> __device__ __forceinline__ u32x4 pack<kFP32>(const float* x) {
+    u32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = __float_as_uint(x[j]);
+    return r;
+}
+
+template <bool kNonTemporal>
+__device__ __forceinline__ u32x4 load16(const u32x4* p) {
+    if constexpr (kNonTemporal) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+
+__device__ __forceinline__ float fmax_nan(float a, float b) {
+    // NaN-propagating maximum (v_maximum3_f32 on gfx950): a NaN logit turns
+    // the running max, and with it every output of its row, into NaN.
+    return __builtin_elementwise_maximum(a, b);
+}
+
+__device__ __forceinline__ float exp2_hw(float u) { return __builtin_amdgcn_exp2f(u); }
+
+// ---------------------------------------------------------------------------
+// Row addressing: row r starts at (r / rows_inner) * stride_outer +
+// (r % rows_inner) * stride_inner elements.
+// ---------------------------------------------------------------------------
+struct RowMap {
+    int64_t rows_inner;
+    int64_t stride_outer;
+    int64_t stride_inner;
+};
+
+__device__ __forceinline__ int64_t row_offset(const RowMap& rm, int64_t r) {
+    if (r < rm.rows_inner) return r * rm.stride_inner;
+    const int64_t q = r / rm.rows_inner;
+    return q * rm.stride_outer + (r - q * rm.rows_inner) * rm.stride_inner;
+}
+
+// Workgroup -> (row, split).  Workgroups are dispatched round-robin over the
+// 8 XCDs (blockIdx % 8); with splits > 1 the splits of one row are given
+// consecutive blockIdx values that are 8 apart, so they share an XCD and its
+// L2, where the last one reads the others' partial states.
+__device__ __forceinline__ void block_to_row_split(int64_t b, int splits, int64_t& row,
+                                                   int& split) {
+    if (splits == 1) {
+        row = b;
+        split = 0;
+        return;
+    }
+    const int64_t xcd = b & 7;
+    const int64_t k = b >> 3;
+    const int64_t group = k / splits;
+    split = static_cast<int>(k - group * splits);
+    row = group * 8 + xcd;
+}
+
+// ---------------------------------------------------------------------------
+// Online state.  Empty state: (m = -inf, z = 0, t = 0), the reference's
+// sentinel (csrc/fused_logprob.cu:127-129).
+// ---------------------------------------------------------------------------
+struct Stat {
+    float m;
+    float z;
+    float t;
+};
+
+__device__ __forceinline__ Stat stat_empty() { return Stat{-INFINITY, 0.0f, 0.0f}; }
+
+// Associative merge; restates combine() of csrc/fused_logprob.cu:141-154
+// (including its empty-side early returns) in base-2 units.
+__device__ __forceinline__ Stat combine(const Stat a, const Stat b) {
+    if (b.m == -INFINITY) return a;
+    if (a.m == -INFINITY) return b;
+    const float m = fmax_nan(a.m, b.m);
+    const float o = m * kLog2e;
+    const float da = a.m * kLog2e - o;  // <= 0
+    const float db = b.m * kLog2e - o;  // <= 0
+    const float sa = exp2_hw(da);
+    const float sb = exp2_hw(db);
+    Stat r;
+    r.m = m;
+    r.z = sa * a.z + sb * b.z;
+    r.t = sa * fmaf(da, a.z, a.t) + sb * fmaf(db, b.z, b.t);
+    return r;
+}
+
+// Absorb K values into the state: one rescale of (z, t) to the new maximum,
+// then one exp2 per value.  With kClamp == false a -inf value makes t NaN
+// (-inf * 0) while z stays finite; the caller detects that and redoes the
+// values with kClamp == true, which maps -inf exponents to kNegBig.
+template <int K, bool kClamp>
+__device__ __forceinline__ void absorb(Stat& s, const float* x) {
+    float c = s.m;
+#pragma unroll
+    for (int j = 0; j < K; ++j) c = fmax_nan(c, x[j]);
+    const float o_raw = c * kLog2e;
+    const float o = (c == -INFINITY) ? 0.0f : o_raw;
+    const float d = (s.m == -INFINITY) ? kNegBig : fmax_nan(s.m * kLog2e - o_raw, kNegBig);
+    const float sc = exp2_hw(d);
+    float z0 = sc * s.z;
+    float t0 = sc * fmaf(d, s.z, s.t);
+    float z1 = 0.0f, t1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        float u = fmaf(x[j], kLog2e, -o);
+        if (kClamp) u = fmax_nan(u, kNegBig);
+        const float e = exp2_hw(u);
+        if (j & 1) {
+            z1 += e;
+            t1 = fmaf(u, e, t1);
+        } else {
+            z0 += e;
+            t0 = fmaf(u, e, t0);
+        }
+    }
+    s.m = c;
+    s.z = z0 + z1;
+    s.t = t0 + t1;
+}
+
+// True when the unclamped scan met a -inf value (t is NaN, z is not).
+__device__ __forceinline__ bool needs_clamped_rescan(const Stat& s) {
+    return __builtin_isnan(s.t) && !__builtin_isnan(s.z);
+}
+
+__device__ __forceinline__ Stat wave_reduce(Stat s) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        Stat o;
+        o.m = __shfl_xor(s.m, off, 64);
+        o.z = __shfl_xor(s.z, off, 64);
+        o.t = __shfl_xor(s.t, off, 64);
+        s = combine(s, o);
+    }
+    return s;
+}
+
+// Final per-row outputs (csrc/fused_logprob.cu:221-224 in base e):
+//   lse     = m + ln z + (o - m*log2e) * ln2
+//   entropy = ln z - ln2 * t / z
+//   logprob = x_target - lse
+// The middle term of lse undoes the rounding of o = RN(m*log2e); it is the
+// exact product remainder, obtained with one fma.
+struct RowOut {
+    float logp;
+    float ent;
+    float lse;
+};
+
+__device__ __forceinline__ RowOut finalize(const Stat s, float x_target) {
+    const float lnz = logf(s.z);
+    float rho = 0.0f;
+    if (s.m != -INFINITY) {
+        const float o = s.m * kLog2e;
+        rho = -fmaf(s.m, kLog2e, -o);
+    }
+    RowOut r;
+    r.lse = s.m + fmaf(rho, kLn2, lnz);
+    r.ent = fmaf(-kLn2, s.t / s.z, lnz);
+    r.logp = x_target - r.lse;
+    return r;
+}
+
+}  // namespace klp

@@ -1,0 +1,265 @@
+// klp_forward.hip — forward kernels for gfx950.
+//
+//  klp_fwd_kernel        production forward (replaces the reference's
+//                        fused_logprob_entropy_v1_kernel, csrc/fused_logprob.cu:156-227)
+//  klp_fwd_naive_kernel  one thread per row, scalar recurrence (replaces
+//                        fused_logprob_entropy_naive_kernel, :69-113)
+//
+// Production forward, per workgroup of WAVES wave64s:
+//  - a workgroup owns one row, or one of `splits` contiguous pieces of a row;
+//  - the row body is read with 16-byte loads (global_load_dwordx4), U per
+//    thread per iteration, consecutive lanes on consecutive 16-byte words;
+//    the few elements before the first 16-byte boundary and after the last
+//    one (head / tail) are read as scalars by split 0;
+//  - every U*16 bytes cost one rescale plus one v_exp_f32 per element
+//    (absorb() in klp_device.h);
+//  - lanes merge with xor-shuffles, waves through LDS in wave order, splits
+//    through a workspace in split order, so results do not depend on timing.
+#include "klp_device.h"
+#include "klp_launch.h"
+
+namespace klp {
+
+template <int DT, bool kClamp, int U, int NTHREADS, bool kNT>
+__device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT>::elem* rp,
+                                               const u32x4* vp, int64_t head, int64_t tail_begin,
+                                               int64_t vocab, bool with_edges, int64_t vb,
+                                               int64_t ve, int tid) {
+    constexpr int EPV = Traits<DT>::kPerVec;
+    // Scalar head / tail elements (fewer than 2 * EPV of them).
+    if (with_edges) {
+        const int64_t n_edge = head + (vocab - tail_begin);
+        if (tid < n_edge) {
+            const int64_t idx = (tid < head) ? tid : tail_begin + (tid - head);
+            float x = to_f32<DT>(rp[idx]);
+            absorb<1, true>(s, &x);
+        }
+    }
+    const int64_t step = static_cast<int64_t>(NTHREADS) * U;
+    int64_t i = vb + tid;
+    const int64_t n_full = (ve - vb) / step;
+    for (int64_t k = 0; k < n_full; ++k) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = load16<kNT>(vp + i + u * NTHREADS);
+        float x[U * EPV];
+#pragma unroll
+        for (int u = 0; u < U; ++u) unpack<DT>(v[u], x + u * EPV);
+        absorb<U * EPV, kClamp>(s, x);
+        i += step;
+    }
+    if (vb + n_full * step < ve) {
+        // Remainder: vectors past the end read as -inf, which the clamped
+        // absorb ignores.
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t idx = i + u * NTHREADS;
+            if (idx < ve) {
+                v[u] = load16<kNT>(vp + idx);
+            } else {
+                const uint32_t w = Traits<DT>::kNegInfWord;
+                v[u] = u32x4{w, w, w, w};
+            }
+        }
+        float x[U * EPV];
+#pragma unroll
+        for (int u = 0; u < U; ++u) unpack<DT>(v[u], x + u * EPV);
+        absorb<U * EPV, true>(s, x);
+    }
+}
+
+template <int DT, int WAVES, int U, bool kNT>
+__global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
+    typedef typename Traits<DT>::elem elem;
+    constexpr int NTHREADS = WAVES * 64;
+    constexpr int EPV = Traits<DT>::kPerVec;
+    constexpr int ESZ = 16 / EPV;
+
+    const int tid = threadIdx.x;
+    int64_t row;
+    int split;
+    block_to_row_split(blockIdx.x, p.splits, row, split);
+    if (row >= p.n_rows) return;  // whole workgroup leaves together
+
+    const int64_t vocab = p.vocab;
+    const elem* rp = static_cast<const elem*>(p.logits) + row_offset(p.rm, row);
+    const int64_t tgt = p.targets[row];
+
+    // The target logit is read directly; the reference captures it inside the
+    // scan (csrc/fused_logprob.cu:180,185) and leaves 0 when the target is out
+    // of range.  Issued first so its latency hides behind the scan.
+    float x_target = 0.0f;
+    if (tid == 0 && tgt >= 0 && tgt < vocab) x_target = to_f32<DT>(rp[tgt]);
+
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(rp);
+    int64_t head = static_cast<int64_t>(((16u - (addr & 15u)) & 15u) / ESZ);
+    if (head > vocab) head = vocab;
+    const int64_t nvec = (vocab - head) / EPV;
+    const int64_t tail_begin = head + nvec * EPV;
+    const u32x4* vp = reinterpret_cast<const u32x4*>(rp + head);
+
+    const int64_t per = (nvec + p.splits - 1) / p.splits;
+    int64_t vb = static_cast<int64_t>(split) * per;
+    int64_t ve = vb + per;
+    if (vb > nvec) vb = nvec;
+    if (ve > nvec) ve = nvec;
+
+    Stat s = stat_empty();
+    scan_row_piece<DT, false, U, NTHREADS, kNT>(s, rp, vp, head, tail_begin, vocab, split == 0,
+                                                vb, ve, tid);
+    if (needs_clamped_rescan(s)) {
+        // This lane met a -inf logit: redo its values with -inf excluded, as
+        // the reference's sentinel rule does (csrc/fused_logprob.cu:142-143).
+        s = stat_empty();
+        scan_row_piece<DT, true, U, NTHREADS, kNT>(s, rp, vp, head, tail_begin, vocab,
+                                                   split == 0, vb, ve, tid);
+    }
+
+    s = wave_reduce(s);
+    __shared__ Stat wave_stat[WAVES];
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    if (lane == 0) wave_stat[wave] = s;
+    __syncthreads();
+    if (tid != 0) return;
+
+    Stat r = wave_stat[0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) r = combine(r, wave_stat[w]);
+
+    if (p.splits == 1) {
+        const RowOut o = finalize(r, x_target);
+        p.logprob[row] = o.logp;
+        p.entropy[row] = o.ent;
+        p.lse[row] = o.lse;
+        return;
+    }
+
+    // Split-row mode: publish this piece's state; the last piece of the row
+    // to arrive merges all pieces in split order and resets the counter.
+    float* slot = p.partials + (row * p.splits + split) * 4;
+    slot[0] = r.m;
+    slot[1] = r.z;
+    slot[2] = r.t;
+    __threadfence();
+    const unsigned prev = atomicAdd(p.counters + row, 1u);
+    if (prev != static_cast<unsigned>(p.splits - 1)) return;
+    __threadfence();
+    Stat acc = stat_empty();
+    for (int k = 0; k < p.splits; ++k) {
+        float* q = p.partials + (row * p.splits + k) * 4;
+        Stat piece;
+        piece.m = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        piece.z = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        piece.t = __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        acc = combine(acc, piece);
+        // Leave the workspace all-zero for the next launch, whatever its
+        // layout (the counter region of a later, larger launch may cover
+        // these slots).
+        q[0] = 0.0f;
+        q[1] = 0.0f;
+        q[2] = 0.0f;
+    }
+    const RowOut o = finalize(acc, x_target);
+    p.logprob[row] = o.logp;
+    p.entropy[row] = o.ent;
+    p.lse[row] = o.lse;
+    __hip_atomic_store(p.counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Naive forward: restates the reference's one-thread-per-row recurrence with
+// its peeled first element (csrc/fused_logprob.cu:79-112), in base e.
+template <int DT>
+__global__ __launch_bounds__(128) void klp_fwd_naive_kernel(NaiveParams p) {
+    typedef typename Traits<DT>::elem elem;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (row >= p.n_rows) return;
+    const elem* rp = static_cast<const elem*>(p.logits) + row_offset(p.rm, row);
+    const int64_t tgt = p.targets[row];
+
+    const float x0 = to_f32<DT>(rp[0]);
+    float m = x0;
+    float z = 1.0f;
+    float t = 0.0f;
+    float x_target = (tgt == 0) ? x0 : 0.0f;
+    for (int64_t v = 1; v < p.vocab; ++v) {
+        const float x = to_f32<DT>(rp[v]);
+        if (v == tgt) x_target = x;
+        const float m_new = fmaxf(m, x);
+        const float delta = m - m_new;
+        const float scale = expf(delta);
+        const float v_new = x - m_new;
+        const float e = expf(v_new);
+        t = scale * (t + delta * z) + v_new * e;
+        z = scale * z + e;
+        m = m_new;
+    }
+    const float lnz = logf(z);
+    const float lse = m + lnz;
+    p.logprob[row] = x_target - lse;
+    p.entropy[row] = lnz - t / z;
+    p.lse[row] = lse;
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+template <int DT, int WAVES, int U, bool kNT>
+static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
+    const int64_t blocks = (p.splits == 1) ? p.n_rows : ((p.n_rows + 7) / 8) * 8 * p.splits;
+    hipLaunchKernelGGL((klp_fwd_kernel<DT, WAVES, U, kNT>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(WAVES * 64), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_fwd_dt(const FwdParams& p, const FwdConfig& c, hipStream_t stream) {
+#define KLP_FWD_CASE(W, U, NT)                                           \
+    if (c.waves == W && c.unroll == U && c.nontemporal == NT)            \
+        return launch_fwd_t<DT, W, U, NT>(p, stream);
+    KLP_FWD_CASE(4, 2, true)
+    KLP_FWD_CASE(4, 4, true)
+    KLP_FWD_CASE(8, 2, true)
+    KLP_FWD_CASE(8, 4, true)
+    KLP_FWD_CASE(4, 2, false)
+    KLP_FWD_CASE(4, 4, false)
+    KLP_FWD_CASE(8, 2, false)
+    KLP_FWD_CASE(8, 4, false)
+#undef KLP_FWD_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream) {
+    switch (dtype) {
+        case kBF16: return launch_fwd_dt<kBF16>(p, c, stream);
+        case kFP16: return launch_fwd_dt<kFP16>(p, c, stream);
+        case kFP32: return launch_fwd_dt<kFP32>(p, c, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool fwd_config_supported(const FwdConfig& c) {
+    const bool w = (c.waves == 4 || c.waves == 8);
+    const bool u = (c.unroll == 2 || c.unroll == 4);
+    return w && u;
+}
+
+hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream) {
+    const unsigned blocks = static_cast<unsigned>((p.n_rows + 127) / 128);
+    switch (dtype) {
+        case kBF16:
+            hipLaunchKernelGGL(klp_fwd_naive_kernel<kBF16>, dim3(blocks), dim3(128), 0, stream, p);
+            break;
+        case kFP16:
+            hipLaunchKernelGGL(klp_fwd_naive_kernel<kFP16>, dim3(blocks), dim3(128), 0, stream, p);
+            break;
+        case kFP32:
+            hipLaunchKernelGGL(klp_fwd_naive_kernel<kFP32>, dim3(blocks), dim3(128), 0, stream, p);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace klp

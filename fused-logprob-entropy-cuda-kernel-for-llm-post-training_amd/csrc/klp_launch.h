@@ -1,0 +1,68 @@
+// klp_launch.h — kernel parameter blocks and launcher declarations shared by
+// the kernel translation units and the C-ABI dispatcher (klp_abi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "klp_device.h"
+
+namespace klp {
+
+struct FwdParams {
+    const void* logits;
+    RowMap rm;
+    int64_t n_rows;
+    int64_t vocab;
+    const int64_t* targets;
+    float* logprob;
+    float* entropy;
+    float* lse;
+    float* partials;     // [n_rows_padded * splits * 4] when splits > 1
+    unsigned* counters;  // [n_rows_padded], zero between launches
+    int splits;
+};
+
+struct NaiveParams {
+    const void* logits;
+    RowMap rm;
+    int64_t n_rows;
+    int64_t vocab;
+    const int64_t* targets;
+    float* logprob;
+    float* entropy;
+    float* lse;
+};
+
+struct BwdParams {
+    const void* logits;
+    RowMap rm;
+    int64_t n_rows;
+    int64_t vocab;
+    const int64_t* targets;
+    const float* lse;
+    const float* entropy;
+    const float* g_logp;  // nullable
+    const float* g_ent;   // nullable
+    const float* g_lse;   // nullable
+    void* d_logits;       // dense [n_rows, vocab]
+    int splits;
+};
+
+// Launch shape: WAVES wave64s per workgroup, `unroll` 16-byte loads per
+// thread per iteration, `splits` workgroups per row, non-temporal loads.
+struct FwdConfig {
+    int waves;
+    int unroll;
+    int splits;
+    bool nontemporal;
+};
+typedef FwdConfig BwdConfig;
+
+hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream);
+hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream);
+hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, hipStream_t stream);
+bool fwd_config_supported(const FwdConfig& c);
+bool bwd_config_supported(const BwdConfig& c);
+
+}  // namespace klp

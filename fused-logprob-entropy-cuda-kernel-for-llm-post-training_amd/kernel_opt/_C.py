@@ -1,0 +1,230 @@
+"""``kernel_opt._C`` — the reference's pybind11 module, restated over the C ABI.
+
+Same three functions, same argument order and out-parameter convention as
+the reference's ``csrc/bindings.cpp:17-27``:
+
+* ``fused_logprob_entropy_naive(logits, targets, logprob, entropy, lse_out)``
+* ``fused_logprob_entropy_v1(logits, targets, logprob, entropy, lse_out)``
+* ``fused_logprob_entropy_v1_backward(logits, targets, lse, entropy,
+  g_logp, g_ent, g_lse, d_logits)``
+
+Tensor checks raise ``RuntimeError`` with the reference's ``TORCH_CHECK``
+messages (``csrc/fused_logprob.cu:294-311,362-374,412-424``).  Differences:
+
+* ``logits`` need not be contiguous: any tensor whose last dim has unit
+  stride and whose rows are reachable through at most two leading strides is
+  accepted (e.g. the shifted slice ``logits[:, :-1, :]``); anything else
+  still raises "logits must be contiguous".
+* In the backward, ``g_logp``/``g_ent``/``g_lse`` may be ``None`` (an all-zero
+  upstream gradient), so callers need not materialise zero tensors.
+* Work runs on the current stream of ``logits``' device, with that device
+  made current for the call.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import torch
+
+from ._library import DTYPE_CODES, check_status, lib
+
+__all__ = [
+    "fused_logprob_entropy_naive",
+    "fused_logprob_entropy_v1",
+    "fused_logprob_entropy_v1_backward",
+    "row_layout",
+    "fwd_launch",
+    "bwd_launch",
+    "default_config",
+]
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def row_layout(t: torch.Tensor):
+    """Return ``(rows_inner, stride_outer, stride_inner)`` addressing the rows
+    of ``t`` (see include/kernel_opt_hip.h), or ``None`` when the rows cannot
+    be reached with unit-stride rows and at most two leading strides."""
+    if t.dim() == 0:
+        return None
+    if t.size(-1) > 1 and t.stride(-1) != 1:
+        return None
+    dims = [(s, st) for s, st in zip(t.shape[:-1], t.stride()[:-1]) if s != 1]
+    merged: list[list[int]] = []
+    for size, stride in dims:
+        if merged and merged[-1][1] == stride * size:
+            merged[-1] = [merged[-1][0] * size, stride]
+        else:
+            merged.append([size, stride])
+    n_rows = 1
+    for s in t.shape[:-1]:
+        n_rows *= s
+    if not merged:
+        return (max(n_rows, 1), 0, 0)
+    if len(merged) == 1:
+        return (merged[0][0], 0, merged[0][1])
+    if len(merged) == 2:
+        return (merged[1][0], merged[0][1], merged[1][1])
+    return None
+
+
+# Split-row workspaces, one per (device, stream): zero-filled once, and left
+# zero-filled by every completed forward launch (include/kernel_opt_hip.h).
+_ws_lock = threading.Lock()
+_workspaces: dict = {}
+
+
+def _workspace(device: torch.device, stream: torch.cuda.Stream, nbytes: int):
+    if nbytes == 0:
+        return None
+    key = (device.index, stream.cuda_stream)
+    with _ws_lock:
+        buf = _workspaces.get(key)
+        if buf is None or buf.numel() < nbytes:
+            with torch.cuda.stream(stream):
+                buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+            _workspaces[key] = buf
+        return buf
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _common_forward_checks(logits, targets, logprob, entropy, lse_out, per_output: bool):
+    _require(logits.is_cuda, "logits must be CUDA")
+    _require(targets.is_cuda, "targets must be CUDA")
+    rows = row_layout(logits)
+    _require(rows is not None, "logits must be contiguous")
+    _require(targets.dtype == torch.int64, "targets must be int64")
+    if per_output:
+        _require(logprob.dtype == torch.float32, "logprob must be float32")
+        _require(entropy.dtype == torch.float32, "entropy must be float32")
+        _require(lse_out.dtype == torch.float32, "lse must be float32")
+    else:
+        _require(logprob.dtype == torch.float32 and entropy.dtype == torch.float32
+                 and lse_out.dtype == torch.float32, "outputs must be float32")
+    _require(logits.dtype in DTYPE_CODES, "logits dtype must be bf16, fp16, or fp32")
+    V = logits.size(-1)
+    _require(V > 0, "logits last dim (vocab) must be >= 1")
+    N = logits.numel() // V
+    _require(targets.numel() == N, "targets numel must match leading dims of logits")
+    _require(logprob.numel() == N and entropy.numel() == N and lse_out.numel() == N,
+             "output tensor numels must equal leading-dim count")
+    _require(targets.is_contiguous(), "targets must be contiguous")
+    _require(logprob.is_contiguous() and entropy.is_contiguous() and lse_out.is_contiguous(),
+             "outputs must be contiguous")
+    for t in (targets, logprob, entropy, lse_out):
+        _require(t.device == logits.device, "all tensors must be on the device of logits")
+    return rows, N, V
+
+
+def fwd_launch(logits, targets, logprob, entropy, lse_out, config=None) -> None:
+    """Forward into caller-allocated outputs.  ``config`` = ``(waves, unroll,
+    splits, nontemporal)`` pins a launch shape (tuning ABI); ``None`` lets the
+    native dispatcher choose."""
+    rows, N, V = _common_forward_checks(logits, targets, logprob, entropy, lse_out, False)
+    if N == 0:
+        return
+    code = DTYPE_CODES[logits.dtype]
+    dev = logits.device
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev)
+        if config is None:
+            nbytes = lib.klp_fwd_workspace_bytes(code, N, V)
+        else:
+            nbytes = lib.klp_fwd_workspace_bytes_ex(N, int(config[2]))
+        ws = _workspace(dev, stream, nbytes)
+        args = [_ptr(logits), code, N, V, rows[0], rows[1], rows[2], _ptr(targets),
+                _ptr(logprob), _ptr(entropy), _ptr(lse_out), _ptr(ws),
+                0 if ws is None else ws.numel()]
+        if config is None:
+            rc = lib.klp_fwd(*args, ctypes.c_void_p(stream.cuda_stream))
+        else:
+            w, u, s, nt = (int(c) for c in config)
+            rc = lib.klp_fwd_ex(*args, w, u, s, nt, ctypes.c_void_p(stream.cuda_stream))
+    check_status(rc)
+
+
+def fused_logprob_entropy_v1(logits, targets, logprob, entropy, lse_out) -> None:
+    """Production forward (reference csrc/fused_logprob.cu:355-403)."""
+    fwd_launch(logits, targets, logprob, entropy, lse_out)
+
+
+def fused_logprob_entropy_naive(logits, targets, logprob, entropy, lse_out) -> None:
+    """Naive forward, one thread per row (reference csrc/fused_logprob.cu:405-458)."""
+    rows, N, V = _common_forward_checks(logits, targets, logprob, entropy, lse_out, True)
+    if N == 0:
+        return
+    dev = logits.device
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev)
+        rc = lib.klp_fwd_naive(_ptr(logits), DTYPE_CODES[logits.dtype], N, V, rows[0], rows[1],
+                               rows[2], _ptr(targets), _ptr(logprob), _ptr(entropy),
+                               _ptr(lse_out), ctypes.c_void_p(stream.cuda_stream))
+    check_status(rc)
+
+
+def _backward_checks(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits):
+    _require(logits.is_cuda, "logits must be contiguous CUDA")
+    rows = row_layout(logits)
+    _require(rows is not None, "logits must be contiguous CUDA")
+    _require(targets.dtype == torch.int64, "targets must be int64")
+    _require(lse.dtype == torch.float32 and entropy.dtype == torch.float32,
+             "saved lse / entropy must be fp32")
+    grads = [g for g in (g_logp, g_ent, g_lse) if g is not None]
+    _require(all(g.dtype == torch.float32 for g in grads), "upstream gradients must be fp32")
+    _require(all(g.is_contiguous() for g in grads), "upstream gradients must be contiguous")
+    _require(d_logits.dtype == logits.dtype and d_logits.is_contiguous()
+             and d_logits.shape == logits.shape,
+             "d_logits must match logits dtype/shape and be contiguous")
+    _require(logits.dtype in DTYPE_CODES, "logits dtype must be bf16, fp16, or fp32")
+    V = logits.size(-1)
+    _require(V > 0, "logits last dim (vocab) must be >= 1")
+    N = logits.numel() // V
+    _require(targets.numel() == N and lse.numel() == N and entropy.numel() == N
+             and all(g.numel() == N for g in grads), "leading-dim count mismatch")
+    _require(targets.is_contiguous() and lse.is_contiguous() and entropy.is_contiguous(),
+             "targets / saved lse / entropy must be contiguous")
+    for t in [targets, lse, entropy, d_logits] + grads:
+        _require(t.device == logits.device, "all tensors must be on the device of logits")
+    return rows, N, V
+
+
+def bwd_launch(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits,
+               config=None) -> None:
+    """Backward into caller-allocated ``d_logits``; ``config`` as in fwd_launch."""
+    rows, N, V = _backward_checks(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits)
+    if N == 0:
+        return
+    dev = logits.device
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev)
+        args = [_ptr(logits), DTYPE_CODES[logits.dtype], N, V, rows[0], rows[1], rows[2],
+                _ptr(targets), _ptr(lse), _ptr(entropy), _ptr(g_logp), _ptr(g_ent),
+                _ptr(g_lse), _ptr(d_logits)]
+        if config is None:
+            rc = lib.klp_bwd(*args, ctypes.c_void_p(stream.cuda_stream))
+        else:
+            w, u, s, nt = (int(c) for c in config)
+            rc = lib.klp_bwd_ex(*args, w, u, s, nt, ctypes.c_void_p(stream.cuda_stream))
+    check_status(rc)
+
+
+def fused_logprob_entropy_v1_backward(logits, targets, lse, entropy, g_logp, g_ent, g_lse,
+                                      d_logits) -> None:
+    """Backward (reference csrc/fused_logprob.cu:284-346)."""
+    bwd_launch(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits)
+
+
+def default_config(which: str, dtype: torch.dtype, n_rows: int, vocab: int):
+    """Launch shape ``(waves, unroll, splits, nontemporal)`` the native
+    dispatcher picks for the forward (``which="fwd"``) or backward."""
+    out = [ctypes.c_int(0) for _ in range(4)]
+    lib.klp_default_config(0 if which == "fwd" else 1, DTYPE_CODES[dtype], n_rows, vocab,
+                           *[ctypes.byref(o) for o in out])
+    return tuple(o.value for o in out)

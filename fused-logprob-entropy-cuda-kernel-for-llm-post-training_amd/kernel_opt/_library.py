@@ -1,0 +1,84 @@
+"""Loader for the HIP shared library ``_lib/libkernel_opt_hip.so``.
+
+The library is built in-tree by ``__graft_entry__.build()`` (hipcc,
+``--offload-arch=gfx950``).  There is no fallback: if the library is missing
+or does not load, importing :mod:`kernel_opt` raises ``ImportError``.
+
+``torch`` is imported first so that the library's ``libamdhip64.so.7``
+dependency resolves (by soname) to the HIP runtime torch already loaded; the
+process then holds a single HIP runtime.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the dlopen below, see module docstring)
+
+LIB_NAME = "libkernel_opt_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", LIB_NAME)
+ABI_VERSION = 1
+
+# klp_dtype values (include/kernel_opt_hip.h)
+KLP_BF16, KLP_FP16, KLP_FP32 = 0, 1, 2
+DTYPE_CODES = {torch.bfloat16: KLP_BF16, torch.float16: KLP_FP16, torch.float32: KLP_FP32}
+
+# klp_status values
+KLP_OK, KLP_EINVAL, KLP_EDTYPE, KLP_ELAUNCH, KLP_EWORKSPACE = 0, 1, 2, 3, 4
+
+# Every symbol the public headers declare, with its ctypes signature.
+_vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+_ROWS = [_vp, _i32, _i64, _i64, _i64, _i64, _i64]  # logits, dtype, N, V, rows_inner, s_outer, s_inner
+SIGNATURES = {
+    # include/kernel_opt_hip.h
+    "klp_abi_version": (_i32, []),
+    "klp_last_error": (_sz, [ctypes.c_char_p, _sz]),
+    "klp_fwd_workspace_bytes": (_sz, [_i32, _i64, _i64]),
+    "klp_fwd": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "klp_fwd_naive": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp]),
+    "klp_bwd": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "klp_debug_fail_next_launches": (None, [_i32]),
+    # include/kernel_opt_hip_tuning.h
+    "klp_fwd_workspace_bytes_ex": (_sz, [_i64, _i32]),
+    "klp_fwd_ex": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _sz, _i32, _i32, _i32, _i32, _vp]),
+    "klp_bwd_ex": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
+                                  _vp]),
+    "klp_default_config": (None, [_i32, _i32, _i64, _i64] + [ctypes.POINTER(_i32)] * 4),
+}
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"kernel_opt: {LIB_PATH} is not built. Build it with "
+            "`python -c 'import __graft_entry__ as g; g.build()'` from the repository root.")
+    try:
+        lib = ctypes.CDLL(LIB_PATH)
+    except OSError as e:  # pragma: no cover - depends on the machine
+        raise ImportError(f"kernel_opt: cannot load {LIB_PATH}: {e}") from e
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = lib.klp_abi_version()
+    if version != ABI_VERSION:
+        raise ImportError(f"kernel_opt: {LIB_NAME} has ABI version {version}, "
+                          f"expected {ABI_VERSION}; rebuild it")
+    return lib
+
+
+lib = _load()
+
+
+def last_error() -> str:
+    n = lib.klp_last_error(None, 0)
+    buf = ctypes.create_string_buffer(n + 1)
+    lib.klp_last_error(buf, n + 1)
+    return buf.value.decode("utf-8", "replace")
+
+
+def check_status(rc: int) -> None:
+    """Raise RuntimeError carrying the native message for a non-zero status
+    (the reference raises RuntimeError from TORCH_CHECK)."""
+    if rc != KLP_OK:
+        raise RuntimeError(last_error() or f"kernel_opt: native call failed with status {rc}")

@@ -1,0 +1,142 @@
+/*
+ * kernel_opt_hip.h — C ABI of the MI355X (gfx950) fused per-token
+ * log-probability + entropy library (libkernel_opt_hip.so).
+ *
+ * This ABI replaces the pybind11 module `kernel_opt._C` of the reference
+ * (csrc/bindings.cpp:17-27).  The three compute entry points correspond
+ * one-to-one to the three functions that module exposes; argument meaning
+ * and the out-parameter convention are the same, but tensors are passed as
+ * raw device pointers plus sizes and strides, so no torch type crosses the
+ * boundary.
+ *
+ * Conventions shared by every entry point
+ * ---------------------------------------
+ *  - `dtype` is a klp_dtype value and describes `logits` (and `d_logits`).
+ *  - `n_rows` = N = product of the leading dims, `vocab` = V (last dim).
+ *  - Row r of `logits` starts at element offset
+ *        (r / rows_inner) * stride_outer + (r % rows_inner) * stride_inner
+ *    from `logits`; elements inside a row are contiguous (unit stride).
+ *    A contiguous [N, V] tensor is (rows_inner = N, stride_outer = 0,
+ *    stride_inner = V).  The non-contiguous slice logits[:, :-1, :] of a
+ *    [B, L, V] tensor is (rows_inner = L - 1, stride_outer = L * V,
+ *    stride_inner = V).  Strides are in elements.
+ *  - `targets` is int64 [N], contiguous.  A target outside [0, V) (for
+ *    example an ignore index of -100) yields logprob = -lse and no one-hot
+ *    term in the gradient, exactly as the reference kernels do.
+ *  - Per-row outputs and saved/upstream tensors are float32 [N], contiguous.
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = the legacy default
+ *    stream).  No entry point synchronises, allocates or frees device
+ *    memory.  N = 0 is a no-op that returns KLP_OK.
+ *  - Every entry point returns a klp_status.  On failure a thread-local
+ *    message is available from klp_last_error().
+ */
+#ifndef KERNEL_OPT_HIP_H
+#define KERNEL_OPT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KLP_ABI_VERSION 1
+
+typedef enum klp_dtype {
+    KLP_BF16 = 0,
+    KLP_FP16 = 1,
+    KLP_FP32 = 2
+} klp_dtype;
+
+typedef enum klp_status {
+    KLP_OK = 0,
+    KLP_EINVAL = 1,       /* bad argument: null pointer, size, stride, alignment */
+    KLP_EDTYPE = 2,       /* unsupported dtype */
+    KLP_ELAUNCH = 3,      /* hipGetLastError() reported a failure after launch */
+    KLP_EWORKSPACE = 4    /* workspace given but too small / misaligned */
+} klp_status;
+
+/* Version of this ABI (KLP_ABI_VERSION). */
+int klp_abi_version(void);
+
+/*
+ * Copies the calling thread's last error message (NUL-terminated, truncated
+ * to `len`) into `buf`.  Returns the full message length.
+ */
+size_t klp_last_error(char* buf, size_t len);
+
+/*
+ * Bytes of device workspace that klp_fwd can use to split each row across
+ * several workgroups (split-row mode) for this problem size.  0 means the
+ * dispatcher keeps one workgroup per row.  The workspace must be zero-filled
+ * once before its first use; klp_fwd leaves it zero-filled again after every
+ * launch that completes.  Launches that share one workspace must be ordered
+ * (same stream, or synchronised).
+ */
+size_t klp_fwd_workspace_bytes(int dtype, int64_t n_rows, int64_t vocab);
+
+/*
+ * Forward: logprob[r] = logits[r, t_r] - lse[r], entropy[r] = -sum_v p log p,
+ * lse[r] = logsumexp(logits[r]).  One streaming pass over each row.
+ *
+ * Replaces kernel_opt::fused_logprob_entropy_v1
+ * (reference csrc/fused_logprob.cu:355-403, bound at csrc/bindings.cpp:21-23).
+ *
+ * `workspace` may be NULL (then one workgroup per row).  When it is not
+ * NULL it must hold klp_fwd_workspace_bytes() bytes, be 16-byte aligned and
+ * follow the zero-fill rule above.
+ */
+int klp_fwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+            int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+            const int64_t* targets,
+            float* logprob, float* entropy, float* lse,
+            void* workspace, size_t workspace_bytes,
+            void* stream);
+
+/*
+ * Naive forward: one thread per row, scalar recurrence.  Correctness anchor,
+ * never fast.  Same outputs as klp_fwd up to fp32 rounding, except that, like
+ * the reference naive kernel, a -inf logit after the first element of a row
+ * makes that row's entropy NaN.
+ *
+ * Replaces kernel_opt::fused_logprob_entropy_naive
+ * (reference csrc/fused_logprob.cu:405-458, bound at csrc/bindings.cpp:18-20).
+ */
+int klp_fwd_naive(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                  int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                  const int64_t* targets,
+                  float* logprob, float* entropy, float* lse,
+                  void* stream);
+
+/*
+ * Backward: d_logits[r, v] = p_v * (g_lse - g_logp - g_ent * (log p_v + H))
+ *                            + (v == t_r ? g_logp : 0),
+ * p_v = exp(logits[r, v] - lse[r]), recomputed from the saved lse in one
+ * read + one write pass.  `g_logp`, `g_ent` and `g_lse` may each be NULL,
+ * meaning an all-zero upstream gradient (autograd's None).  `d_logits` is a
+ * dense row-major [N, V] array of `dtype`, written with round-to-nearest-even.
+ *
+ * Replaces kernel_opt::fused_logprob_entropy_v1_backward
+ * (reference csrc/fused_logprob.cu:284-346, bound at csrc/bindings.cpp:24-26).
+ */
+int klp_bwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+            int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+            const int64_t* targets,
+            const float* lse, const float* entropy,
+            const float* g_logp, const float* g_ent, const float* g_lse,
+            void* d_logits,
+            void* stream);
+
+/*
+ * Test hook with no counterpart in the reference: the next `count` compute
+ * calls on the calling thread return KLP_ELAUNCH without launching anything,
+ * as if hipGetLastError() had reported a failure.  Lets the error path be
+ * tested on machines without a GPU.  count = 0 disarms it.
+ */
+void klp_debug_fail_next_launches(int count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KERNEL_OPT_HIP_H */

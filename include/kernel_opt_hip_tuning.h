@@ -1,0 +1,56 @@
+/*
+ * kernel_opt_hip_tuning.h — launch-shape control for libkernel_opt_hip.so.
+ *
+ * None of these entry points has a counterpart in the reference (whose
+ * launch shape is fixed: one 256-thread block per row,
+ * csrc/fused_logprob.cu:313,376).  They exist for benchmarks, sweeps and
+ * tests that must pin a launch shape (for example to exercise split-row mode
+ * at a size where the default dispatcher would not choose it).  Results do
+ * not depend on the launch shape beyond fp32 rounding of the reduction order.
+ *
+ * Conventions are those of kernel_opt_hip.h.  Supported shapes:
+ * waves in {4, 8} (wave64s per workgroup), unroll in {2, 4} (16-byte loads per
+ * thread per iteration), splits in [1, 1024] (workgroups per row),
+ * nontemporal in {0, 1}.
+ */
+#ifndef KERNEL_OPT_HIP_TUNING_H
+#define KERNEL_OPT_HIP_TUNING_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Workspace bytes klp_fwd_ex needs for `splits` workgroups per row. */
+size_t klp_fwd_workspace_bytes_ex(int64_t n_rows, int splits);
+
+/* klp_fwd with an explicit launch shape.  splits > 1 needs a workspace. */
+int klp_fwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+               int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+               const int64_t* targets,
+               float* logprob, float* entropy, float* lse,
+               void* workspace, size_t workspace_bytes,
+               int waves, int unroll, int splits, int nontemporal,
+               void* stream);
+
+/* klp_bwd with an explicit launch shape (splits need no workspace). */
+int klp_bwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+               int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+               const int64_t* targets,
+               const float* lse, const float* entropy,
+               const float* g_logp, const float* g_ent, const float* g_lse,
+               void* d_logits,
+               int waves, int unroll, int splits, int nontemporal,
+               void* stream);
+
+/* The launch shape klp_fwd (which = 0) or klp_bwd (which = 1) would pick. */
+void klp_default_config(int which, int dtype, int64_t n_rows, int64_t vocab,
+                        int* waves, int* unroll, int* splits, int* nontemporal);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KERNEL_OPT_HIP_TUNING_H */

@@ -1,0 +1,182 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol the public
+headers declare, and rejects bad arguments with the documented status and
+message before touching the GPU.  No compute call is made."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("kernel_opt_hip.h", "kernel_opt_hip_tuning.h")]
+
+
+def _declared_functions():
+    names = []
+    for h in HEADERS:
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b(klp_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    from kernel_opt import _library
+    declared = _declared_functions()
+    assert len(declared) >= 10
+    lib = ctypes.CDLL(_library.LIB_PATH)
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    # and the Python loader binds exactly these
+    assert sorted(_library.SIGNATURES) == declared
+
+
+def test_abi_version():
+    from kernel_opt import _library
+    assert _library.lib.klp_abi_version() == _library.ABI_VERSION == 1
+
+
+# Fake, suitably aligned addresses: every call below must fail validation (or
+# hit the injected failure) before any pointer is dereferenced or any HIP call
+# is made.
+P = ctypes.c_void_p(0x10000)
+
+
+def _fwd(lib, dtype=0, n=4, v=100, rows_inner=4, so=0, si=100, logits=P, targets=P, outs=(P, P, P),
+         ws=None, ws_bytes=0):
+    return lib.klp_fwd(logits, dtype, n, v, rows_inner, so, si, targets, *outs, ws, ws_bytes, None)
+
+
+def _err():
+    from kernel_opt import _library
+    return _library.last_error()
+
+
+def test_validation_errors():
+    from kernel_opt._library import KLP_EDTYPE, KLP_EINVAL, KLP_OK, lib
+    assert _fwd(lib, dtype=7) == KLP_EDTYPE
+    assert _err() == "logits dtype must be bf16, fp16, or fp32"
+    assert _fwd(lib, v=0) == KLP_EINVAL and "vocab" in _err()
+    assert _fwd(lib, n=-1) == KLP_EINVAL
+    assert _fwd(lib, logits=None) == KLP_EINVAL and "non-null" in _err()
+    assert _fwd(lib, logits=ctypes.c_void_p(0x10001)) == KLP_EINVAL and "aligned" in _err()
+    assert _fwd(lib, targets=ctypes.c_void_p(0x10004)) == KLP_EINVAL and "targets" in _err()
+    assert _fwd(lib, rows_inner=0) == KLP_EINVAL
+    assert _fwd(lib, si=-5) == KLP_EINVAL
+    assert _fwd(lib, outs=(P, None, P)) == KLP_EINVAL and "entropy" in _err()
+    # N = 0 is a no-op: succeeds even with null pointers
+    assert _fwd(lib, n=0, logits=None, targets=None, outs=(None, None, None)) == KLP_OK
+    assert _err() == ""
+
+
+def test_workspace_and_launch_shape_errors():
+    from kernel_opt._library import KLP_EINVAL, KLP_EWORKSPACE, lib
+    need = lib.klp_fwd_workspace_bytes_ex(4, 8)
+    assert need > 0
+    rc = lib.klp_fwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, P, P, need - 16, 8, 4, 8, 1, None)
+    assert rc == KLP_EWORKSPACE and "workspace" in _err()
+    rc = lib.klp_fwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, P, ctypes.c_void_p(0x10008), need,
+                        8, 4, 8, 1, None)
+    assert rc == KLP_EWORKSPACE  # misaligned workspace
+    rc = lib.klp_fwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, P, None, 0, 5, 4, 1, 1, None)
+    assert rc == KLP_EINVAL and "launch shape" in _err()
+    rc = lib.klp_bwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, None, None, None, P, 8, 3, 1, 1, None)
+    assert rc == KLP_EINVAL and "launch shape" in _err()
+    rc = lib.klp_bwd(P, 0, 4, 100, 4, 0, 100, P, P, P, None, None, None, None, None)
+    assert rc == KLP_EINVAL and "d_logits" in _err()
+
+
+def test_injected_launch_failure_reports_elaunch():
+    from kernel_opt._library import KLP_ELAUNCH, lib
+    lib.klp_debug_fail_next_launches(2)
+    try:
+        assert _fwd(lib) == KLP_ELAUNCH
+        assert "launch failed" in _err() and "injected" in _err()
+        rc = lib.klp_bwd(P, 0, 4, 100, 4, 0, 100, P, P, P, None, None, None, P, None)
+        assert rc == KLP_ELAUNCH
+    finally:
+        lib.klp_debug_fail_next_launches(0)
+
+
+def test_last_error_truncates():
+    from kernel_opt._library import lib
+    _fwd(lib, dtype=9)
+    n = lib.klp_last_error(None, 0)
+    buf = ctypes.create_string_buffer(8)
+    assert lib.klp_last_error(buf, 8) == n
+    assert buf.value == b"logits "
+
+
+def test_default_launch_shapes():
+    from kernel_opt import _C
+    # headline config: split rows so that 1024 rows fill 256 CUs
+    w, u, s, nt = _C.default_config("fwd", torch.bfloat16, 1024, 152064)
+    assert s >= 2 and w in (4, 8) and u in (2, 4)
+    # tiny vocab: never split
+    assert _C.default_config("fwd", torch.float32, 4, 64)[2] == 1
+    # many rows: one workgroup per row
+    assert _C.default_config("fwd", torch.bfloat16, 32768, 151936)[2] == 1
+    from kernel_opt._library import lib
+    assert lib.klp_fwd_workspace_bytes(0, 32768, 151936) == 0
+    assert lib.klp_fwd_workspace_bytes(0, 1024, 152064) > 0
+
+
+def test_shim_rejects_cpu_tensors_with_reference_messages():
+    from kernel_opt import _C
+    x = torch.zeros(2, 8)
+    t = torch.zeros(2, dtype=torch.int64)
+    o = [torch.zeros(2) for _ in range(3)]
+    with pytest.raises(RuntimeError, match="logits must be CUDA"):
+        _C.fused_logprob_entropy_v1(x, t, *o)
+    with pytest.raises(RuntimeError, match="logits must be CUDA"):
+        _C.fused_logprob_entropy_naive(x, t, *o)
+    with pytest.raises(RuntimeError, match="logits must be contiguous CUDA"):
+        _C.fused_logprob_entropy_v1_backward(x, t, o[0], o[1], None, None, None, x)
+
+
+def test_ops_assert_on_cpu_tensors():
+    import kernel_opt
+    x = torch.zeros(2, 8)
+    t = torch.zeros(2, dtype=torch.int64)
+    for f in (kernel_opt.fused_logprob_entropy, kernel_opt.fused_logprob_entropy_forward,
+              kernel_opt.fused_logprob_entropy_naive):
+        with pytest.raises(AssertionError):
+            f(x, t)
+
+
+def test_row_layout():
+    from kernel_opt._C import row_layout
+    x = torch.zeros(4, 6, 10)
+    assert row_layout(x) == (24, 0, 10)
+    assert row_layout(x[:, :-1, :]) == (5, 60, 10)
+    assert row_layout(x[:, 1:, :]) == (5, 60, 10)
+    assert row_layout(x[1]) == (6, 0, 10)
+    assert row_layout(x[:2, :3]) == (3, 60, 10)
+    assert row_layout(x[:, :, :5]) == (24, 0, 10)   # narrowed rows keep unit stride
+    assert row_layout(x[:, ::2, :]) == (12, 0, 20)   # (b, s) -> (3b + s) * 20
+    assert row_layout(x.transpose(0, 1)) == (4, 10, 60)
+    assert row_layout(x[::2, ::2, :]) == (3, 120, 20)
+    assert row_layout(x[:, :, ::2]) is None          # non-unit element stride
+    assert row_layout(torch.zeros(2, 3, 4, 5)[:, :, :-1]) == (3, 20, 5)
+    assert row_layout(torch.zeros(2, 3, 4, 5)[:, :-1, :-1]) is None  # three strides
+    assert row_layout(torch.zeros(1, 1, 7)) == (1, 0, 0)
+    assert row_layout(torch.zeros(7)) == (1, 0, 0)
+    assert row_layout(torch.zeros(())) is None
+
+
+def test_package_surface_matches_reference():
+    """reference python/kernel_opt/__init__.py:1-15."""
+    import kernel_opt
+    for name in ("fused_logprob_entropy", "fused_logprob_entropy_forward",
+                 "fused_logprob_entropy_naive", "_C", "__version__"):
+        assert hasattr(kernel_opt, name)
+    assert kernel_opt.__version__ == "0.0.1"
+    for name in ("fused_logprob_entropy_naive", "fused_logprob_entropy_v1",
+                 "fused_logprob_entropy_v1_backward"):
+        assert callable(getattr(kernel_opt._C, name))
+    with pytest.raises(AttributeError):
+        kernel_opt.does_not_exist  # noqa: B018

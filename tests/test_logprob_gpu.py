@@ -1,0 +1,466 @@
+"""GPU parity tests of the fused kernels against the float64 oracle and the
+reference's fp32 eager path.
+
+Mirrors the reference's tests/test_logprob.py (each test names the one it
+follows) and adds the north-star bars:
+  * forward: |ours - oracle| <= 1e-5 (fp32 input) / 2e-5 (bf16, fp16 input);
+  * backward: bf16/fp16 gradients within 1 ulp of the float64 oracle rounded
+    to nearest-even; fp32 gradients within 1 ulp of the row's largest
+    gradient magnitude (elementwise 1 ulp is below what an fp32 lse allows,
+    since lse itself carries half an ulp of rounding that enters every
+    exp(x - lse)).
+All inputs are generated on the CPU from fixed seeds and copied to the GPU.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from klp_testutil import (DTYPE_NAME, FWD_TOL, WIDTH, bits_of, seeded_logits, seeded_targets,
+                          storage_bits, ulp_diff)
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+DEV = "cuda"
+
+
+def _ko():
+    import kernel_opt
+    return kernel_opt
+
+
+def _eager():
+    from oracle import eager_ref
+    return eager_ref
+
+
+def _check_fwd(oracle, x_cpu, t_cpu, outs, tol, label=""):
+    ref = oracle.forward(x_cpu, t_cpu.numpy())
+    for name, ours, r in zip(("logp", "entropy", "lse"), outs, ref):
+        o = ours.detach().cpu().double().numpy().reshape(r.shape)
+        err = np.abs(o - r).max() if o.size else 0.0
+        assert err <= tol, f"{label} {name}: max abs err vs oracle {err:.3g} > {tol}"
+
+
+def _grad_ulps(oracle, x_cpu, t_cpu, lse, ent, d_ours, g_logp=None, g_ent=None, g_lse=None):
+    """Max ulp distance of the kernel's gradient to the oracle's (see module
+    docstring for the fp32 row-scale rule).  Returns (max_ulp, detail)."""
+    d_ref = oracle.backward(x_cpu, t_cpu.numpy(), lse.cpu().numpy(), ent.cpu().numpy(),
+                            g_logp=None if g_logp is None else g_logp.cpu().numpy(),
+                            g_ent=None if g_ent is None else g_ent.cpu().numpy(),
+                            g_lse=None if g_lse is None else g_lse.cpu().numpy())
+    dt = d_ours.dtype
+    if dt == torch.float32:
+        V = x_cpu.shape[-1]
+        d = d_ours.detach().cpu().double().numpy().reshape(-1, V)
+        r = d_ref.reshape(-1, V)
+        row_max = np.abs(r).max(axis=1, keepdims=True)
+        scale = np.where(row_max > 0, 2.0 ** (np.floor(np.log2(np.maximum(row_max, 1e-300))) - 23),
+                         2.0 ** -149)
+        return float((np.abs(d - r) / scale).max()), "row-scale ulps"
+    ref_bits = bits_of(oracle.round_to(d_ref, DTYPE_NAME[dt]))
+    return float(ulp_diff(storage_bits(d_ours), ref_bits, WIDTH[dt]).max()), "elementwise ulps"
+
+
+# ---------------------------------------------------------------------------
+# Forward — reference tests/test_logprob.py:28-54 (naive) and :114-137 (v1)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(2, 16, 4096), (1, 1, 32000), (3, 8, 8192)])
+def test_naive_matches_fp32_reference(dtype, shape, oracle):
+    B, S, V = shape
+    x = seeded_logits(shape, dtype, seed=0)
+    t = seeded_targets((B, S), V, seed=0)
+    out = _ko().fused_logprob_entropy_naive(x.to(DEV), t.to(DEV))
+    ref = _eager().ref_fp32(x.to(DEV), t.to(DEV))
+    atol = 1e-4 if dtype == torch.float32 else 5e-3  # reference :44-47
+    for o, r in zip(out, ref):
+        assert torch.allclose(o, r, atol=atol, rtol=atol)
+    _check_fwd(oracle, x, t, out, tol=1e-4, label="naive")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(2, 16, 4096), (1, 1, 32000), (3, 8, 8192), (4, 64, 128256)])
+def test_v1_matches_fp32_reference(dtype, shape, oracle):
+    B, S, V = shape
+    x = seeded_logits(shape, dtype, seed=2)
+    t = seeded_targets((B, S), V, seed=2)
+    out = _ko().fused_logprob_entropy(x.to(DEV), t.to(DEV))
+    _check_fwd(oracle, x, t, out, tol=FWD_TOL[dtype], label=f"v1 {shape} {dtype}")
+    # against the reference's own fp32 eager path (its ground truth)
+    ref = _eager().ref_fp32(x.to(DEV), t.to(DEV))
+    for name, o, r in zip(("logp", "entropy", "lse"), out, ref):
+        err = (o - r).abs().max().item()
+        assert err <= FWD_TOL[dtype], f"{name} vs fp32 eager path: {err:.3g}"
+
+
+def test_at_least_as_accurate_as_trl_bf16():
+    """reference :57-98, against this repo's restatement of TRL's eager path."""
+    B, S, V = 2, 32, 8192
+    x = seeded_logits((B, S, V), torch.bfloat16, seed=1, scale=1.0).to(DEV)
+    t = seeded_targets((B, S), V, seed=1).to(DEV)
+    e = _eager()
+    logp, ent, _ = _ko().fused_logprob_entropy_naive(x, t)
+    trl_logp = e.trl_selective_log_softmax(x, t).float()
+    trl_ent = e.trl_entropy_from_logits(x).float()
+    gt_logp, gt_ent, _ = e.ref_fp32(x, t)
+    ours_logp_err = (logp - gt_logp).abs().max().item()
+    trl_logp_err = (trl_logp - gt_logp).abs().max().item()
+    ours_ent_err = (ent - gt_ent).abs().max().item()
+    trl_ent_err = (trl_ent - gt_ent).abs().max().item()
+    assert ours_logp_err <= trl_logp_err * 1.2 + 1e-4
+    assert ours_ent_err <= trl_ent_err * 1.2 + 1e-4
+    assert ours_ent_err < trl_ent_err
+    # and the production kernel too
+    logp1, ent1, _ = _ko().fused_logprob_entropy(x, t)
+    assert (ent1 - gt_ent).abs().max().item() < trl_ent_err
+
+
+@pytest.mark.parametrize("fn", ["naive", "v1"])
+def test_extreme_values_no_overflow(fn, oracle):
+    """reference :101-111 (+60 shift stays finite) — and stays accurate."""
+    B, S, V = 1, 4, 1024
+    x = (seeded_logits((B, S, V), torch.float32, seed=3, scale=1.0) + 60.0)
+    t = seeded_targets((B, S), V, seed=3)
+    f = _ko().fused_logprob_entropy_naive if fn == "naive" else _ko().fused_logprob_entropy
+    out = f(x.to(DEV), t.to(DEV))
+    for o in out:
+        assert torch.isfinite(o).all()
+    _check_fwd(oracle, x, t, out, tol=1e-4 if fn == "naive" else 1e-5, label=fn)
+
+
+@pytest.mark.parametrize("fn", ["naive", "v1"])
+@pytest.mark.parametrize("V", [4096, 152064, 7])
+def test_uniform_logits_entropy_equals_logV(fn, V):
+    """reference :140-152: zeros -> entropy = lse = log V, logp = -log V."""
+    x = torch.zeros(1, 3, V, device=DEV)
+    t = torch.zeros(1, 3, dtype=torch.int64, device=DEV)
+    f = _ko().fused_logprob_entropy_naive if fn == "naive" else _ko().fused_logprob_entropy
+    logp, ent, lse = f(x, t)
+    lv = math.log(V)
+    tol = 1e-4 if fn == "naive" else 1e-5
+    assert (ent - lv).abs().max().item() <= tol
+    assert (lse - lv).abs().max().item() <= tol
+    assert (logp + lv).abs().max().item() <= tol
+
+
+# ---------------------------------------------------------------------------
+# Backward — reference tests/test_logprob.py:170-252
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(2, 4, 256), (1, 8, 4096), (3, 16, 8192)])
+def test_backward_matches_pytorch_autograd(dtype, shape):
+    """reference :170-206: autograd of the eager formulas in the input dtype."""
+    B, S, V = shape
+    base = seeded_logits(shape, dtype, seed=7, scale=1.0).to(DEV)
+    t = seeded_targets((B, S), V, seed=7).to(DEV)
+    g = torch.Generator().manual_seed(77)
+    gl, ge, gs = [(torch.randn(B, S, generator=g) * 0.5).to(DEV) for _ in range(3)]
+    x_ref = base.clone().requires_grad_(True)
+    lp, h, l = _eager().ref_forward_pt(x_ref, t)
+    (lp * gl + h * ge + l * gs).sum().backward()
+    x = base.clone().requires_grad_(True)
+    lp2, h2, l2 = _ko().fused_logprob_entropy(x, t)
+    (lp2 * gl + h2 * ge + l2 * gs).sum().backward()
+    assert x.grad.dtype == dtype
+    atol = 1e-4 if dtype == torch.float32 else 1e-2
+    assert torch.allclose(x.grad.float(), x_ref.grad.float(), atol=atol, rtol=atol)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(2, 4, 256), (1, 8, 4096), (3, 16, 8192), (2, 8, 50257)])
+def test_backward_within_one_ulp_of_oracle(dtype, shape, oracle):
+    B, S, V = shape
+    x_cpu = seeded_logits(shape, dtype, seed=11)
+    t_cpu = seeded_targets((B, S), V, seed=11)
+    g = torch.Generator().manual_seed(111)
+    gl, ge, gs = [torch.randn(B, S, generator=g) * 0.5 for _ in range(3)]
+    x = x_cpu.to(DEV).requires_grad_(True)
+    lp, h, l = _ko().fused_logprob_entropy(x, t_cpu.to(DEV))
+    (lp * gl.to(DEV) + h * ge.to(DEV) + l * gs.to(DEV)).sum().backward()
+    ulps, kind = _grad_ulps(oracle, x_cpu, t_cpu, l.detach(), h.detach(), x.grad, gl, ge, gs)
+    assert ulps <= 1.0, f"{kind}: {ulps}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_backward_within_one_ulp_of_fp32_eager_path(dtype):
+    """North-star bar against the reference's fp32 path itself: autograd of
+    the fp32 formulas on the upcast logits, rounded to the output dtype."""
+    B, S, V = 2, 16, 32000
+    x_cpu = seeded_logits((B, S, V), dtype, seed=12)
+    t = seeded_targets((B, S), V, seed=12).to(DEV)
+    g = torch.Generator().manual_seed(121)
+    gl, ge = [(torch.randn(B, S, generator=g) * 0.5).to(DEV) for _ in range(2)]
+    xf = x_cpu.to(DEV).float().requires_grad_(True)
+    lp, h, _ = _eager().ref_fp32(xf, t)
+    (lp * gl + h * ge).sum().backward()
+    ref = xf.grad.to(dtype)
+    x = x_cpu.to(DEV).requires_grad_(True)
+    lp2, h2, _ = _ko().fused_logprob_entropy(x, t)
+    (lp2 * gl + h2 * ge).sum().backward()
+    d = ulp_diff(storage_bits(x.grad), storage_bits(ref), 16).max()
+    assert d <= 1, f"{d} ulp from the fp32 eager path"
+
+
+def test_backward_only_logprob_grad(oracle):
+    """reference :209-231: entropy and lse unused downstream (None grads)."""
+    B, S, V = 2, 8, 4096
+    x_cpu = seeded_logits((B, S, V), torch.float32, seed=8, scale=1.0)
+    t_cpu = seeded_targets((B, S), V, seed=8)
+    gl = torch.randn(B, S, generator=torch.Generator().manual_seed(88))
+    x_ref = x_cpu.to(DEV).requires_grad_(True)
+    lp_r, _, _ = _eager().ref_forward_pt(x_ref, t_cpu.to(DEV))
+    (lp_r * gl.to(DEV)).sum().backward()
+    x = x_cpu.to(DEV).requires_grad_(True)
+    lp, h, l = _ko().fused_logprob_entropy(x, t_cpu.to(DEV))
+    (lp * gl.to(DEV)).sum().backward()
+    assert torch.allclose(x.grad, x_ref.grad, atol=1e-4, rtol=1e-4)
+    ulps, kind = _grad_ulps(oracle, x_cpu, t_cpu, l.detach(), h.detach(), x.grad, g_logp=gl)
+    assert ulps <= 1.0, f"{kind}: {ulps}"
+
+
+def test_gradcheck_small():
+    """reference :234-252."""
+    B, S, V = 1, 2, 64
+    t = seeded_targets((B, S), V, seed=9).to(DEV)
+
+    def fn(x_double):
+        logp, ent, lse = _ko().fused_logprob_entropy(x_double.float(), t)
+        return logp.double(), ent.double(), lse.double()
+
+    g = torch.Generator().manual_seed(99)
+    x = torch.randn(B, S, V, generator=g, dtype=torch.float64).to(DEV).requires_grad_(True)
+    assert torch.autograd.gradcheck(fn, (x,), eps=1e-3, atol=1e-2, rtol=1e-2, nondet_tol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# Launch shapes, layouts and edge cases
+# ---------------------------------------------------------------------------
+LAUNCHES = [(w, u, s, nt) for w in (4, 8) for u in (2, 4) for s in (1, 2, 3, 8) for nt in (0, 1)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_every_launch_shape_matches_oracle(dtype, oracle):
+    from kernel_opt import _C
+    N, V = 24, 20011  # odd V: unaligned rows, head and tail elements
+    x_cpu = seeded_logits((N, V), dtype, seed=21)
+    t_cpu = seeded_targets((N,), V, seed=21)
+    x, t = x_cpu.to(DEV), t_cpu.to(DEV)
+    g = torch.Generator().manual_seed(211)
+    gl, ge, gs = [(torch.randn(N, generator=g) * 0.5).to(DEV) for _ in range(3)]
+    first = None
+    for cfg in LAUNCHES:
+        outs = [torch.empty(N, device=DEV) for _ in range(3)]
+        _C.fwd_launch(x, t, *outs, config=cfg)
+        _check_fwd(oracle, x_cpu, t_cpu, outs, FWD_TOL[dtype], label=f"fwd {cfg}")
+        d = torch.empty_like(x)
+        _C.bwd_launch(x, t, outs[2], outs[1], gl, ge, gs, d, config=cfg)
+        if first is None:
+            first = outs
+            ulps, kind = _grad_ulps(oracle, x_cpu, t_cpu, outs[2], outs[1], d, gl, ge, gs)
+            assert ulps <= 1.0, f"{cfg} {kind}: {ulps}"
+            d_first = d.clone()
+        else:
+            # same saved lse/entropy -> the backward is elementwise and must be
+            # bitwise identical across launch shapes
+            d2 = torch.empty_like(x)
+            _C.bwd_launch(x, t, first[2], first[1], gl, ge, gs, d2, config=cfg)
+            assert np.array_equal(storage_bits(d2), storage_bits(d_first)), \
+                f"backward differs for launch {cfg}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("V", [1, 2, 3, 7, 8, 9, 15, 16, 17, 63, 64, 65, 1000, 4097])
+@pytest.mark.parametrize("offset", [0, 1, 3])
+def test_small_and_misaligned_rows(dtype, V, offset, oracle):
+    """Rows shorter than a vector, and rows starting off a 16-byte boundary."""
+    N = 5
+    x_cpu = seeded_logits((N, V), dtype, seed=V * 10 + offset)
+    t_cpu = seeded_targets((N,), V, seed=V)
+    buf = torch.empty(N * V + offset, dtype=dtype, device=DEV)
+    x = buf[offset:].view(N, V)
+    x.copy_(x_cpu.to(DEV))
+    t = t_cpu.to(DEV)
+    xg = x.detach().requires_grad_(True)
+    lp, h, l = _ko().fused_logprob_entropy(xg, t)
+    _check_fwd(oracle, x_cpu, t_cpu, (lp, h, l), FWD_TOL[dtype], label=f"V={V} off={offset}")
+    gl = torch.full((N,), 0.3, device=DEV)
+    ge = torch.full((N,), -0.2, device=DEV)
+    (lp * gl + h * ge).sum().backward()
+    ulps, kind = _grad_ulps(oracle, x_cpu, t_cpu, l.detach(), h.detach(), xg.grad, gl, ge)
+    assert ulps <= 1.0, f"{kind}: {ulps}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_strided_rows_shifted_slice(dtype, oracle):
+    """logits[:, :-1, :] of a [B, L, V] tensor, passed without a copy (C5's
+    layout) — one launch, same results as the contiguous copy."""
+    B, L, V = 3, 9, 3001
+    parent_cpu = seeded_logits((B, L, V), dtype, seed=31)
+    t_cpu = seeded_targets((B, L - 1), V, seed=31)
+    parent = parent_cpu.to(DEV)
+    view = parent[:, :-1, :].detach().requires_grad_(True)
+    assert not view.is_contiguous()
+    t = t_cpu.to(DEV)
+    lp, h, l = _ko().fused_logprob_entropy(view, t)
+    x_cpu = parent_cpu[:, :-1, :].contiguous()
+    _check_fwd(oracle, x_cpu, t_cpu, (lp, h, l), FWD_TOL[dtype], label="strided")
+    gl = torch.full((B, L - 1), -0.25, device=DEV)
+    (lp * gl).sum().backward()
+    assert view.grad.shape == view.shape
+    ulps, kind = _grad_ulps(oracle, x_cpu, t_cpu, l.detach(), h.detach(), view.grad, g_logp=gl)
+    assert ulps <= 1.0, f"{kind}: {ulps}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_out_of_range_targets(dtype, oracle):
+    """A target outside [0, V) gives logp = -lse and no one-hot gradient term
+    (the reference's target logit defaults to 0, csrc/fused_logprob.cu:180)."""
+    N, V = 6, 4099
+    x_cpu = seeded_logits((N, V), dtype, seed=41)
+    t_cpu = torch.tensor([-100, -1, 0, V - 1, V, V + 12345], dtype=torch.int64)
+    x = x_cpu.to(DEV).requires_grad_(True)
+    lp, h, l = _ko().fused_logprob_entropy(x, t_cpu.to(DEV))
+    _check_fwd(oracle, x_cpu, t_cpu, (lp, h, l), FWD_TOL[dtype])
+    bad = torch.tensor([0, 1, 4, 5])
+    assert torch.equal(lp[bad], -l[bad])
+    gl = torch.full((N,), 0.5, device=DEV)
+    (lp * gl).sum().backward()
+    ulps, kind = _grad_ulps(oracle, x_cpu, t_cpu, l.detach(), h.detach(), x.grad, g_logp=gl)
+    assert ulps <= 1.0, f"{kind}: {ulps}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("config", [None, (8, 4, 4, 1)])
+def test_negative_infinity_logits(dtype, config, oracle):
+    """-inf logits are skipped by the forward (the reference's sentinel rule,
+    csrc/fused_logprob.cu:142-143) and get a zero gradient."""
+    from kernel_opt import _C
+    N, V = 8, 9001
+    x_cpu = seeded_logits((N, V), dtype, seed=51)
+    g = torch.Generator().manual_seed(511)
+    mask = torch.rand(N, V, generator=g) < 0.3
+    mask[3] = torch.rand(V, generator=g) < 0.999  # almost all masked
+    mask[5, :4000] = True                          # a long masked run
+    x_cpu = x_cpu.masked_fill(mask, float("-inf"))
+    t_cpu = seeded_targets((N,), V, seed=51)
+    t_cpu[0] = int(torch.nonzero(mask[0])[0])     # a -inf target: logp = -inf
+    x, t = x_cpu.to(DEV), t_cpu.to(DEV)
+    outs = [torch.empty(N, device=DEV) for _ in range(3)]
+    _C.fwd_launch(x, t, *outs, config=config)
+    ref = oracle.forward(x_cpu, t_cpu.numpy())
+    for name, o, r in zip(("logp", "entropy", "lse"), outs, ref):
+        o = o.cpu().double().numpy()
+        assert np.array_equal(np.isfinite(o), np.isfinite(r)), name
+        fin = np.isfinite(r)
+        assert np.abs(o[fin] - r[fin]).max() <= FWD_TOL[dtype], name
+    assert outs[0][0].item() == float("-inf")
+    d = torch.empty_like(x)
+    gl = torch.full((N,), 0.5, device=DEV)
+    ge = torch.full((N,), 0.25, device=DEV)
+    _C.bwd_launch(x, t, outs[2], outs[1], gl, ge, None, d)
+    assert torch.isfinite(d.float()).all()
+    assert (d.float()[mask.to(DEV)] == 0).all()
+    ulps, kind = _grad_ulps(oracle, x_cpu, t_cpu, outs[2], outs[1], d, gl, ge)
+    assert ulps <= 1.0, f"{kind}: {ulps}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_special_rows(dtype):
+    """Whole row -inf, a NaN, a +inf: same outcome classes as the reference
+    v1 kernel (lse -inf / entropy NaN; NaN rows; NaN for +inf)."""
+    V = 1000
+    x = seeded_logits((4, V), dtype, seed=61).to(DEV)
+    x[0] = float("-inf")
+    x[1, 17] = float("nan")
+    x[2, 999] = float("inf")
+    t = torch.tensor([3, 3, 3, 3], device=DEV)
+    for config in (None, (4, 2, 2, 1)):
+        from kernel_opt import _C
+        lp, h, l = [torch.empty(4, device=DEV) for _ in range(3)]
+        _C.fwd_launch(x, t, lp, h, l, config=config)
+        assert l[0].item() == float("-inf") and math.isnan(h[0].item())
+        assert math.isnan(lp[0].item())  # x_t - lse = -inf - (-inf)
+        assert math.isnan(l[1].item()) and math.isnan(h[1].item()) and math.isnan(lp[1].item())
+        assert math.isnan(l[2].item()) and math.isnan(h[2].item())
+        assert torch.isfinite(torch.stack([lp[3], h[3], l[3]])).all()
+
+
+def test_naive_negative_infinity_semantics(oracle):
+    """The naive kernel keeps the reference naive kernel's behaviour: a -inf
+    logit after the first element turns the entropy NaN (:93-106)."""
+    V = 512
+    x_cpu = seeded_logits((2, V), torch.float32, seed=71)
+    x_cpu[0, 100] = float("-inf")
+    t_cpu = torch.tensor([5, 5])
+    lp, h, l = _ko().fused_logprob_entropy_naive(x_cpu.to(DEV), t_cpu.to(DEV))
+    r_lp, r_h, r_l = oracle.forward(x_cpu, t_cpu.numpy(), naive=True)
+    assert math.isnan(r_h[0]) and math.isnan(h[0].item())
+    assert abs(l[0].item() - r_l[0]) <= 1e-4 and abs(lp[0].item() - r_lp[0]) <= 1e-4
+    assert abs(h[1].item() - r_h[1]) <= 1e-4
+
+
+def test_empty_batch():
+    for dtype in DTYPES:
+        x = torch.empty(0, 5, 100, dtype=dtype, device=DEV, requires_grad=True)
+        t = torch.empty(0, 5, dtype=torch.int64, device=DEV)
+        lp, h, l = _ko().fused_logprob_entropy(x, t)
+        assert lp.shape == (0, 5)
+        (lp.sum() + h.sum()).backward()
+        assert x.grad.shape == x.shape
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_deterministic(dtype):
+    """Fixed reduction order: repeated runs are bitwise identical, split-row
+    mode included."""
+    from kernel_opt import _C
+    N, V = 64, 65537
+    x = seeded_logits((N, V), dtype, seed=81).to(DEV)
+    t = seeded_targets((N,), V, seed=81).to(DEV)
+    for config in (None, (8, 4, 8, 1), (4, 2, 16, 0)):
+        res = []
+        for _ in range(3):
+            outs = [torch.empty(N, device=DEV) for _ in range(3)]
+            _C.fwd_launch(x, t, *outs, config=config)
+            res.append(torch.stack(outs))
+        assert torch.equal(res[0], res[1]) and torch.equal(res[0], res[2]), config
+
+
+def test_workspace_reuse_across_shapes(oracle):
+    """The split-row workspace is left zero-filled after every launch, so a
+    sequence of launches with different row counts and split counts on one
+    stream stays correct."""
+    from kernel_opt import _C
+    V = 40009
+    seq = [(33, 8), (200, 2), (7, 32), (200, 8), (64, 3), (33, 16), (512, 4)]
+    for i, (N, s) in enumerate(seq):
+        x_cpu = seeded_logits((N, V), torch.bfloat16, seed=91 + i)
+        t_cpu = seeded_targets((N,), V, seed=91 + i)
+        outs = [torch.empty(N, device=DEV) for _ in range(3)]
+        _C.fwd_launch(x_cpu.to(DEV), t_cpu.to(DEV), *outs, config=(8, 2, s, 1))
+        _check_fwd(oracle, x_cpu, t_cpu, outs, 2e-5, label=f"N={N} splits={s}")
+
+
+def test_multiple_streams(oracle):
+    """Launches on two streams use separate workspaces."""
+    from kernel_opt import _C
+    V = 30011
+    xs = [seeded_logits((48, V), torch.bfloat16, seed=101 + i) for i in range(2)]
+    ts = [seeded_targets((48,), V, seed=101 + i) for i in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[torch.empty(48, device=DEV) for _ in range(3)] for _ in range(2)]
+    xd = [x.to(DEV) for x in xs]
+    td = [t.to(DEV) for t in ts]
+    torch.cuda.synchronize()
+    for rep in range(5):
+        for i in range(2):
+            with torch.cuda.stream(streams[i]):
+                _C.fwd_launch(xd[i], td[i], *outs[i], config=(8, 2, 8, 1))
+    torch.cuda.synchronize()
+    for i in range(2):
+        _check_fwd(oracle, xs[i], ts[i], outs[i], 2e-5, label=f"stream {i}")
