@@ -148,25 +148,26 @@ def algorithmic_bytes(n_rows: int, vocab: int, elem_bytes: int):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the reference's CPU eager path on a bounded row sample.
+# CPU baseline: the reference's CPU eager path.
 # ---------------------------------------------------------------------------
-def cpu_baseline(name: str, sample_rows: int, logits_gpu, targets_gpu, g_logp, g_ent):
+def cpu_baseline(name: str, max_rows: int, logits_gpu, targets_gpu, g_logp, g_ent, reps=3):
+    """Times the reference's CPU eager path on the workload (its first
+    `max_rows` rows, whole batch elements): the forward as TRL computes it
+    (selective_log_softmax + entropy_from_logits, restated in
+    oracle/eager_ref.py) and forward + backward as PyTorch autograd of the
+    eager formulas.  One warm-up, then the median of `reps` runs."""
     from oracle import eager_ref
 
     cfg = CONFIGS[name]
-    V = cfg["shape"][2]
-    N = logits_gpu.numel() // V
-    rows = min(sample_rows, N)
-    x = logits_gpu.reshape(-1, V)[:rows].detach().cpu().contiguous()
-    t = targets_gpu.reshape(-1)[:rows].cpu()
-    gl = g_logp.reshape(-1)[:rows].cpu()
-    ge = g_ent.reshape(-1)[:rows].cpu()
-    threads = torch.get_num_threads()
+    B, S, V = cfg["shape"]
+    b_keep = max(1, min(B, max_rows // S))
+    x = torch.stack([logits_gpu[b].detach().cpu() for b in range(b_keep)]).contiguous()
+    t = targets_gpu[:b_keep].cpu().contiguous()
+    gl = g_logp.reshape(B, S)[:b_keep].cpu()
+    ge = g_ent.reshape(B, S)[:b_keep].cpu()
 
     def fwd():
-        lp = eager_ref.trl_selective_log_softmax(x.unsqueeze(0), t.unsqueeze(0))
-        h = eager_ref.trl_entropy_from_logits(x.unsqueeze(0))
-        return lp, h
+        return eager_ref.trl_selective_log_softmax(x, t), eager_ref.trl_entropy_from_logits(x)
 
     def fwd_bwd():
         xr = x.clone().requires_grad_(True)
@@ -174,17 +175,51 @@ def cpu_baseline(name: str, sample_rows: int, logits_gpu, targets_gpu, g_logp, g
         (lp * gl + h * ge).sum().backward()
         return xr.grad
 
-    fwd()  # warm-up
-    t0 = time.perf_counter()
-    fwd()
-    t_fwd = time.perf_counter() - t0
-    fwd_bwd()
-    t0 = time.perf_counter()
-    fwd_bwd()
-    t_fb = time.perf_counter() - t0
-    scale = N / rows
-    return dict(fwd_ms=t_fwd * scale * 1e3, fwd_bwd_ms=t_fb * scale * 1e3, rows=rows,
-                threads=threads)
+    def timed(fn):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2]
+
+    t_fwd = timed(fwd)
+    t_fb = timed(fwd_bwd)
+    scale = B / b_keep
+    return dict(fwd_ms=t_fwd * scale * 1e3, fwd_bwd_ms=t_fb * scale * 1e3, rows=b_keep * S,
+                threads=torch.get_num_threads(), scaled=b_keep < B)
+
+
+class _HipEvents:
+    """Raw HIP events from the HIP runtime torch already loaded (same soname),
+    used with klp_time_next_call for kernel-exact durations."""
+
+    def __init__(self):
+        import ctypes
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self):
+        ev = self.ct.c_void_p()
+        rc = self.hip.hipEventCreate(self.ct.byref(ev))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreate failed: {rc}")
+        return ev
+
+    def elapsed_ms(self, a, b):
+        ms = self.ct.c_float()
+        rc = self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
+        return ms.value
+
+    def destroy(self, ev):
+        self.hip.hipEventDestroy(ev)
 
 
 # ---------------------------------------------------------------------------
@@ -197,12 +232,15 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
     ap.add_argument("--flush", action="store_true",
-                    help="write a 1 GiB buffer before every launch (cold Infinity Cache)")
+                    help="overwrite a 1 GiB buffer before every launch (cold Infinity Cache)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=16,
-                    help="rows of the workload the CPU baseline times")
-    ap.add_argument("--fwd-config", default=None, help="waves,unroll,splits,nt")
-    ap.add_argument("--bwd-config", default=None, help="waves,unroll,splits,nt")
+    ap.add_argument("--cpu-rows", type=int, default=1024,
+                    help="rows of the workload the CPU baseline times (whole batch elements)")
+    ap.add_argument("--fwd-config", default=None, help="waves,unroll,splits,flags")
+    ap.add_argument("--bwd-config", default=None, help="waves,unroll,splits,flags")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run torch's copy of a buffer the size of the logits (known "
+                         "traffic, for scaling HBM counters)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -212,6 +250,7 @@ def main(argv=None):
         return 2
 
     from kernel_opt import _C
+    from kernel_opt._library import lib
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
@@ -241,52 +280,68 @@ def main(argv=None):
     for _ in range(args.warmup):
         fwd()
         bwd()
+    if args.copy_calibration:
+        src = logits if logits.is_contiguous() else logits.contiguous()
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        del dst
     torch.cuda.synchronize()
 
     K = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
+    hev = _HipEvents()
+    evs = [[hev.create() for _ in range(4)] for _ in range(K)]
+    step_start = torch.cuda.Event(enable_timing=True)
+    step_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_wall0 = time.perf_counter()
+    step_start.record(stream)
     for k in range(K):
         if flush_buf is not None:
             flush_buf.fill_(k & 0xFF)
-        ev[k][0].record(stream)
+        lib.klp_time_next_call(evs[k][0], evs[k][1])
         fwd()
-        ev[k][1].record(stream)
         if flush_buf is not None:
             flush_buf.fill_((k + 1) & 0xFF)
-        ev[k][2].record(stream)
+        lib.klp_time_next_call(evs[k][2], evs[k][3])
         bwd()
-        ev[k][3].record(stream)
+    step_end.record(stream)
     torch.cuda.synchronize()
     t_wall = time.perf_counter() - t_wall0
 
-    fwd_ms = [e[0].elapsed_time(e[1]) for e in ev]
-    bwd_ms = [e[2].elapsed_time(e[3]) for e in ev]
+    fwd_ms = [hev.elapsed_ms(e[0], e[1]) for e in evs]
+    bwd_ms = [hev.elapsed_ms(e[2], e[3]) for e in evs]
+    for e in evs:
+        for x in e:
+            hev.destroy(x)
     fwd_avg = sum(fwd_ms) / K
     bwd_avg = sum(bwd_ms) / K
-    fwd_med = sorted(fwd_ms)[K // 2]
-    bwd_med = sorted(bwd_ms)[K // 2]
     fb, bb = algorithmic_bytes(N, V, esz)
     fwd_tbps = fb / (fwd_avg * 1e-3) / 1e12
     bwd_tbps = bb / (bwd_avg * 1e-3) / 1e12
-    step_ms = fwd_avg + bwd_avg
+    if flush_buf is None:
+        step_ms = step_start.elapsed_time(step_end) / K  # includes gaps between launches
+    else:
+        step_ms = fwd_avg + bwd_avg  # the flush fills are not part of the step
     step_tbps = (fb + bb) / (step_ms * 1e-3) / 1e12
 
     cpu = None
     if not args.no_cpu_baseline:
         c = cpu_baseline(name, args.cpu_rows, logits, targets, g_logp, g_ent)
+        sample = (f"{c['rows']} of {N} rows of {name} (the whole batch)" if not c["scaled"] else
+                  f"{c['rows']} of {N} rows of {name}, scaled by {N}/{c['rows']}")
         cpu = {
-            "value": (fb + bb) / ((c["fwd_ms"] + c["fwd_bwd_ms"]) * 1e-3) / 1e12,
+            "value": round((fb + bb) / ((c["fwd_ms"] + c["fwd_bwd_ms"]) * 1e-3) / 1e12, 6),
             "unit": "TB/s",
             "cores": c["threads"],
             "kind": "port",
-            "sample": (f"{c['rows']} of {N} rows of {name}, timed once after one warm-up and "
-                       f"scaled by {N}/{c['rows']}: TRL-eager forward (restated) "
-                       f"{c['fwd_ms']:.1f} ms, eager fwd+autograd bwd {c['fwd_bwd_ms']:.1f} ms "
-                       f"for the full batch"),
-            "fwd_ms": c["fwd_ms"],
-            "fwd_bwd_ms": c["fwd_bwd_ms"],
+            "sample": (f"{sample}; torch CPU, {c['threads']} threads, median of 3 after one "
+                       f"warm-up: TRL-eager forward (restated, oracle/eager_ref.py) "
+                       f"{c['fwd_ms']:.1f} ms + eager fwd with autograd bwd "
+                       f"{c['fwd_bwd_ms']:.1f} ms per batch; value = the step's algorithmic "
+                       f"bytes over their sum"),
+            "fwd_ms": round(c["fwd_ms"], 3),
+            "fwd_bwd_ms": round(c["fwd_bwd_ms"], 3),
         }
 
     B, S, _ = cfg["shape"]
@@ -307,20 +362,21 @@ def main(argv=None):
             logits.dtype],
         "data": "synthetic",
         "config": {"workload": f"{name}: logits [{B},{S},{V}] "
-                               f"{str(logits.dtype).replace('torch.', '')}, fwd+bwd",
+                               f"{str(logits.dtype).replace('torch.', '')}, one forward + one "
+                               f"backward launch per step",
                    "global_batch": B, "seq_len": S, "vocab": V, "n_rows": N,
                    "parallelism": "single-gpu",
                    "infinity_cache": "flushed" if args.flush else "warm"},
         "fwd_ms": round(fwd_avg, 5),
         "bwd_ms": round(bwd_avg, 5),
-        "fwd_ms_median": round(fwd_med, 5),
-        "bwd_ms_median": round(bwd_med, 5),
+        "fwd_ms_median": round(sorted(fwd_ms)[K // 2], 5),
+        "bwd_ms_median": round(sorted(bwd_ms)[K // 2], 5),
         "fwd_tbps": round(fwd_tbps, 4),
         "bwd_tbps": round(bwd_tbps, 4),
         "fwd_pct_peak": round(100 * fwd_tbps / HBM_PEAK_TBPS, 2),
         "bwd_pct_peak": round(100 * bwd_tbps / HBM_PEAK_TBPS, 2),
-        "fwd_launch": dict(zip(("waves", "unroll", "splits", "nontemporal"), fwd_used)),
-        "bwd_launch": dict(zip(("waves", "unroll", "splits", "nontemporal"), bwd_used)),
+        "fwd_launch": dict(zip(("waves", "unroll", "splits", "flags"), fwd_used)),
+        "bwd_launch": dict(zip(("waves", "unroll", "splits", "flags"), bwd_used)),
         "wall_s_timed": round(t_wall, 4),
         "roofline": {
             "bound": "hbm",

@@ -20,6 +20,13 @@ namespace {
 
 thread_local std::string g_last_error;
 thread_local int g_fail_next = 0;
+thread_local klp::Timing g_timing;  // consumed by the next compute call
+
+klp::Timing take_timing() {
+    const klp::Timing t = g_timing;
+    g_timing = klp::Timing{};
+    return t;
+}
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -40,8 +47,14 @@ int elem_bytes(int dtype) { return dtype == KLP_FP32 ? 4 : 2; }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-constexpr int64_t kTargetBlocks = 2048;  // 8 workgroups per CU on 256 CUs
-constexpr int kMaxSplits = 32;
+// Launch-shape targets.  Forward: at least kFwdTargetWaves resident wave64s
+// (16 per CU on 256 CUs) so that enough 16-byte loads are in flight to cover
+// HBM latency; rows are split across workgroups only when a whole 1024-thread
+// workgroup per row still leaves the chip short of that.  Backward: splitting
+// needs no second pass, so it aims at kBwdTargetBlocks workgroups.
+constexpr int64_t kFwdTargetWaves = 4096;
+constexpr int64_t kBwdTargetBlocks = 8192;
+constexpr int kMaxSplits = 64;
 
 // Shared checks of the row-addressed logits operand.
 int check_rows(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t rows_inner,
@@ -86,50 +99,49 @@ bool injected_failure(const char* what) {
 
 int64_t body_vectors(int dtype, int64_t vocab) { return vocab / (16 / elem_bytes(dtype)); }
 
-int default_fwd_splits(int dtype, int64_t n_rows, int64_t vocab, int threads, int unroll) {
-    const int64_t nvec = body_vectors(dtype, vocab);
-    int s = 1;
-    // Split while the grid is short of kTargetBlocks and every thread still
-    // gets at least two full iterations per piece.
-    while (s < kMaxSplits && n_rows * s < kTargetBlocks &&
-           nvec / (2 * s) >= static_cast<int64_t>(threads) * unroll * 2)
-        s *= 2;
-    return s;
-}
-
 klp::FwdConfig default_fwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     klp::FwdConfig c;
-    c.waves = 8;
     c.unroll = 4;
-    c.nontemporal = true;
-    c.splits = default_fwd_splits(dtype, n_rows, vocab, c.waves * 64, c.unroll);
+    c.flags = 0;
+    c.splits = 1;
+    if (n_rows * 4 >= kFwdTargetWaves) {
+        c.waves = 4;
+    } else if (n_rows * 8 >= kFwdTargetWaves) {
+        c.waves = 8;
+    } else {
+        c.waves = 16;
+        const int64_t nvec = body_vectors(dtype, vocab);
+        const int64_t tile = static_cast<int64_t>(c.waves) * 64 * c.unroll;
+        // Split while short of the wave target and every piece still keeps
+        // each thread busy for at least two full iterations.
+        while (c.splits < kMaxSplits && n_rows * c.splits * c.waves < kFwdTargetWaves &&
+               nvec / (2 * c.splits) >= 2 * tile)
+            c.splits *= 2;
+    }
     return c;
 }
 
 klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     klp::BwdConfig c;
-    c.waves = 4;
+    c.waves = 16;
     c.unroll = 2;
-    c.nontemporal = true;
+    c.flags = klp::kFlagNtStore;
+    c.splits = 1;
     const int64_t nvec = body_vectors(dtype, vocab);
-    int s = 1;
-    while (s < kMaxSplits && n_rows * s < kTargetBlocks &&
-           nvec / (2 * s) >= static_cast<int64_t>(c.waves) * 64 * c.unroll)
-        s *= 2;
-    c.splits = s;
+    const int64_t tile = static_cast<int64_t>(c.waves) * 64 * c.unroll;
+    while (c.splits < kMaxSplits && n_rows * c.splits < kBwdTargetBlocks &&
+           nvec / (2 * c.splits) >= tile)
+        c.splits *= 2;
     return c;
 }
 
 size_t workspace_bytes_for(int64_t n_rows, int splits) {
     if (splits <= 1 || n_rows <= 0) return 0;
-    const size_t padded = static_cast<size_t>((n_rows + 7) / 8) * 8;
-    const size_t partial_bytes = padded * static_cast<size_t>(splits) * 4 * sizeof(float);
-    const size_t counter_bytes = ((padded * sizeof(unsigned) + 15) / 16) * 16;
-    return partial_bytes + counter_bytes;
+    return static_cast<size_t>(n_rows) * static_cast<size_t>(splits) * 4 * sizeof(float);
 }
 
 int check_grid(int64_t n_rows, int splits, int threads) {
-    const int64_t blocks = (splits == 1) ? n_rows : ((n_rows + 7) / 8) * 8 * splits;
+    const int64_t blocks = n_rows * splits;
     if (blocks > (int64_t{1} << 31) - 1 || blocks * threads > (int64_t{1} << 32) - 1)
         return fail(KLP_EINVAL, "grid of %lld workgroups x %d threads is too large",
                     static_cast<long long>(blocks), threads);
@@ -147,9 +159,10 @@ int fwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     if ((rc = check_f32(logprob, "logprob")) != KLP_OK) return rc;
     if ((rc = check_f32(entropy, "entropy")) != KLP_OK) return rc;
     if ((rc = check_f32(lse, "lse")) != KLP_OK) return rc;
-    if (!klp::fwd_config_supported(cfg) || cfg.splits < 1 || cfg.splits > 1024)
-        return fail(KLP_EINVAL, "unsupported forward launch shape (waves=%d unroll=%d splits=%d)",
-                    cfg.waves, cfg.unroll, cfg.splits);
+    if (!klp::fwd_config_supported(cfg) || cfg.splits < 1 || cfg.splits > 1024 || cfg.flags != 0)
+        return fail(KLP_EINVAL,
+                    "unsupported forward launch shape (waves=%d unroll=%d splits=%d flags=%d)",
+                    cfg.waves, cfg.unroll, cfg.splits, cfg.flags);
     if (cfg.splits > 1) {
         const size_t need = workspace_bytes_for(n_rows, cfg.splits);
         if (workspace == nullptr) {
@@ -172,18 +185,9 @@ int fwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     p.entropy = entropy;
     p.lse = lse;
     p.splits = cfg.splits;
-    p.partials = nullptr;
-    p.counters = nullptr;
-    if (cfg.splits > 1) {
-        // Layout: [counters: padded rows x u32, rounded up to 16 B][partials:
-        // padded rows x splits x float4].  The kernel leaves both zero.
-        const size_t padded = static_cast<size_t>((n_rows + 7) / 8) * 8;
-        const size_t counter_bytes = ((padded * sizeof(unsigned) + 15) / 16) * 16;
-        p.counters = static_cast<unsigned*>(workspace);
-        p.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + counter_bytes);
-    }
+    p.partials = (cfg.splits > 1) ? static_cast<float*>(workspace) : nullptr;
     if (injected_failure("forward")) return KLP_ELAUNCH;
-    return after_launch(klp::launch_fwd(dtype, p, cfg, static_cast<hipStream_t>(stream)),
+    return after_launch(klp::launch_fwd(dtype, p, cfg, take_timing(), static_cast<hipStream_t>(stream)),
                         "forward");
 }
 
@@ -204,8 +208,9 @@ int bwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     if (!aligned(d_logits, elem_bytes(dtype)))
         return fail(KLP_EINVAL, "d_logits pointer is not aligned to its element size");
     if (!klp::bwd_config_supported(cfg) || cfg.splits < 1 || cfg.splits > 1024)
-        return fail(KLP_EINVAL, "unsupported backward launch shape (waves=%d unroll=%d splits=%d)",
-                    cfg.waves, cfg.unroll, cfg.splits);
+        return fail(KLP_EINVAL,
+                    "unsupported backward launch shape (waves=%d unroll=%d splits=%d flags=%d)",
+                    cfg.waves, cfg.unroll, cfg.splits, cfg.flags);
     if ((rc = check_grid(n_rows, cfg.splits, cfg.waves * 64)) != KLP_OK) return rc;
 
     klp::BwdParams p;
@@ -222,7 +227,7 @@ int bwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     p.d_logits = d_logits;
     p.splits = cfg.splits;
     if (injected_failure("backward")) return KLP_ELAUNCH;
-    return after_launch(klp::launch_bwd(dtype, p, cfg, static_cast<hipStream_t>(stream)),
+    return after_launch(klp::launch_bwd(dtype, p, cfg, take_timing(), static_cast<hipStream_t>(stream)),
                         "backward");
 }
 
@@ -243,6 +248,11 @@ size_t klp_last_error(char* buf, size_t len) {
 }
 
 void klp_debug_fail_next_launches(int count) { g_fail_next = count > 0 ? count : 0; }
+
+void klp_time_next_call(void* start_event, void* stop_event) {
+    g_timing.start = static_cast<hipEvent_t>(start_event);
+    g_timing.stop = static_cast<hipEvent_t>(stop_event);
+}
 
 size_t klp_fwd_workspace_bytes(int dtype, int64_t n_rows, int64_t vocab) {
     if (dtype != KLP_BF16 && dtype != KLP_FP16 && dtype != KLP_FP32) return 0;
@@ -266,12 +276,12 @@ int klp_fwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_
 int klp_fwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t rows_inner,
                int64_t stride_outer, int64_t stride_inner, const int64_t* targets, float* logprob,
                float* entropy, float* lse, void* workspace, size_t workspace_bytes, int waves,
-               int unroll, int splits, int nontemporal, void* stream) {
+               int unroll, int splits, int flags, void* stream) {
     klp::FwdConfig cfg;
     cfg.waves = waves;
     cfg.unroll = unroll;
     cfg.splits = splits;
-    cfg.nontemporal = nontemporal != 0;
+    cfg.flags = flags;
     return fwd_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner, targets,
                     logprob, entropy, lse, workspace, workspace_bytes, cfg, stream);
 }
@@ -297,7 +307,7 @@ int klp_fwd_naive(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
     p.entropy = entropy;
     p.lse = lse;
     if (injected_failure("naive forward")) return KLP_ELAUNCH;
-    return after_launch(klp::launch_fwd_naive(dtype, p, static_cast<hipStream_t>(stream)),
+    return after_launch(klp::launch_fwd_naive(dtype, p, take_timing(), static_cast<hipStream_t>(stream)),
                         "naive forward");
 }
 
@@ -314,24 +324,24 @@ int klp_bwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int
                int64_t stride_outer, int64_t stride_inner, const int64_t* targets,
                const float* lse, const float* entropy, const float* g_logp, const float* g_ent,
                const float* g_lse, void* d_logits, int waves, int unroll, int splits,
-               int nontemporal, void* stream) {
+               int flags, void* stream) {
     klp::BwdConfig cfg;
     cfg.waves = waves;
     cfg.unroll = unroll;
     cfg.splits = splits;
-    cfg.nontemporal = nontemporal != 0;
+    cfg.flags = flags;
     return bwd_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner, targets,
                     lse, entropy, g_logp, g_ent, g_lse, d_logits, cfg, stream);
 }
 
 void klp_default_config(int which, int dtype, int64_t n_rows, int64_t vocab, int* waves,
-                        int* unroll, int* splits, int* nontemporal) {
+                        int* unroll, int* splits, int* flags) {
     klp::FwdConfig c = (which == 0) ? default_fwd_config(dtype, n_rows, vocab)
                                     : default_bwd_config(dtype, n_rows, vocab);
     if (waves) *waves = c.waves;
     if (unroll) *unroll = c.unroll;
     if (splits) *splits = c.splits;
-    if (nontemporal) *nontemporal = c.nontemporal ? 1 : 0;
+    if (flags) *flags = c.flags;
 }
 
 }  // extern "C"

@@ -28,7 +28,7 @@ __device__ __forceinline__ float grad_one(float x, const RowGrad& g) {
     return p * fmaf(-g.g_ent, lp, g.c0);
 }
 
-template <int DT, int WAVES, int U, bool kNT>
+template <int DT, int WAVES, int U, bool kNtStore>
 __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
     typedef typename Traits<DT>::elem elem;
     constexpr int NTHREADS = WAVES * 64;
@@ -36,10 +36,8 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
     constexpr int ESZ = 16 / EPV;
 
     const int tid = threadIdx.x;
-    int64_t row;
-    int split;
-    block_to_row_split(blockIdx.x, p.splits, row, split);
-    if (row >= p.n_rows) return;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) / p.splits;
+    const int split = static_cast<int>(static_cast<int64_t>(blockIdx.x) - row * p.splits);
 
     const int64_t vocab = p.vocab;
     const elem* rp = static_cast<const elem*>(p.logits) + row_offset(p.rm, row);
@@ -106,7 +104,7 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t idx = i0 + tid + u * NTHREADS;
-            if (idx < ve) v[u] = load16<kNT>(vin + idx);
+            if (idx < ve) v[u] = load16<true>(vin + idx);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -121,50 +119,52 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
                     for (int j = 0; j < EPV; ++j)
                         if (j == t_lane_elem) x[j] += g.g_logp;
                 }
-                vout[idx] = pack<DT>(x);
+                if constexpr (kNtStore) __builtin_nontemporal_store(pack<DT>(x), vout + idx);
+                else vout[idx] = pack<DT>(x);
             }
         }
     }
 }
 
-template <int DT, int WAVES, int U, bool kNT>
-static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
-    const int64_t blocks = (p.splits == 1) ? p.n_rows : ((p.n_rows + 7) / 8) * 8 * p.splits;
-    hipLaunchKernelGGL((klp_bwd_kernel<DT, WAVES, U, kNT>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(WAVES * 64), 0, stream, p);
-    return hipGetLastError();
+template <int DT, int WAVES, int U, bool kNtStore>
+static hipError_t launch_bwd_t(const BwdParams& p, const Timing& tm, hipStream_t stream) {
+    return launch_kernel(klp_bwd_kernel<DT, WAVES, U, kNtStore>,
+                         dim3(static_cast<unsigned>(p.n_rows * p.splits)), dim3(WAVES * 64),
+                         stream, tm.start, tm.stop, p);
 }
 
 template <int DT>
-static hipError_t launch_bwd_dt(const BwdParams& p, const BwdConfig& c, hipStream_t stream) {
-#define KLP_BWD_CASE(W, U, NT)                                           \
-    if (c.waves == W && c.unroll == U && c.nontemporal == NT)            \
-        return launch_bwd_t<DT, W, U, NT>(p, stream);
-    KLP_BWD_CASE(4, 2, true)
-    KLP_BWD_CASE(4, 4, true)
-    KLP_BWD_CASE(8, 2, true)
-    KLP_BWD_CASE(8, 4, true)
-    KLP_BWD_CASE(4, 2, false)
-    KLP_BWD_CASE(4, 4, false)
-    KLP_BWD_CASE(8, 2, false)
-    KLP_BWD_CASE(8, 4, false)
+static hipError_t launch_bwd_dt(const BwdParams& p, const BwdConfig& c, const Timing& tm,
+                                hipStream_t stream) {
+    const bool nt = (c.flags & kFlagNtStore) != 0;
+#define KLP_BWD_CASE(W, U)                                                     \
+    if (c.waves == W && c.unroll == U)                                         \
+        return nt ? launch_bwd_t<DT, W, U, true>(p, tm, stream)                \
+                  : launch_bwd_t<DT, W, U, false>(p, tm, stream);
+    KLP_BWD_CASE(4, 2)
+    KLP_BWD_CASE(4, 4)
+    KLP_BWD_CASE(8, 2)
+    KLP_BWD_CASE(8, 4)
+    KLP_BWD_CASE(16, 2)
+    KLP_BWD_CASE(16, 4)
 #undef KLP_BWD_CASE
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, hipStream_t stream) {
+hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, const Timing& tm,
+                      hipStream_t stream) {
     switch (dtype) {
-        case kBF16: return launch_bwd_dt<kBF16>(p, c, stream);
-        case kFP16: return launch_bwd_dt<kFP16>(p, c, stream);
-        case kFP32: return launch_bwd_dt<kFP32>(p, c, stream);
+        case kBF16: return launch_bwd_dt<kBF16>(p, c, tm, stream);
+        case kFP16: return launch_bwd_dt<kFP16>(p, c, tm, stream);
+        case kFP32: return launch_bwd_dt<kFP32>(p, c, tm, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 bool bwd_config_supported(const BwdConfig& c) {
-    const bool w = (c.waves == 4 || c.waves == 8);
+    const bool w = (c.waves == 4 || c.waves == 8 || c.waves == 16);
     const bool u = (c.unroll == 2 || c.unroll == 4);
-    return w && u;
+    return w && u && (c.flags & ~kFlagNtStore) == 0;
 }
 
 }  // namespace klp

@@ -21,6 +21,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kLn2 = 0.69314718055994530942f;
@@ -85,12 +88,11 @@ template <> __device__ __forceinline__ void unpack<kBF16>(const u32x4 v, float* 
     }
 }
 template <> __device__ __forceinline__ void unpack<kFP16>(const u32x4 v, float* x) {
+    // Whole-vector bit_cast: hipcc 7.2 miscompiles __builtin_bit_cast applied
+    // to an element expression v[j] (it reads element 0 for every j).
+    const f32x8 f = __builtin_convertvector(__builtin_bit_cast(f16x8, v), f32x8);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const f32x2 f = __builtin_convertvector(__builtin_bit_cast(f16x2, v[j]), f32x2);
-        x[2 * j] = f.x;
-        x[2 * j + 1] = f.y;
-    }
+    for (int j = 0; j < 8; ++j) x[j] = f[j];
 }
 template <> __device__ __forceinline__ void unpack<kFP32>(const u32x4 v, float* x) {
 #pragma unroll
@@ -100,22 +102,16 @@ template <> __device__ __forceinline__ void unpack<kFP32>(const u32x4 v, float* 
 // kPerVec floats -> 16 bytes, round to nearest even.
 template <int DT> __device__ __forceinline__ u32x4 pack(const float* x);
 template <> __device__ __forceinline__ u32x4 pack<kBF16>(const float* x) {
-    u32x4 r;
+    f32x8 f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const f32x2 f = {x[2 * j], x[2 * j + 1]};
-        r[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
-    }
-    return r;
+    for (int j = 0; j < 8; ++j) f[j] = x[j];
+    return __builtin_bit_cast(u32x4, __builtin_convertvector(f, bf16x8));
 }
 template <> __device__ __forceinline__ u32x4 pack<kFP16>(const float* x) {
-    u32x4 r;
+    f32x8 f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const f32x2 f = {x[2 * j], x[2 * j + 1]};
-        r[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
-    }
-    return r;
+    for (int j = 0; j < 8; ++j) f[j] = x[j];
+    return __builtin_bit_cast(u32x4, __builtin_convertvector(f, f16x8));
 }
 template <> __device__ __forceinline__ u32x4 pack<kFP32>(const float* x) {
     u32x4 r;
@@ -152,24 +148,6 @@ __device__ __forceinline__ int64_t row_offset(const RowMap& rm, int64_t r) {
     if (r < rm.rows_inner) return r * rm.stride_inner;
     const int64_t q = r / rm.rows_inner;
     return q * rm.stride_outer + (r - q * rm.rows_inner) * rm.stride_inner;
-}
-
-// Workgroup -> (row, split).  Workgroups are dispatched round-robin over the
-// 8 XCDs (blockIdx % 8); with splits > 1 the splits of one row are given
-// consecutive blockIdx values that are 8 apart, so they share an XCD and its
-// L2, where the last one reads the others' partial states.
-__device__ __forceinline__ void block_to_row_split(int64_t b, int splits, int64_t& row,
-                                                   int& split) {
-    if (splits == 1) {
-        row = b;
-        split = 0;
-        return;
-    }
-    const int64_t xcd = b & 7;
-    const int64_t k = b >> 3;
-    const int64_t group = k / splits;
-    split = static_cast<int>(k - group * splits);
-    row = group * 8 + xcd;
 }
 
 // ---------------------------------------------------------------------------

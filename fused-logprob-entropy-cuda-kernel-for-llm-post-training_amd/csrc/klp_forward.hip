@@ -20,7 +20,7 @@
 
 namespace klp {
 
-template <int DT, bool kClamp, int U, int NTHREADS, bool kNT>
+template <int DT, bool kClamp, int U, int NTHREADS>
 __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT>::elem* rp,
                                                const u32x4* vp, int64_t head, int64_t tail_begin,
                                                int64_t vocab, bool with_edges, int64_t vb,
@@ -41,7 +41,7 @@ __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT
     for (int64_t k = 0; k < n_full; ++k) {
         u32x4 v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = load16<kNT>(vp + i + u * NTHREADS);
+        for (int u = 0; u < U; ++u) v[u] = load16<true>(vp + i + u * NTHREADS);
         float x[U * EPV];
 #pragma unroll
         for (int u = 0; u < U; ++u) unpack<DT>(v[u], x + u * EPV);
@@ -56,7 +56,7 @@ __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT
         for (int u = 0; u < U; ++u) {
             const int64_t idx = i + u * NTHREADS;
             if (idx < ve) {
-                v[u] = load16<kNT>(vp + idx);
+                v[u] = load16<true>(vp + idx);
             } else {
                 const uint32_t w = Traits<DT>::kNegInfWord;
                 v[u] = u32x4{w, w, w, w};
@@ -69,7 +69,7 @@ __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT
     }
 }
 
-template <int DT, int WAVES, int U, bool kNT>
+template <int DT, int WAVES, int U, bool kSplit>
 __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     typedef typename Traits<DT>::elem elem;
     constexpr int NTHREADS = WAVES * 64;
@@ -77,20 +77,22 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     constexpr int ESZ = 16 / EPV;
 
     const int tid = threadIdx.x;
-    int64_t row;
-    int split;
-    block_to_row_split(blockIdx.x, p.splits, row, split);
-    if (row >= p.n_rows) return;  // whole workgroup leaves together
+    const int64_t b = blockIdx.x;
+    const int64_t row = kSplit ? b / p.splits : b;
+    const int split = kSplit ? static_cast<int>(b - row * p.splits) : 0;
 
     const int64_t vocab = p.vocab;
     const elem* rp = static_cast<const elem*>(p.logits) + row_offset(p.rm, row);
-    const int64_t tgt = p.targets[row];
 
-    // The target logit is read directly; the reference captures it inside the
-    // scan (csrc/fused_logprob.cu:180,185) and leaves 0 when the target is out
-    // of range.  Issued first so its latency hides behind the scan.
+    // The target logit is read directly (the reference captures it inside the
+    // scan, csrc/fused_logprob.cu:180,185, leaving 0 for an out-of-range
+    // target).  Issued first so that its latency hides behind the scan.  In
+    // split mode the combine kernel reads it instead.
     float x_target = 0.0f;
-    if (tid == 0 && tgt >= 0 && tgt < vocab) x_target = to_f32<DT>(rp[tgt]);
+    if (!kSplit && tid == 0) {
+        const int64_t tgt = p.targets[row];
+        if (tgt >= 0 && tgt < vocab) x_target = to_f32<DT>(rp[tgt]);
+    }
 
     const uintptr_t addr = reinterpret_cast<uintptr_t>(rp);
     int64_t head = static_cast<int64_t>(((16u - (addr & 15u)) & 15u) / ESZ);
@@ -99,21 +101,24 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     const int64_t tail_begin = head + nvec * EPV;
     const u32x4* vp = reinterpret_cast<const u32x4*>(rp + head);
 
-    const int64_t per = (nvec + p.splits - 1) / p.splits;
-    int64_t vb = static_cast<int64_t>(split) * per;
-    int64_t ve = vb + per;
-    if (vb > nvec) vb = nvec;
-    if (ve > nvec) ve = nvec;
+    int64_t vb = 0, ve = nvec;
+    if (kSplit) {
+        const int64_t per = (nvec + p.splits - 1) / p.splits;
+        vb = static_cast<int64_t>(split) * per;
+        ve = vb + per;
+        if (vb > nvec) vb = nvec;
+        if (ve > nvec) ve = nvec;
+    }
 
     Stat s = stat_empty();
-    scan_row_piece<DT, false, U, NTHREADS, kNT>(s, rp, vp, head, tail_begin, vocab, split == 0,
-                                                vb, ve, tid);
+    scan_row_piece<DT, false, U, NTHREADS>(s, rp, vp, head, tail_begin, vocab, split == 0, vb,
+                                           ve, tid);
     if (needs_clamped_rescan(s)) {
         // This lane met a -inf logit: redo its values with -inf excluded, as
         // the reference's sentinel rule does (csrc/fused_logprob.cu:142-143).
         s = stat_empty();
-        scan_row_piece<DT, true, U, NTHREADS, kNT>(s, rp, vp, head, tail_begin, vocab,
-                                                   split == 0, vb, ve, tid);
+        scan_row_piece<DT, true, U, NTHREADS>(s, rp, vp, head, tail_begin, vocab, split == 0, vb,
+                                              ve, tid);
     }
 
     s = wave_reduce(s);
@@ -128,44 +133,40 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) r = combine(r, wave_stat[w]);
 
-    if (p.splits == 1) {
-        const RowOut o = finalize(r, x_target);
-        p.logprob[row] = o.logp;
-        p.entropy[row] = o.ent;
-        p.lse[row] = o.lse;
+    if (kSplit) {
+        // Partial state of this piece; klp_fwd_combine_kernel merges the
+        // pieces of each row in split order after this kernel completes.
+        float4* slot = reinterpret_cast<float4*>(p.partials) + b;
+        *slot = make_float4(r.m, r.z, r.t, 0.0f);
         return;
     }
+    const RowOut o = finalize(r, x_target);
+    p.logprob[row] = o.logp;
+    p.entropy[row] = o.ent;
+    p.lse[row] = o.lse;
+}
 
-    // Split-row mode: publish this piece's state; the last piece of the row
-    // to arrive merges all pieces in split order and resets the counter.
-    float* slot = p.partials + (row * p.splits + split) * 4;
-    slot[0] = r.m;
-    slot[1] = r.z;
-    slot[2] = r.t;
-    __threadfence();
-    const unsigned prev = atomicAdd(p.counters + row, 1u);
-    if (prev != static_cast<unsigned>(p.splits - 1)) return;
-    __threadfence();
+// Split-row second pass: one thread per row merges the row's `splits`
+// partial states in split order (a fixed order, so results do not depend on
+// which workgroup finished first) and writes the outputs.
+template <int DT>
+__global__ __launch_bounds__(256) void klp_fwd_combine_kernel(FwdParams p) {
+    typedef typename Traits<DT>::elem elem;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (row >= p.n_rows) return;
+    const elem* rp = static_cast<const elem*>(p.logits) + row_offset(p.rm, row);
+    const int64_t tgt = p.targets[row];
+    const float x_target = (tgt >= 0 && tgt < p.vocab) ? to_f32<DT>(rp[tgt]) : 0.0f;
+    const float4* part = reinterpret_cast<const float4*>(p.partials) + row * p.splits;
     Stat acc = stat_empty();
     for (int k = 0; k < p.splits; ++k) {
-        float* q = p.partials + (row * p.splits + k) * 4;
-        Stat piece;
-        piece.m = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        piece.z = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        piece.t = __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        acc = combine(acc, piece);
-        // Leave the workspace all-zero for the next launch, whatever its
-        // layout (the counter region of a later, larger launch may cover
-        // these slots).
-        q[0] = 0.0f;
-        q[1] = 0.0f;
-        q[2] = 0.0f;
+        const float4 q = part[k];
+        acc = combine(acc, Stat{q.x, q.y, q.z});
     }
     const RowOut o = finalize(acc, x_target);
     p.logprob[row] = o.logp;
     p.entropy[row] = o.ent;
     p.lse[row] = o.lse;
-    __hip_atomic_store(p.counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Naive forward: restates the reference's one-thread-per-row recurrence with
@@ -205,61 +206,64 @@ __global__ __launch_bounds__(128) void klp_fwd_naive_kernel(NaiveParams p) {
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-template <int DT, int WAVES, int U, bool kNT>
-static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
-    const int64_t blocks = (p.splits == 1) ? p.n_rows : ((p.n_rows + 7) / 8) * 8 * p.splits;
-    hipLaunchKernelGGL((klp_fwd_kernel<DT, WAVES, U, kNT>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(WAVES * 64), 0, stream, p);
-    return hipGetLastError();
+template <int DT, int WAVES, int U>
+static hipError_t launch_fwd_t(const FwdParams& p, const Timing& tm, hipStream_t stream) {
+    if (p.splits == 1)
+        return launch_kernel(klp_fwd_kernel<DT, WAVES, U, false>,
+                             dim3(static_cast<unsigned>(p.n_rows)), dim3(WAVES * 64), stream,
+                             tm.start, tm.stop, p);
+    hipError_t e = launch_kernel(klp_fwd_kernel<DT, WAVES, U, true>,
+                                 dim3(static_cast<unsigned>(p.n_rows * p.splits)),
+                                 dim3(WAVES * 64), stream, tm.start, nullptr, p);
+    if (e != hipSuccess) return e;
+    return launch_kernel(klp_fwd_combine_kernel<DT>,
+                         dim3(static_cast<unsigned>((p.n_rows + 255) / 256)), dim3(256), stream,
+                         nullptr, tm.stop, p);
 }
 
 template <int DT>
-static hipError_t launch_fwd_dt(const FwdParams& p, const FwdConfig& c, hipStream_t stream) {
-#define KLP_FWD_CASE(W, U, NT)                                           \
-    if (c.waves == W && c.unroll == U && c.nontemporal == NT)            \
-        return launch_fwd_t<DT, W, U, NT>(p, stream);
-    KLP_FWD_CASE(4, 2, true)
-    KLP_FWD_CASE(4, 4, true)
-    KLP_FWD_CASE(8, 2, true)
-    KLP_FWD_CASE(8, 4, true)
-    KLP_FWD_CASE(4, 2, false)
-    KLP_FWD_CASE(4, 4, false)
-    KLP_FWD_CASE(8, 2, false)
-    KLP_FWD_CASE(8, 4, false)
+static hipError_t launch_fwd_dt(const FwdParams& p, const FwdConfig& c, const Timing& tm,
+                                hipStream_t stream) {
+#define KLP_FWD_CASE(W, U) \
+    if (c.waves == W && c.unroll == U) return launch_fwd_t<DT, W, U>(p, tm, stream);
+    KLP_FWD_CASE(4, 2)
+    KLP_FWD_CASE(4, 4)
+    KLP_FWD_CASE(8, 2)
+    KLP_FWD_CASE(8, 4)
+    KLP_FWD_CASE(16, 2)
+    KLP_FWD_CASE(16, 4)
 #undef KLP_FWD_CASE
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream) {
+hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, const Timing& tm,
+                      hipStream_t stream) {
     switch (dtype) {
-        case kBF16: return launch_fwd_dt<kBF16>(p, c, stream);
-        case kFP16: return launch_fwd_dt<kFP16>(p, c, stream);
-        case kFP32: return launch_fwd_dt<kFP32>(p, c, stream);
+        case kBF16: return launch_fwd_dt<kBF16>(p, c, tm, stream);
+        case kFP16: return launch_fwd_dt<kFP16>(p, c, tm, stream);
+        case kFP32: return launch_fwd_dt<kFP32>(p, c, tm, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 bool fwd_config_supported(const FwdConfig& c) {
-    const bool w = (c.waves == 4 || c.waves == 8);
+    const bool w = (c.waves == 4 || c.waves == 8 || c.waves == 16);
     const bool u = (c.unroll == 2 || c.unroll == 4);
     return w && u;
 }
 
-hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream) {
-    const unsigned blocks = static_cast<unsigned>((p.n_rows + 127) / 128);
+hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, const Timing& tm,
+                            hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((p.n_rows + 127) / 128));
     switch (dtype) {
-        case kBF16:
-            hipLaunchKernelGGL(klp_fwd_naive_kernel<kBF16>, dim3(blocks), dim3(128), 0, stream, p);
-            break;
-        case kFP16:
-            hipLaunchKernelGGL(klp_fwd_naive_kernel<kFP16>, dim3(blocks), dim3(128), 0, stream, p);
-            break;
-        case kFP32:
-            hipLaunchKernelGGL(klp_fwd_naive_kernel<kFP32>, dim3(blocks), dim3(128), 0, stream, p);
-            break;
+        case kBF16: return launch_kernel(klp_fwd_naive_kernel<kBF16>, grid, dim3(128), stream,
+                                         tm.start, tm.stop, p);
+        case kFP16: return launch_kernel(klp_fwd_naive_kernel<kFP16>, grid, dim3(128), stream,
+                                         tm.start, tm.stop, p);
+        case kFP32: return launch_kernel(klp_fwd_naive_kernel<kFP32>, grid, dim3(128), stream,
+                                         tm.start, tm.stop, p);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace klp

@@ -2,6 +2,7 @@
 // the kernel translation units and the C-ABI dispatcher (klp_abi.hip).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -18,8 +19,7 @@ struct FwdParams {
     float* logprob;
     float* entropy;
     float* lse;
-    float* partials;     // [n_rows_padded * splits * 4] when splits > 1
-    unsigned* counters;  // [n_rows_padded], zero between launches
+    float* partials;  // [n_rows * splits] float4 (m, z, t, unused) when splits > 1
     int splits;
 };
 
@@ -49,19 +49,44 @@ struct BwdParams {
     int splits;
 };
 
-// Launch shape: WAVES wave64s per workgroup, `unroll` 16-byte loads per
-// thread per iteration, `splits` workgroups per row, non-temporal loads.
+// Launch shape: `waves` wave64s per workgroup, `unroll` 16-byte loads per
+// thread per iteration, `splits` workgroups per row.  `flags` selects kernel
+// variants: bit 0 (backward only) = non-temporal gradient stores.  Loads of
+// logits are always non-temporal.
 struct FwdConfig {
     int waves;
     int unroll;
     int splits;
-    bool nontemporal;
+    int flags;
 };
 typedef FwdConfig BwdConfig;
+constexpr int kFlagNtStore = 1;
 
-hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream);
-hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream);
-hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, hipStream_t stream);
+// Optional timing events: when set, the first kernel of a call records
+// `start` as it begins and the last one records `stop` as it ends
+// (hipExtLaunchKernel), so the elapsed time is kernel execution only.
+struct Timing {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+
+template <typename... KArgs, typename... Args>
+inline hipError_t launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block,
+                                hipStream_t stream, hipEvent_t start, hipEvent_t stop,
+                                Args... args) {
+    if (start != nullptr || stop != nullptr)
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+    return hipGetLastError();
+}
+
+hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, const Timing& tm,
+                      hipStream_t stream);
+hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, const Timing& tm,
+                            hipStream_t stream);
+hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, const Timing& tm,
+                      hipStream_t stream);
 bool fwd_config_supported(const FwdConfig& c);
 bool bwd_config_supported(const BwdConfig& c);
 

@@ -72,8 +72,8 @@ def row_layout(t: torch.Tensor):
     return None
 
 
-# Split-row workspaces, one per (device, stream): zero-filled once, and left
-# zero-filled by every completed forward launch (include/kernel_opt_hip.h).
+# Split-row workspaces (partial states), one per (device, stream) so that
+# launches sharing one are ordered by their stream.  No initialisation needed.
 _ws_lock = threading.Lock()
 _workspaces: dict = {}
 
@@ -86,7 +86,7 @@ def _workspace(device: torch.device, stream: torch.cuda.Stream, nbytes: int):
         buf = _workspaces.get(key)
         if buf is None or buf.numel() < nbytes:
             with torch.cuda.stream(stream):
-                buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+                buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
             _workspaces[key] = buf
         return buf
 
@@ -125,7 +125,7 @@ def _common_forward_checks(logits, targets, logprob, entropy, lse_out, per_outpu
 
 def fwd_launch(logits, targets, logprob, entropy, lse_out, config=None) -> None:
     """Forward into caller-allocated outputs.  ``config`` = ``(waves, unroll,
-    splits, nontemporal)`` pins a launch shape (tuning ABI); ``None`` lets the
+    splits, flags)`` pins a launch shape (tuning ABI); ``None`` lets the
     native dispatcher choose."""
     rows, N, V = _common_forward_checks(logits, targets, logprob, entropy, lse_out, False)
     if N == 0:
@@ -145,8 +145,8 @@ def fwd_launch(logits, targets, logprob, entropy, lse_out, config=None) -> None:
         if config is None:
             rc = lib.klp_fwd(*args, ctypes.c_void_p(stream.cuda_stream))
         else:
-            w, u, s, nt = (int(c) for c in config)
-            rc = lib.klp_fwd_ex(*args, w, u, s, nt, ctypes.c_void_p(stream.cuda_stream))
+            w, u, sp, fl = (int(c) for c in config)
+            rc = lib.klp_fwd_ex(*args, w, u, sp, fl, ctypes.c_void_p(stream.cuda_stream))
     check_status(rc)
 
 
@@ -210,8 +210,8 @@ def bwd_launch(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits,
         if config is None:
             rc = lib.klp_bwd(*args, ctypes.c_void_p(stream.cuda_stream))
         else:
-            w, u, s, nt = (int(c) for c in config)
-            rc = lib.klp_bwd_ex(*args, w, u, s, nt, ctypes.c_void_p(stream.cuda_stream))
+            w, u, sp, fl = (int(c) for c in config)
+            rc = lib.klp_bwd_ex(*args, w, u, sp, fl, ctypes.c_void_p(stream.cuda_stream))
     check_status(rc)
 
 
@@ -222,7 +222,7 @@ def fused_logprob_entropy_v1_backward(logits, targets, lse, entropy, g_logp, g_e
 
 
 def default_config(which: str, dtype: torch.dtype, n_rows: int, vocab: int):
-    """Launch shape ``(waves, unroll, splits, nontemporal)`` the native
+    """Launch shape ``(waves, unroll, splits, flags)`` the native
     dispatcher picks for the forward (``which="fwd"``) or backward."""
     out = [ctypes.c_int(0) for _ in range(4)]
     lib.klp_default_config(0 if which == "fwd" else 1, DTYPE_CODES[dtype], n_rows, vocab,

@@ -67,11 +67,12 @@ size_t klp_last_error(char* buf, size_t len);
 
 /*
  * Bytes of device workspace that klp_fwd can use to split each row across
- * several workgroups (split-row mode) for this problem size.  0 means the
- * dispatcher keeps one workgroup per row.  The workspace must be zero-filled
- * once before its first use; klp_fwd leaves it zero-filled again after every
- * launch that completes.  Launches that share one workspace must be ordered
- * (same stream, or synchronised).
+ * several workgroups (split-row mode) for this problem size; 0 means the
+ * dispatcher keeps one workgroup per row.  In split-row mode klp_fwd enqueues
+ * two kernels: the first writes one partial (max, sum-exp, sum-x-exp) state
+ * per row piece into the workspace, the second merges each row's pieces in a
+ * fixed order.  The workspace needs no initialisation; launches that share
+ * one workspace must be ordered (same stream, or synchronised).
  */
 size_t klp_fwd_workspace_bytes(int dtype, int64_t n_rows, int64_t vocab);
 
@@ -83,8 +84,7 @@ size_t klp_fwd_workspace_bytes(int dtype, int64_t n_rows, int64_t vocab);
  * (reference csrc/fused_logprob.cu:355-403, bound at csrc/bindings.cpp:21-23).
  *
  * `workspace` may be NULL (then one workgroup per row).  When it is not
- * NULL it must hold klp_fwd_workspace_bytes() bytes, be 16-byte aligned and
- * follow the zero-fill rule above.
+ * NULL it must hold klp_fwd_workspace_bytes() bytes and be 16-byte aligned.
  */
 int klp_fwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
             int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,

@@ -9,9 +9,10 @@
  * not depend on the launch shape beyond fp32 rounding of the reduction order.
  *
  * Conventions are those of kernel_opt_hip.h.  Supported shapes:
- * waves in {4, 8} (wave64s per workgroup), unroll in {2, 4} (16-byte loads per
- * thread per iteration), splits in [1, 1024] (workgroups per row),
- * nontemporal in {0, 1}.
+ * waves in {4, 8, 16} (wave64s per workgroup), unroll in {2, 4} (16-byte
+ * loads per thread per iteration), splits in [1, 1024] (workgroups per row).
+ * `flags` selects kernel variants: forward: must be 0; backward: bit 0 =
+ * non-temporal gradient stores.
  */
 #ifndef KERNEL_OPT_HIP_TUNING_H
 #define KERNEL_OPT_HIP_TUNING_H
@@ -32,7 +33,7 @@ int klp_fwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                const int64_t* targets,
                float* logprob, float* entropy, float* lse,
                void* workspace, size_t workspace_bytes,
-               int waves, int unroll, int splits, int nontemporal,
+               int waves, int unroll, int splits, int flags,
                void* stream);
 
 /* klp_bwd with an explicit launch shape (splits need no workspace). */
@@ -42,12 +43,21 @@ int klp_bwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                const float* lse, const float* entropy,
                const float* g_logp, const float* g_ent, const float* g_lse,
                void* d_logits,
-               int waves, int unroll, int splits, int nontemporal,
+               int waves, int unroll, int splits, int flags,
                void* stream);
+
+/*
+ * Kernel-exact timing for benchmarks: the next compute call on the calling
+ * thread (klp_fwd*, klp_fwd_naive, klp_bwd*) records `start_event` when its
+ * first kernel starts executing and `stop_event` when its last kernel ends
+ * (hipExtLaunchKernel), instead of at enqueue.  Both are hipEvent_t created
+ * with timing enabled; either may be NULL.  One call consumes the setting.
+ */
+void klp_time_next_call(void* start_event, void* stop_event);
 
 /* The launch shape klp_fwd (which = 0) or klp_bwd (which = 1) would pick. */
 void klp_default_config(int which, int dtype, int64_t n_rows, int64_t vocab,
-                        int* waves, int* unroll, int* splits, int* nontemporal);
+                        int* waves, int* unroll, int* splits, int* flags);
 
 #ifdef __cplusplus
 }

@@ -87,7 +87,11 @@ static double round_format(double x, int p, int emin, double maxf) {
     e -= 1;
     if (e < emin) e = emin;
     const double ulp = ldexp(1.0, e - (p - 1));
+#if KLP_MUTANT == 8 /* planted: truncation instead of nearest-even */
+    const double r = trunc(x / ulp) * ulp;
+#else
     const double r = rint(x / ulp) * ulp; /* rint: ties to even */
+#endif
     if (fabs(r) > maxf) return x > 0 ? INFINITY : -INFINITY;
     return r;
 }
@@ -296,7 +300,11 @@ void klp_oracle_backward(const void* logits, int dtype, int64_t n_rows, int64_t 
                 val = p * (c0 - ge * lp);
 #endif
             }
+#if KLP_MUTANT == 7 /* planted: wrong sign of the one-hot term */
+            if (v == tgt) val -= gl;
+#else
             if (v == tgt) val += gl;
+#endif
             d[v] = val;
         }
     }

@@ -76,14 +76,17 @@ def test_validation_errors():
 def test_workspace_and_launch_shape_errors():
     from kernel_opt._library import KLP_EINVAL, KLP_EWORKSPACE, lib
     need = lib.klp_fwd_workspace_bytes_ex(4, 8)
-    assert need > 0
-    rc = lib.klp_fwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, P, P, need - 16, 8, 4, 8, 1, None)
+    assert need == 4 * 8 * 16  # one float4 partial state per (row, split)
+    assert lib.klp_fwd_workspace_bytes_ex(4, 1) == 0
+    rc = lib.klp_fwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, P, P, need - 16, 8, 4, 8, 0, None)
     assert rc == KLP_EWORKSPACE and "workspace" in _err()
     rc = lib.klp_fwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, P, ctypes.c_void_p(0x10008), need,
-                        8, 4, 8, 1, None)
+                        8, 4, 8, 0, None)
     assert rc == KLP_EWORKSPACE  # misaligned workspace
-    rc = lib.klp_fwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, P, None, 0, 5, 4, 1, 1, None)
+    rc = lib.klp_fwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, P, None, 0, 5, 4, 1, 0, None)
     assert rc == KLP_EINVAL and "launch shape" in _err()
+    rc = lib.klp_fwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, P, None, 0, 8, 4, 1, 1, None)
+    assert rc == KLP_EINVAL and "flags" in _err()  # forward has no variant flags
     rc = lib.klp_bwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, None, None, None, P, 8, 3, 1, 1, None)
     assert rc == KLP_EINVAL and "launch shape" in _err()
     rc = lib.klp_bwd(P, 0, 4, 100, 4, 0, 100, P, P, P, None, None, None, None, None)
@@ -113,16 +116,22 @@ def test_last_error_truncates():
 
 def test_default_launch_shapes():
     from kernel_opt import _C
-    # headline config: split rows so that 1024 rows fill 256 CUs
-    w, u, s, nt = _C.default_config("fwd", torch.bfloat16, 1024, 152064)
-    assert s >= 2 and w in (4, 8) and u in (2, 4)
+    # headline config: 1024 rows x 4 waves already fill 256 CUs, no split
+    w, u, s, f = _C.default_config("fwd", torch.bfloat16, 1024, 152064)
+    assert (w, s, f) == (4, 1, 0) and u in (2, 4)
+    # 256 rows: wider workgroups instead of splitting
+    assert _C.default_config("fwd", torch.float32, 256, 32000)[::2] == (16, 1)
+    # few rows, long vocab: split rows (two-kernel mode, needs a workspace)
+    w, u, s, f = _C.default_config("fwd", torch.bfloat16, 16, 152064)
+    assert w == 16 and s >= 2
     # tiny vocab: never split
     assert _C.default_config("fwd", torch.float32, 4, 64)[2] == 1
-    # many rows: one workgroup per row
-    assert _C.default_config("fwd", torch.bfloat16, 32768, 151936)[2] == 1
     from kernel_opt._library import lib
     assert lib.klp_fwd_workspace_bytes(0, 32768, 151936) == 0
-    assert lib.klp_fwd_workspace_bytes(0, 1024, 152064) > 0
+    assert lib.klp_fwd_workspace_bytes(0, 1024, 152064) == 0
+    assert lib.klp_fwd_workspace_bytes(0, 16, 152064) == 16 * s * 16
+    # backward splits rows freely (no second pass)
+    assert _C.default_config("bwd", torch.bfloat16, 1024, 152064)[2] >= 2
 
 
 def test_shim_rejects_cpu_tensors_with_reference_messages():

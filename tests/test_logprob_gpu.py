@@ -4,11 +4,10 @@ reference's fp32 eager path.
 Mirrors the reference's tests/test_logprob.py (each test names the one it
 follows) and adds the north-star bars:
   * forward: |ours - oracle| <= 1e-5 (fp32 input) / 2e-5 (bf16, fp16 input);
-  * backward: bf16/fp16 gradients within 1 ulp of the float64 oracle rounded
-    to nearest-even; fp32 gradients within 1 ulp of the row's largest
-    gradient magnitude (elementwise 1 ulp is below what an fp32 lse allows,
-    since lse itself carries half an ulp of rounding that enters every
-    exp(x - lse)).
+  * backward: every gradient element within 1 ulp of the output dtype of the
+    float64 oracle (rounded to nearest-even), except where the exact value is
+    a cancellation of larger fp32 terms; there within the fp32 evaluation
+    noise of those terms (klp_testutil.grad_check states the bound).
 All inputs are generated on the CPU from fixed seeds and copied to the GPU.
 """
 from __future__ import annotations
@@ -19,8 +18,8 @@ import numpy as np
 import pytest
 import torch
 
-from klp_testutil import (DTYPE_NAME, FWD_TOL, WIDTH, bits_of, seeded_logits, seeded_targets,
-                          storage_bits, ulp_diff)
+from klp_testutil import (FWD_TOL, grad_check, seeded_logits, seeded_targets, storage_bits,
+                          ulp_diff)
 
 pytestmark = pytest.mark.gpu
 
@@ -47,23 +46,7 @@ def _check_fwd(oracle, x_cpu, t_cpu, outs, tol, label=""):
 
 
 def _grad_ulps(oracle, x_cpu, t_cpu, lse, ent, d_ours, g_logp=None, g_ent=None, g_lse=None):
-    """Max ulp distance of the kernel's gradient to the oracle's (see module
-    docstring for the fp32 row-scale rule).  Returns (max_ulp, detail)."""
-    d_ref = oracle.backward(x_cpu, t_cpu.numpy(), lse.cpu().numpy(), ent.cpu().numpy(),
-                            g_logp=None if g_logp is None else g_logp.cpu().numpy(),
-                            g_ent=None if g_ent is None else g_ent.cpu().numpy(),
-                            g_lse=None if g_lse is None else g_lse.cpu().numpy())
-    dt = d_ours.dtype
-    if dt == torch.float32:
-        V = x_cpu.shape[-1]
-        d = d_ours.detach().cpu().double().numpy().reshape(-1, V)
-        r = d_ref.reshape(-1, V)
-        row_max = np.abs(r).max(axis=1, keepdims=True)
-        scale = np.where(row_max > 0, 2.0 ** (np.floor(np.log2(np.maximum(row_max, 1e-300))) - 23),
-                         2.0 ** -149)
-        return float((np.abs(d - r) / scale).max()), "row-scale ulps"
-    ref_bits = bits_of(oracle.round_to(d_ref, DTYPE_NAME[dt]))
-    return float(ulp_diff(storage_bits(d_ours), ref_bits, WIDTH[dt]).max()), "elementwise ulps"
+    return grad_check(oracle, x_cpu, t_cpu, lse, ent, d_ours, g_logp, g_ent, g_lse)
 
 
 # ---------------------------------------------------------------------------
@@ -240,7 +223,7 @@ def test_gradcheck_small():
 # ---------------------------------------------------------------------------
 # Launch shapes, layouts and edge cases
 # ---------------------------------------------------------------------------
-LAUNCHES = [(w, u, s, nt) for w in (4, 8) for u in (2, 4) for s in (1, 2, 3, 8) for nt in (0, 1)]
+LAUNCHES = [(w, u, s, f) for w in (4, 8, 16) for u in (2, 4) for s in (1, 2, 3, 8) for f in (0, 1)]
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -255,7 +238,7 @@ def test_every_launch_shape_matches_oracle(dtype, oracle):
     first = None
     for cfg in LAUNCHES:
         outs = [torch.empty(N, device=DEV) for _ in range(3)]
-        _C.fwd_launch(x, t, *outs, config=cfg)
+        _C.fwd_launch(x, t, *outs, config=cfg[:3] + (0,))
         _check_fwd(oracle, x_cpu, t_cpu, outs, FWD_TOL[dtype], label=f"fwd {cfg}")
         d = torch.empty_like(x)
         _C.bwd_launch(x, t, outs[2], outs[1], gl, ge, gs, d, config=cfg)
@@ -335,7 +318,7 @@ def test_out_of_range_targets(dtype, oracle):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("config", [None, (8, 4, 4, 1)])
+@pytest.mark.parametrize("config", [None, (16, 4, 4, 0)])
 def test_negative_infinity_logits(dtype, config, oracle):
     """-inf logits are skipped by the forward (the reference's sentinel rule,
     csrc/fused_logprob.cu:142-143) and get a zero gradient."""
@@ -364,7 +347,10 @@ def test_negative_infinity_logits(dtype, config, oracle):
     ge = torch.full((N,), 0.25, device=DEV)
     _C.bwd_launch(x, t, outs[2], outs[1], gl, ge, None, d)
     assert torch.isfinite(d.float()).all()
-    assert (d.float()[mask.to(DEV)] == 0).all()
+    not_target = torch.ones_like(mask)
+    not_target[torch.arange(N), t_cpu.clamp(0, V - 1)] = False
+    assert (d.float()[(mask & not_target).to(DEV)] == 0).all()
+    assert d.float()[0, t_cpu[0]].item() == 0.5  # a -inf target keeps its one-hot term
     ulps, kind = _grad_ulps(oracle, x_cpu, t_cpu, outs[2], outs[1], d, gl, ge)
     assert ulps <= 1.0, f"{kind}: {ulps}"
 
@@ -379,7 +365,7 @@ def test_special_rows(dtype):
     x[1, 17] = float("nan")
     x[2, 999] = float("inf")
     t = torch.tensor([3, 3, 3, 3], device=DEV)
-    for config in (None, (4, 2, 2, 1)):
+    for config in (None, (4, 2, 2, 0)):
         from kernel_opt import _C
         lp, h, l = [torch.empty(4, device=DEV) for _ in range(3)]
         _C.fwd_launch(x, t, lp, h, l, config=config)
@@ -422,7 +408,7 @@ def test_deterministic(dtype):
     N, V = 64, 65537
     x = seeded_logits((N, V), dtype, seed=81).to(DEV)
     t = seeded_targets((N,), V, seed=81).to(DEV)
-    for config in (None, (8, 4, 8, 1), (4, 2, 16, 0)):
+    for config in (None, (8, 4, 8, 0), (16, 2, 16, 0)):
         res = []
         for _ in range(3):
             outs = [torch.empty(N, device=DEV) for _ in range(3)]
@@ -432,9 +418,8 @@ def test_deterministic(dtype):
 
 
 def test_workspace_reuse_across_shapes(oracle):
-    """The split-row workspace is left zero-filled after every launch, so a
-    sequence of launches with different row counts and split counts on one
-    stream stays correct."""
+    """One split-row workspace reused by a sequence of launches with
+    different row counts and split counts on one stream."""
     from kernel_opt import _C
     V = 40009
     seq = [(33, 8), (200, 2), (7, 32), (200, 8), (64, 3), (33, 16), (512, 4)]
@@ -442,7 +427,7 @@ def test_workspace_reuse_across_shapes(oracle):
         x_cpu = seeded_logits((N, V), torch.bfloat16, seed=91 + i)
         t_cpu = seeded_targets((N,), V, seed=91 + i)
         outs = [torch.empty(N, device=DEV) for _ in range(3)]
-        _C.fwd_launch(x_cpu.to(DEV), t_cpu.to(DEV), *outs, config=(8, 2, s, 1))
+        _C.fwd_launch(x_cpu.to(DEV), t_cpu.to(DEV), *outs, config=(8, 2, s, 0))
         _check_fwd(oracle, x_cpu, t_cpu, outs, 2e-5, label=f"N={N} splits={s}")
 
 
@@ -460,7 +445,45 @@ def test_multiple_streams(oracle):
     for rep in range(5):
         for i in range(2):
             with torch.cuda.stream(streams[i]):
-                _C.fwd_launch(xd[i], td[i], *outs[i], config=(8, 2, 8, 1))
+                _C.fwd_launch(xd[i], td[i], *outs[i], config=(8, 2, 8, 0))
     torch.cuda.synchronize()
     for i in range(2):
         _check_fwd(oracle, xs[i], ts[i], outs[i], 2e-5, label=f"stream {i}")
+
+
+# ---------------------------------------------------------------------------
+# Committed known-answer fixtures (tests/golden/klp_golden.npz)
+# ---------------------------------------------------------------------------
+def _golden_cases():
+    from test_golden_cpu import CASES
+    return CASES
+
+
+@pytest.mark.parametrize("name", ["fp32_randn", "bf16_randn", "fp16_spiked", "bf16_neg_inf",
+                                  "fp32_tiny", "bf16_wide"])
+def test_golden_fixtures(name, oracle):
+    from klp_testutil import grad_score
+    from kernel_opt import _C
+    c = _golden_cases()[name]
+    dt = {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}[str(c["dtype"])]
+    bits = torch.from_numpy(c["logits_bits"].copy())
+    x_cpu = bits if dt == torch.float32 else bits.view(torch.int16).view(dt)
+    t_cpu = torch.from_numpy(c["targets"].copy())
+    x, t = x_cpu.to(DEV), t_cpu.to(DEV)
+    N = x.shape[0]
+    for config in (None, (16, 2, 3, 0)):
+        lp, h, l = [torch.empty(N, device=DEV) for _ in range(3)]
+        _C.fwd_launch(x, t, lp, h, l, config=config)
+        for nm, ours, exp in (("logp", lp, c["logp"]), ("entropy", h, c["entropy"]),
+                              ("lse", l, c["lse"])):
+            err = np.abs(ours.cpu().double().numpy() - exp).max()
+            assert err <= FWD_TOL[dt], f"{name} {nm} {config}: {err:.3g}"
+    lse32 = torch.from_numpy(c["lse32"].copy()).to(DEV)
+    ent32 = torch.from_numpy(c["ent32"].copy()).to(DEV)
+    gl, ge, gs = [torch.from_numpy(c[k].copy()).to(DEV) for k in ("g_logp", "g_ent", "g_lse")]
+    d = torch.empty_like(x)
+    _C.bwd_launch(x, t, lse32, ent32, gl, ge, gs, d)
+    worst, detail = grad_score(oracle, x_cpu, t_cpu, c["lse32"].astype(np.float64),
+                               c["ent32"].astype(np.float64), d, c["d"],
+                               *(c[k].astype(np.float64) for k in ("g_logp", "g_ent", "g_lse")))
+    assert worst <= 1.0, f"{name}: {detail}"
