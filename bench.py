@@ -16,16 +16,21 @@ Algorithmic bytes per launch (s = bytes per logit, N rows, V vocab):
     backward = 2*N*V*s + 8N (targets) + 16N (lse, entropy, g_logp, g_ent)
 (g_lse is None in these workloads, so it is not read.)
 
-The roofline object reports the dominant kernel (the backward: it moves
-twice the forward's bytes).  Kernel times come from HIP events recorded on
-the stream the kernels run on, around each launch, averaged over the timed
-steps.
+Timing (HIP events on the stream the kernels run on): `ms_per_step` is one
+event pair around K interleaved forward+backward steps, divided by K; the
+per-kernel `fwd_ms` / `bwd_ms` are one event pair around K back-to-back
+launches of that kernel, divided by K.  With --flush a 1 GiB buffer is
+overwritten before every launch and each launch is timed on its own.  The
+roofline object reports the dominant kernel, the backward (it moves twice the
+forward's bytes); `traffic` is the HBM bytes per launch that rocprofv3's
+FETCH_SIZE / WRITE_SIZE counters measured for that launch shape, scaled by
+their readings for a plain copy of known size (MEASURED_TRAFFIC below).
 
 The cpu_baseline leg times the reference's CPU eager path (TRL
 selective_log_softmax + entropy_from_logits forward, restated in
 oracle/eager_ref.py, plus PyTorch autograd through the eager formulas for
-the backward) on a bounded sample of rows of the same workload, on this
-machine's cores, and scales it to the full batch.
+the backward) on the same workload (C2: the whole batch, well under a
+second) on this machine's cores.
 """
 from __future__ import annotations
 
@@ -45,6 +50,15 @@ for _p in (PKG_DIR, ROOT):
 import torch  # noqa: E402
 
 HBM_PEAK_TBPS = 8.0
+
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
+# each scaled by the counter's reading for a plain copy of known size
+# (profiles/klp_C2_bf16_hbm_traffic.md).  Keyed by workload, kernel and
+# launch shape (waves, unroll, splits, flags); reported only for that shape.
+MEASURED_TRAFFIC = {
+    ("C2", "fwd", (4, 4, 1, 0)): 311760691,
+    ("C2", "bwd", (16, 2, 8, 1)): 623333215,
+}
 ROW_BLOCK = 256  # rows per seeded generator block
 
 # BASELINE.json configs.  Seeds are per config; each block of ROW_BLOCK rows
@@ -191,37 +205,6 @@ def cpu_baseline(name: str, max_rows: int, logits_gpu, targets_gpu, g_logp, g_en
                 threads=torch.get_num_threads(), scaled=b_keep < B)
 
 
-class _HipEvents:
-    """Raw HIP events from the HIP runtime torch already loaded (same soname),
-    used with klp_time_next_call for kernel-exact durations."""
-
-    def __init__(self):
-        import ctypes
-        self.ct = ctypes
-        self.hip = ctypes.CDLL("libamdhip64.so.7")
-        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
-        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
-                                                 ctypes.c_void_p]
-        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
-
-    def create(self):
-        ev = self.ct.c_void_p()
-        rc = self.hip.hipEventCreate(self.ct.byref(ev))
-        if rc != 0:
-            raise RuntimeError(f"hipEventCreate failed: {rc}")
-        return ev
-
-    def elapsed_ms(self, a, b):
-        ms = self.ct.c_float()
-        rc = self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b)
-        if rc != 0:
-            raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
-        return ms.value
-
-    def destroy(self, ev):
-        self.hip.hipEventDestroy(ev)
-
-
 # ---------------------------------------------------------------------------
 # GPU timing
 # ---------------------------------------------------------------------------
@@ -250,7 +233,6 @@ def main(argv=None):
         return 2
 
     from kernel_opt import _C
-    from kernel_opt._library import lib
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
@@ -289,40 +271,49 @@ def main(argv=None):
     torch.cuda.synchronize()
 
     K = args.steps
-    hev = _HipEvents()
-    evs = [[hev.create() for _ in range(4)] for _ in range(K)]
-    step_start = torch.cuda.Event(enable_timing=True)
-    step_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_wall0 = time.perf_counter()
-    step_start.record(stream)
-    for k in range(K):
-        if flush_buf is not None:
-            flush_buf.fill_(k & 0xFF)
-        lib.klp_time_next_call(evs[k][0], evs[k][1])
-        fwd()
-        if flush_buf is not None:
-            flush_buf.fill_((k + 1) & 0xFF)
-        lib.klp_time_next_call(evs[k][2], evs[k][3])
-        bwd()
-    step_end.record(stream)
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter() - t_wall0
 
-    fwd_ms = [hev.elapsed_ms(e[0], e[1]) for e in evs]
-    bwd_ms = [hev.elapsed_ms(e[2], e[3]) for e in evs]
-    for e in evs:
-        for x in e:
-            hev.destroy(x)
-    fwd_avg = sum(fwd_ms) / K
-    bwd_avg = sum(bwd_ms) / K
+    def timed_loop(body):
+        """Average ms of `body` over K back-to-back calls: one event pair on
+        the stream the kernels run on, around the whole loop."""
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(K):
+            body()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / K
+
+    def timed_each(fn):
+        """Per-launch ms with the Infinity Cache overwritten before each launch."""
+        ts = []
+        for k in range(K):
+            flush_buf.fill_(k & 0xFF)
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn()
+            b.record(stream)
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return sum(ts) / K
+
+    t_wall0 = time.perf_counter()
+    if flush_buf is None:
+        # the step as a training loop runs it: forward then backward, repeated
+        step_ms = timed_loop(lambda: (fwd(), bwd()))
+        # each kernel on its own, launched back to back
+        fwd_avg = timed_loop(fwd)
+        bwd_avg = timed_loop(bwd)
+    else:
+        fwd_avg = timed_each(fwd)
+        bwd_avg = timed_each(bwd)
+        step_ms = fwd_avg + bwd_avg
+    t_wall = time.perf_counter() - t_wall0
     fb, bb = algorithmic_bytes(N, V, esz)
     fwd_tbps = fb / (fwd_avg * 1e-3) / 1e12
     bwd_tbps = bb / (bwd_avg * 1e-3) / 1e12
-    if flush_buf is None:
-        step_ms = step_start.elapsed_time(step_end) / K  # includes gaps between launches
-    else:
-        step_ms = fwd_avg + bwd_avg  # the flush fills are not part of the step
     step_tbps = (fb + bb) / (step_ms * 1e-3) / 1e12
 
     cpu = None
@@ -331,15 +322,15 @@ def main(argv=None):
         sample = (f"{c['rows']} of {N} rows of {name} (the whole batch)" if not c["scaled"] else
                   f"{c['rows']} of {N} rows of {name}, scaled by {N}/{c['rows']}")
         cpu = {
-            "value": round((fb + bb) / ((c["fwd_ms"] + c["fwd_bwd_ms"]) * 1e-3) / 1e12, 6),
+            "value": round((fb + bb) / (c["fwd_bwd_ms"] * 1e-3) / 1e12, 6),
             "unit": "TB/s",
             "cores": c["threads"],
             "kind": "port",
             "sample": (f"{sample}; torch CPU, {c['threads']} threads, median of 3 after one "
-                       f"warm-up: TRL-eager forward (restated, oracle/eager_ref.py) "
-                       f"{c['fwd_ms']:.1f} ms + eager fwd with autograd bwd "
-                       f"{c['fwd_bwd_ms']:.1f} ms per batch; value = the step's algorithmic "
-                       f"bytes over their sum"),
+                       f"warm-up.  Step = eager forward + autograd backward "
+                       f"{c['fwd_bwd_ms']:.1f} ms (value = the step's algorithmic bytes over "
+                       f"it); the TRL-eager forward alone (restated, oracle/eager_ref.py) "
+                       f"takes {c['fwd_ms']:.1f} ms"),
             "fwd_ms": round(c["fwd_ms"], 3),
             "fwd_bwd_ms": round(c["fwd_bwd_ms"], 3),
         }
@@ -369,8 +360,6 @@ def main(argv=None):
                    "infinity_cache": "flushed" if args.flush else "warm"},
         "fwd_ms": round(fwd_avg, 5),
         "bwd_ms": round(bwd_avg, 5),
-        "fwd_ms_median": round(sorted(fwd_ms)[K // 2], 5),
-        "bwd_ms_median": round(sorted(bwd_ms)[K // 2], 5),
         "fwd_tbps": round(fwd_tbps, 4),
         "bwd_tbps": round(bwd_tbps, 4),
         "fwd_pct_peak": round(100 * fwd_tbps / HBM_PEAK_TBPS, 2),
@@ -385,8 +374,10 @@ def main(argv=None):
             "peak": HBM_PEAK_TBPS * 1000,
             "unit": "GB/s",
             "frac": round(bwd_tbps / HBM_PEAK_TBPS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC.get((name, "bwd", tuple(bwd_used))),
             "algorithmic_bytes": bb,
+            "fwd_traffic": MEASURED_TRAFFIC.get((name, "fwd", tuple(fwd_used))),
+            "fwd_algorithmic_bytes": fb,
         },
         "cpu_baseline": cpu,
     }

@@ -20,13 +20,7 @@ namespace {
 
 thread_local std::string g_last_error;
 thread_local int g_fail_next = 0;
-thread_local klp::Timing g_timing;  // consumed by the next compute call
 
-klp::Timing take_timing() {
-    const klp::Timing t = g_timing;
-    g_timing = klp::Timing{};
-    return t;
-}
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -51,9 +45,10 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 // (16 per CU on 256 CUs) so that enough 16-byte loads are in flight to cover
 // HBM latency; rows are split across workgroups only when a whole 1024-thread
 // workgroup per row still leaves the chip short of that.  Backward: splitting
-// needs no second pass, so it aims at kBwdTargetBlocks workgroups.
+// needs no second pass; see default_bwd_config.
 constexpr int64_t kFwdTargetWaves = 4096;
 constexpr int64_t kBwdTargetBlocks = 8192;
+constexpr int kBwdMinSplits = 8;
 constexpr int kMaxSplits = 64;
 
 // Shared checks of the row-addressed logits operand.
@@ -129,8 +124,12 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     c.splits = 1;
     const int64_t nvec = body_vectors(dtype, vocab);
     const int64_t tile = static_cast<int64_t>(c.waves) * 64 * c.unroll;
-    while (c.splits < kMaxSplits && n_rows * c.splits < kBwdTargetBlocks &&
-           nvec / (2 * c.splits) >= tile)
+    // Up to 8 pieces per row whatever the batch: resident workgroups then
+    // cover a narrower address window, which measured faster for this mixed
+    // read/write stream (C4: 5.46 vs 5.13 TB/s).  Beyond 8, split only while
+    // the grid is short of kBwdTargetBlocks.
+    while (c.splits < kMaxSplits && nvec / (2 * c.splits) >= tile &&
+           (c.splits < kBwdMinSplits || n_rows * c.splits < kBwdTargetBlocks))
         c.splits *= 2;
     return c;
 }
@@ -187,7 +186,7 @@ int fwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     p.splits = cfg.splits;
     p.partials = (cfg.splits > 1) ? static_cast<float*>(workspace) : nullptr;
     if (injected_failure("forward")) return KLP_ELAUNCH;
-    return after_launch(klp::launch_fwd(dtype, p, cfg, take_timing(), static_cast<hipStream_t>(stream)),
+    return after_launch(klp::launch_fwd(dtype, p, cfg, static_cast<hipStream_t>(stream)),
                         "forward");
 }
 
@@ -227,7 +226,7 @@ int bwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     p.d_logits = d_logits;
     p.splits = cfg.splits;
     if (injected_failure("backward")) return KLP_ELAUNCH;
-    return after_launch(klp::launch_bwd(dtype, p, cfg, take_timing(), static_cast<hipStream_t>(stream)),
+    return after_launch(klp::launch_bwd(dtype, p, cfg, static_cast<hipStream_t>(stream)),
                         "backward");
 }
 
@@ -248,11 +247,6 @@ size_t klp_last_error(char* buf, size_t len) {
 }
 
 void klp_debug_fail_next_launches(int count) { g_fail_next = count > 0 ? count : 0; }
-
-void klp_time_next_call(void* start_event, void* stop_event) {
-    g_timing.start = static_cast<hipEvent_t>(start_event);
-    g_timing.stop = static_cast<hipEvent_t>(stop_event);
-}
 
 size_t klp_fwd_workspace_bytes(int dtype, int64_t n_rows, int64_t vocab) {
     if (dtype != KLP_BF16 && dtype != KLP_FP16 && dtype != KLP_FP32) return 0;
@@ -307,7 +301,7 @@ int klp_fwd_naive(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
     p.entropy = entropy;
     p.lse = lse;
     if (injected_failure("naive forward")) return KLP_ELAUNCH;
-    return after_launch(klp::launch_fwd_naive(dtype, p, take_timing(), static_cast<hipStream_t>(stream)),
+    return after_launch(klp::launch_fwd_naive(dtype, p, static_cast<hipStream_t>(stream)),
                         "naive forward");
 }
 

@@ -127,20 +127,19 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
 }
 
 template <int DT, int WAVES, int U, bool kNtStore>
-static hipError_t launch_bwd_t(const BwdParams& p, const Timing& tm, hipStream_t stream) {
+static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
     return launch_kernel(klp_bwd_kernel<DT, WAVES, U, kNtStore>,
                          dim3(static_cast<unsigned>(p.n_rows * p.splits)), dim3(WAVES * 64),
-                         stream, tm.start, tm.stop, p);
+                         stream, p);
 }
 
 template <int DT>
-static hipError_t launch_bwd_dt(const BwdParams& p, const BwdConfig& c, const Timing& tm,
-                                hipStream_t stream) {
+static hipError_t launch_bwd_dt(const BwdParams& p, const BwdConfig& c, hipStream_t stream) {
     const bool nt = (c.flags & kFlagNtStore) != 0;
 #define KLP_BWD_CASE(W, U)                                                     \
     if (c.waves == W && c.unroll == U)                                         \
-        return nt ? launch_bwd_t<DT, W, U, true>(p, tm, stream)                \
-                  : launch_bwd_t<DT, W, U, false>(p, tm, stream);
+        return nt ? launch_bwd_t<DT, W, U, true>(p, stream)                \
+                  : launch_bwd_t<DT, W, U, false>(p, stream);
     KLP_BWD_CASE(4, 2)
     KLP_BWD_CASE(4, 4)
     KLP_BWD_CASE(8, 2)
@@ -151,12 +150,11 @@ static hipError_t launch_bwd_dt(const BwdParams& p, const BwdConfig& c, const Ti
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, const Timing& tm,
-                      hipStream_t stream) {
+hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, hipStream_t stream) {
     switch (dtype) {
-        case kBF16: return launch_bwd_dt<kBF16>(p, c, tm, stream);
-        case kFP16: return launch_bwd_dt<kFP16>(p, c, tm, stream);
-        case kFP32: return launch_bwd_dt<kFP32>(p, c, tm, stream);
+        case kBF16: return launch_bwd_dt<kBF16>(p, c, stream);
+        case kFP16: return launch_bwd_dt<kFP16>(p, c, stream);
+        case kFP32: return launch_bwd_dt<kFP32>(p, c, stream);
         default: return hipErrorInvalidValue;
     }
 }

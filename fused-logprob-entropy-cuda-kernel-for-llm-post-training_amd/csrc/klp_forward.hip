@@ -207,25 +207,22 @@ __global__ __launch_bounds__(128) void klp_fwd_naive_kernel(NaiveParams p) {
 // Launchers
 // ---------------------------------------------------------------------------
 template <int DT, int WAVES, int U>
-static hipError_t launch_fwd_t(const FwdParams& p, const Timing& tm, hipStream_t stream) {
+static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
     if (p.splits == 1)
         return launch_kernel(klp_fwd_kernel<DT, WAVES, U, false>,
-                             dim3(static_cast<unsigned>(p.n_rows)), dim3(WAVES * 64), stream,
-                             tm.start, tm.stop, p);
+                             dim3(static_cast<unsigned>(p.n_rows)), dim3(WAVES * 64), stream, p);
     hipError_t e = launch_kernel(klp_fwd_kernel<DT, WAVES, U, true>,
                                  dim3(static_cast<unsigned>(p.n_rows * p.splits)),
-                                 dim3(WAVES * 64), stream, tm.start, nullptr, p);
+                                 dim3(WAVES * 64), stream, p);
     if (e != hipSuccess) return e;
     return launch_kernel(klp_fwd_combine_kernel<DT>,
-                         dim3(static_cast<unsigned>((p.n_rows + 255) / 256)), dim3(256), stream,
-                         nullptr, tm.stop, p);
+                         dim3(static_cast<unsigned>((p.n_rows + 255) / 256)), dim3(256), stream, p);
 }
 
 template <int DT>
-static hipError_t launch_fwd_dt(const FwdParams& p, const FwdConfig& c, const Timing& tm,
-                                hipStream_t stream) {
+static hipError_t launch_fwd_dt(const FwdParams& p, const FwdConfig& c, hipStream_t stream) {
 #define KLP_FWD_CASE(W, U) \
-    if (c.waves == W && c.unroll == U) return launch_fwd_t<DT, W, U>(p, tm, stream);
+    if (c.waves == W && c.unroll == U) return launch_fwd_t<DT, W, U>(p, stream);
     KLP_FWD_CASE(4, 2)
     KLP_FWD_CASE(4, 4)
     KLP_FWD_CASE(8, 2)
@@ -236,12 +233,11 @@ static hipError_t launch_fwd_dt(const FwdParams& p, const FwdConfig& c, const Ti
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, const Timing& tm,
-                      hipStream_t stream) {
+hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream) {
     switch (dtype) {
-        case kBF16: return launch_fwd_dt<kBF16>(p, c, tm, stream);
-        case kFP16: return launch_fwd_dt<kFP16>(p, c, tm, stream);
-        case kFP32: return launch_fwd_dt<kFP32>(p, c, tm, stream);
+        case kBF16: return launch_fwd_dt<kBF16>(p, c, stream);
+        case kFP16: return launch_fwd_dt<kFP16>(p, c, stream);
+        case kFP32: return launch_fwd_dt<kFP32>(p, c, stream);
         default: return hipErrorInvalidValue;
     }
 }
@@ -252,16 +248,12 @@ bool fwd_config_supported(const FwdConfig& c) {
     return w && u;
 }
 
-hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, const Timing& tm,
-                            hipStream_t stream) {
+hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((p.n_rows + 127) / 128));
     switch (dtype) {
-        case kBF16: return launch_kernel(klp_fwd_naive_kernel<kBF16>, grid, dim3(128), stream,
-                                         tm.start, tm.stop, p);
-        case kFP16: return launch_kernel(klp_fwd_naive_kernel<kFP16>, grid, dim3(128), stream,
-                                         tm.start, tm.stop, p);
-        case kFP32: return launch_kernel(klp_fwd_naive_kernel<kFP32>, grid, dim3(128), stream,
-                                         tm.start, tm.stop, p);
+        case kBF16: return launch_kernel(klp_fwd_naive_kernel<kBF16>, grid, dim3(128), stream, p);
+        case kFP16: return launch_kernel(klp_fwd_naive_kernel<kFP16>, grid, dim3(128), stream, p);
+        case kFP32: return launch_kernel(klp_fwd_naive_kernel<kFP32>, grid, dim3(128), stream, p);
         default: return hipErrorInvalidValue;
     }
 }

@@ -2,7 +2,6 @@
 // the kernel translation units and the C-ABI dispatcher (klp_abi.hip).
 #pragma once
 
-#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -62,31 +61,16 @@ struct FwdConfig {
 typedef FwdConfig BwdConfig;
 constexpr int kFlagNtStore = 1;
 
-// Optional timing events: when set, the first kernel of a call records
-// `start` as it begins and the last one records `stop` as it ends
-// (hipExtLaunchKernel), so the elapsed time is kernel execution only.
-struct Timing {
-    hipEvent_t start = nullptr;
-    hipEvent_t stop = nullptr;
-};
-
 template <typename... KArgs, typename... Args>
 inline hipError_t launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block,
-                                hipStream_t stream, hipEvent_t start, hipEvent_t stop,
-                                Args... args) {
-    if (start != nullptr || stop != nullptr)
-        hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0, args...);
-    else
-        hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+                                hipStream_t stream, Args... args) {
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
     return hipGetLastError();
 }
 
-hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, const Timing& tm,
-                      hipStream_t stream);
-hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, const Timing& tm,
-                            hipStream_t stream);
-hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, const Timing& tm,
-                      hipStream_t stream);
+hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream);
+hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream);
+hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, hipStream_t stream);
 bool fwd_config_supported(const FwdConfig& c);
 bool bwd_config_supported(const BwdConfig& c);
 

@@ -43,7 +43,6 @@ SIGNATURES = {
     "klp_fwd_ex": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _sz, _i32, _i32, _i32, _i32, _vp]),
     "klp_bwd_ex": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                   _vp]),
-    "klp_time_next_call": (None, [_vp, _vp]),
     "klp_default_config": (None, [_i32, _i32, _i64, _i64] + [ctypes.POINTER(_i32)] * 4),
 }
 

@@ -46,15 +46,6 @@ int klp_bwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                int waves, int unroll, int splits, int flags,
                void* stream);
 
-/*
- * Kernel-exact timing for benchmarks: the next compute call on the calling
- * thread (klp_fwd*, klp_fwd_naive, klp_bwd*) records `start_event` when its
- * first kernel starts executing and `stop_event` when its last kernel ends
- * (hipExtLaunchKernel), instead of at enqueue.  Both are hipEvent_t created
- * with timing enabled; either may be NULL.  One call consumes the setting.
- */
-void klp_time_next_call(void* start_event, void* stop_event);
-
 /* The launch shape klp_fwd (which = 0) or klp_bwd (which = 1) would pick. */
 void klp_default_config(int which, int dtype, int64_t n_rows, int64_t vocab,
                         int* waves, int* unroll, int* splits, int* flags);
