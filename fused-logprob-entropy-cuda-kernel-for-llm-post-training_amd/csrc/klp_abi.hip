@@ -8,6 +8,7 @@
 // reference has none).  Nothing here allocates, frees or synchronises.
 #include <stdarg.h>
 #include <stdio.h>
+#include <math.h>
 #include <string.h>
 
 #include <string>
@@ -139,6 +140,18 @@ size_t workspace_bytes_for(int64_t n_rows, int splits) {
     return static_cast<size_t>(n_rows) * static_cast<size_t>(splits) * 4 * sizeof(float);
 }
 
+// 1/temperature rounded once to fp32; rejects temperatures that are not
+// finite and positive.
+bool scale_from_temperature(float temperature, float* scale) {
+    if (!(temperature > 0.0f) || temperature == INFINITY) {
+        fail(KLP_EINVAL, "temperature must be finite and > 0, got %g",
+             static_cast<double>(temperature));
+        return false;
+    }
+    *scale = static_cast<float>(1.0 / static_cast<double>(temperature));
+    return true;
+}
+
 int check_grid(int64_t n_rows, int splits, int threads) {
     const int64_t blocks = n_rows * splits;
     if (blocks > (int64_t{1} << 31) - 1 || blocks * threads > (int64_t{1} << 32) - 1)
@@ -150,7 +163,7 @@ int check_grid(int64_t n_rows, int splits, int threads) {
 int fwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t rows_inner,
              int64_t stride_outer, int64_t stride_inner, const int64_t* targets, float* logprob,
              float* entropy, float* lse, void* workspace, size_t workspace_bytes,
-             klp::FwdConfig cfg, void* stream) {
+             klp::FwdConfig cfg, float scale, void* stream) {
     int rc = check_rows(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
                         targets);
     if (rc != KLP_OK) return rc;
@@ -185,6 +198,7 @@ int fwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     p.lse = lse;
     p.splits = cfg.splits;
     p.partials = (cfg.splits > 1) ? static_cast<float*>(workspace) : nullptr;
+    p.scale = scale;
     if (injected_failure("forward")) return KLP_ELAUNCH;
     return after_launch(klp::launch_fwd(dtype, p, cfg, static_cast<hipStream_t>(stream)),
                         "forward");
@@ -193,7 +207,7 @@ int fwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
 int bwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t rows_inner,
              int64_t stride_outer, int64_t stride_inner, const int64_t* targets, const float* lse,
              const float* entropy, const float* g_logp, const float* g_ent, const float* g_lse,
-             void* d_logits, klp::BwdConfig cfg, void* stream) {
+             void* d_logits, klp::BwdConfig cfg, float scale, void* stream) {
     int rc = check_rows(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
                         targets);
     if (rc != KLP_OK) return rc;
@@ -225,6 +239,7 @@ int bwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     p.g_lse = g_lse;
     p.d_logits = d_logits;
     p.splits = cfg.splits;
+    p.scale = scale;
     if (injected_failure("backward")) return KLP_ELAUNCH;
     return after_launch(klp::launch_bwd(dtype, p, cfg, static_cast<hipStream_t>(stream)),
                         "backward");
@@ -264,7 +279,7 @@ int klp_fwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_
             float* entropy, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
     klp::FwdConfig cfg = default_fwd_config(dtype, n_rows, vocab);
     return fwd_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner, targets,
-                    logprob, entropy, lse, workspace, workspace_bytes, cfg, stream);
+                    logprob, entropy, lse, workspace, workspace_bytes, cfg, 1.0f, stream);
 }
 
 int klp_fwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t rows_inner,
@@ -277,7 +292,7 @@ int klp_fwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int
     cfg.splits = splits;
     cfg.flags = flags;
     return fwd_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner, targets,
-                    logprob, entropy, lse, workspace, workspace_bytes, cfg, stream);
+                    logprob, entropy, lse, workspace, workspace_bytes, cfg, 1.0f, stream);
 }
 
 int klp_fwd_naive(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
@@ -311,7 +326,29 @@ int klp_bwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_
             void* d_logits, void* stream) {
     klp::BwdConfig cfg = default_bwd_config(dtype, n_rows, vocab);
     return bwd_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner, targets,
-                    lse, entropy, g_logp, g_ent, g_lse, d_logits, cfg, stream);
+                    lse, entropy, g_logp, g_ent, g_lse, d_logits, cfg, 1.0f, stream);
+}
+
+int klp_fwd_temp(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t rows_inner,
+                 int64_t stride_outer, int64_t stride_inner, const int64_t* targets,
+                 float temperature, float* logprob, float* entropy, float* lse, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+    float scale;
+    if (!scale_from_temperature(temperature, &scale)) return KLP_EINVAL;
+    klp::FwdConfig cfg = default_fwd_config(dtype, n_rows, vocab);
+    return fwd_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner, targets,
+                    logprob, entropy, lse, workspace, workspace_bytes, cfg, scale, stream);
+}
+
+int klp_bwd_temp(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t rows_inner,
+                 int64_t stride_outer, int64_t stride_inner, const int64_t* targets,
+                 float temperature, const float* lse, const float* entropy, const float* g_logp,
+                 const float* g_ent, const float* g_lse, void* d_logits, void* stream) {
+    float scale;
+    if (!scale_from_temperature(temperature, &scale)) return KLP_EINVAL;
+    klp::BwdConfig cfg = default_bwd_config(dtype, n_rows, vocab);
+    return bwd_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner, targets,
+                    lse, entropy, g_logp, g_ent, g_lse, d_logits, cfg, scale, stream);
 }
 
 int klp_bwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t rows_inner,
@@ -325,7 +362,7 @@ int klp_bwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int
     cfg.splits = splits;
     cfg.flags = flags;
     return bwd_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner, targets,
-                    lse, entropy, g_logp, g_ent, g_lse, d_logits, cfg, stream);
+                    lse, entropy, g_logp, g_ent, g_lse, d_logits, cfg, 1.0f, stream);
 }
 
 void klp_default_config(int which, int dtype, int64_t n_rows, int64_t vocab, int* waves,

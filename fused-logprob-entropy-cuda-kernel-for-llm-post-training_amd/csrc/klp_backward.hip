@@ -12,6 +12,9 @@
 // rounded head and its exact fma remainder, so the exponent carries one
 // rounding.  A -inf logit gets a gradient of exactly 0 (p = 0), where the
 // reference's 0 * inf gives NaN; lp is clamped for that.
+//
+// With a temperature T (BwdParams::scale = 1/T != 1) the logits are scaled by
+// 1/T on load, as in the forward, and the gradient is multiplied by 1/T.
 #include "klp_device.h"
 #include "klp_launch.h"
 
@@ -21,6 +24,8 @@ struct RowGrad {
     float lse, lse_hi, lse_lo, g_ent, g_logp, c0;
 };
 
+// Gradient with respect to the (temperature-scaled) logit x; the chain-rule
+// factor 1/T for the unscaled logit is applied by the caller.
 __device__ __forceinline__ float grad_one(float x, const RowGrad& g) {
     const float lp = fmax_nan(x - g.lse, kNegBig);
     const float arg = fmaf(x, kLog2e, -g.lse_hi) - g.lse_lo;
@@ -28,7 +33,7 @@ __device__ __forceinline__ float grad_one(float x, const RowGrad& g) {
     return p * fmaf(-g.g_ent, lp, g.c0);
 }
 
-template <int DT, int WAVES, int U, bool kNtStore>
+template <int DT, int WAVES, int U, bool kNtStore, bool kScaled>
 __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
     typedef typename Traits<DT>::elem elem;
     constexpr int NTHREADS = WAVES * 64;
@@ -64,8 +69,11 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
         int64_t e = b + per;
         if (e > vocab) e = vocab;
         for (int64_t v = b + tid; v < e; v += NTHREADS) {
-            float d = grad_one(to_f32<DT>(rp[v]), g);
+            float x = to_f32<DT>(rp[v]);
+            if (kScaled) x *= p.scale;
+            float d = grad_one(x, g);
             if (v == tgt) d += g.g_logp;
+            if (kScaled) d *= p.scale;
             dp[v] = from_f32<DT>(d);
         }
         return;
@@ -80,8 +88,11 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
         const int64_t n_edge = head + (vocab - tail_begin);
         if (tid < n_edge) {
             const int64_t v = (tid < head) ? tid : tail_begin + (tid - head);
-            float d = grad_one(to_f32<DT>(rp[v]), g);
+            float x = to_f32<DT>(rp[v]);
+            if (kScaled) x *= p.scale;
+            float d = grad_one(x, g);
             if (v == tgt) d += g.g_logp;
+            if (kScaled) d *= p.scale;
             dp[v] = from_f32<DT>(d);
         }
     }
@@ -113,11 +124,15 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
                 float x[EPV];
                 unpack<DT>(v[u], x);
 #pragma unroll
-                for (int j = 0; j < EPV; ++j) x[j] = grad_one(x[j], g);
+                for (int j = 0; j < EPV; ++j) x[j] = grad_one(kScaled ? x[j] * p.scale : x[j], g);
                 if (idx == t_vec) {
 #pragma unroll
                     for (int j = 0; j < EPV; ++j)
                         if (j == t_lane_elem) x[j] += g.g_logp;
+                }
+                if (kScaled) {
+#pragma unroll
+                    for (int j = 0; j < EPV; ++j) x[j] *= p.scale;
                 }
                 if constexpr (kNtStore) __builtin_nontemporal_store(pack<DT>(x), vout + idx);
                 else vout[idx] = pack<DT>(x);
@@ -128,7 +143,11 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
 
 template <int DT, int WAVES, int U, bool kNtStore>
 static hipError_t launch_bwd_t(const BwdParams& p, hipStream_t stream) {
-    return launch_kernel(klp_bwd_kernel<DT, WAVES, U, kNtStore>,
+    if (p.scale != 1.0f)
+        return launch_kernel(klp_bwd_kernel<DT, WAVES, U, kNtStore, true>,
+                             dim3(static_cast<unsigned>(p.n_rows * p.splits)),
+                             dim3(WAVES * 64), stream, p);
+    return launch_kernel(klp_bwd_kernel<DT, WAVES, U, kNtStore, false>,
                          dim3(static_cast<unsigned>(p.n_rows * p.splits)), dim3(WAVES * 64),
                          stream, p);
 }

@@ -13,6 +13,9 @@
 //    one (head / tail) are read as scalars by split 0;
 //  - every U*16 bytes cost one rescale plus one v_exp_f32 per element
 //    (absorb() in klp_device.h);
+//  - with a temperature T (FwdParams::scale = 1/T != 1) every logit is
+//    multiplied by 1/T in fp32 as it is loaded, which fuses the GRPO trainer's
+//    separate `logits.div_(temperature)` pass (reference trainer.py:101);
 //  - lanes merge with xor-shuffles, waves through LDS in wave order, splits
 //    through a workspace in split order, so results do not depend on timing.
 #include "klp_device.h"
@@ -20,11 +23,11 @@
 
 namespace klp {
 
-template <int DT, bool kClamp, int U, int NTHREADS>
+template <int DT, bool kClamp, int U, int NTHREADS, bool kScaled>
 __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT>::elem* rp,
                                                const u32x4* vp, int64_t head, int64_t tail_begin,
                                                int64_t vocab, bool with_edges, int64_t vb,
-                                               int64_t ve, int tid) {
+                                               int64_t ve, int tid, float scale) {
     constexpr int EPV = Traits<DT>::kPerVec;
     // Scalar head / tail elements (fewer than 2 * EPV of them).
     if (with_edges) {
@@ -32,6 +35,7 @@ __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT
         if (tid < n_edge) {
             const int64_t idx = (tid < head) ? tid : tail_begin + (tid - head);
             float x = to_f32<DT>(rp[idx]);
+            if (kScaled) x *= scale;
             absorb<1, true>(s, &x);
         }
     }
@@ -45,6 +49,10 @@ __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT
         float x[U * EPV];
 #pragma unroll
         for (int u = 0; u < U; ++u) unpack<DT>(v[u], x + u * EPV);
+        if (kScaled) {
+#pragma unroll
+            for (int j = 0; j < U * EPV; ++j) x[j] *= scale;
+        }
         absorb<U * EPV, kClamp>(s, x);
         i += step;
     }
@@ -65,11 +73,15 @@ __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT
         float x[U * EPV];
 #pragma unroll
         for (int u = 0; u < U; ++u) unpack<DT>(v[u], x + u * EPV);
+        if (kScaled) {
+#pragma unroll
+            for (int j = 0; j < U * EPV; ++j) x[j] *= scale;
+        }
         absorb<U * EPV, true>(s, x);
     }
 }
 
-template <int DT, int WAVES, int U, bool kSplit>
+template <int DT, int WAVES, int U, bool kSplit, bool kScaled>
 __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     typedef typename Traits<DT>::elem elem;
     constexpr int NTHREADS = WAVES * 64;
@@ -91,7 +103,7 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     float x_target = 0.0f;
     if (!kSplit && tid == 0) {
         const int64_t tgt = p.targets[row];
-        if (tgt >= 0 && tgt < vocab) x_target = to_f32<DT>(rp[tgt]);
+        if (tgt >= 0 && tgt < vocab) x_target = to_f32<DT>(rp[tgt]) * p.scale;
     }
 
     const uintptr_t addr = reinterpret_cast<uintptr_t>(rp);
@@ -111,14 +123,14 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     }
 
     Stat s = stat_empty();
-    scan_row_piece<DT, false, U, NTHREADS>(s, rp, vp, head, tail_begin, vocab, split == 0, vb,
-                                           ve, tid);
+    scan_row_piece<DT, false, U, NTHREADS, kScaled>(s, rp, vp, head, tail_begin, vocab,
+                                                    split == 0, vb, ve, tid, p.scale);
     if (needs_clamped_rescan(s)) {
         // This lane met a -inf logit: redo its values with -inf excluded, as
         // the reference's sentinel rule does (csrc/fused_logprob.cu:142-143).
         s = stat_empty();
-        scan_row_piece<DT, true, U, NTHREADS>(s, rp, vp, head, tail_begin, vocab, split == 0, vb,
-                                              ve, tid);
+        scan_row_piece<DT, true, U, NTHREADS, kScaled>(s, rp, vp, head, tail_begin, vocab,
+                                                       split == 0, vb, ve, tid, p.scale);
     }
 
     s = wave_reduce(s);
@@ -156,7 +168,7 @@ __global__ __launch_bounds__(256) void klp_fwd_combine_kernel(FwdParams p) {
     if (row >= p.n_rows) return;
     const elem* rp = static_cast<const elem*>(p.logits) + row_offset(p.rm, row);
     const int64_t tgt = p.targets[row];
-    const float x_target = (tgt >= 0 && tgt < p.vocab) ? to_f32<DT>(rp[tgt]) : 0.0f;
+    const float x_target = (tgt >= 0 && tgt < p.vocab) ? to_f32<DT>(rp[tgt]) * p.scale : 0.0f;
     const float4* part = reinterpret_cast<const float4*>(p.partials) + row * p.splits;
     Stat acc = stat_empty();
     for (int k = 0; k < p.splits; ++k) {
@@ -206,12 +218,12 @@ __global__ __launch_bounds__(128) void klp_fwd_naive_kernel(NaiveParams p) {
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
-template <int DT, int WAVES, int U>
+template <int DT, int WAVES, int U, bool kScaled>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
     if (p.splits == 1)
-        return launch_kernel(klp_fwd_kernel<DT, WAVES, U, false>,
+        return launch_kernel(klp_fwd_kernel<DT, WAVES, U, false, kScaled>,
                              dim3(static_cast<unsigned>(p.n_rows)), dim3(WAVES * 64), stream, p);
-    hipError_t e = launch_kernel(klp_fwd_kernel<DT, WAVES, U, true>,
+    hipError_t e = launch_kernel(klp_fwd_kernel<DT, WAVES, U, true, kScaled>,
                                  dim3(static_cast<unsigned>(p.n_rows * p.splits)),
                                  dim3(WAVES * 64), stream, p);
     if (e != hipSuccess) return e;
@@ -221,8 +233,11 @@ static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
 
 template <int DT>
 static hipError_t launch_fwd_dt(const FwdParams& p, const FwdConfig& c, hipStream_t stream) {
-#define KLP_FWD_CASE(W, U) \
-    if (c.waves == W && c.unroll == U) return launch_fwd_t<DT, W, U>(p, stream);
+    const bool scaled = (p.scale != 1.0f);
+#define KLP_FWD_CASE(W, U)                                                     \
+    if (c.waves == W && c.unroll == U)                                         \
+        return scaled ? launch_fwd_t<DT, W, U, true>(p, stream)                \
+                      : launch_fwd_t<DT, W, U, false>(p, stream);
     KLP_FWD_CASE(4, 2)
     KLP_FWD_CASE(4, 4)
     KLP_FWD_CASE(8, 2)

@@ -20,6 +20,7 @@ struct FwdParams {
     float* lse;
     float* partials;  // [n_rows * splits] float4 (m, z, t, unused) when splits > 1
     int splits;
+    float scale;      // 1 / temperature; logits are multiplied by it on load
 };
 
 struct NaiveParams {
@@ -46,6 +47,7 @@ struct BwdParams {
     const float* g_lse;   // nullable
     void* d_logits;       // dense [n_rows, vocab]
     int splits;
+    float scale;          // 1 / temperature (gradient is w.r.t. the unscaled logits)
 };
 
 // Launch shape: `waves` wave64s per workgroup, `unroll` 16-byte loads per

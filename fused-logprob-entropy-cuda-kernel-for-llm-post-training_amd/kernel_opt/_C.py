@@ -123,11 +123,22 @@ def _common_forward_checks(logits, targets, logprob, entropy, lse_out, per_outpu
     return rows, N, V
 
 
-def fwd_launch(logits, targets, logprob, entropy, lse_out, config=None) -> None:
+def _temperature(temperature, config):
+    if temperature is None or float(temperature) == 1.0:
+        return None
+    _require(config is None, "a launch shape cannot be pinned together with a temperature")
+    t = float(temperature)
+    _require(t > 0.0 and t != float("inf"), f"temperature must be finite and > 0, got {t}")
+    return t
+
+
+def fwd_launch(logits, targets, logprob, entropy, lse_out, config=None, temperature=None) -> None:
     """Forward into caller-allocated outputs.  ``config`` = ``(waves, unroll,
     splits, flags)`` pins a launch shape (tuning ABI); ``None`` lets the
-    native dispatcher choose."""
+    native dispatcher choose.  ``temperature`` T divides the logits (as
+    x * fp32(1/T)) inside the kernel."""
     rows, N, V = _common_forward_checks(logits, targets, logprob, entropy, lse_out, False)
+    temp = _temperature(temperature, config)
     if N == 0:
         return
     code = DTYPE_CODES[logits.dtype]
@@ -142,7 +153,9 @@ def fwd_launch(logits, targets, logprob, entropy, lse_out, config=None) -> None:
         args = [_ptr(logits), code, N, V, rows[0], rows[1], rows[2], _ptr(targets),
                 _ptr(logprob), _ptr(entropy), _ptr(lse_out), _ptr(ws),
                 0 if ws is None else ws.numel()]
-        if config is None:
+        if temp is not None:
+            rc = lib.klp_fwd_temp(*args[:8], temp, *args[8:], ctypes.c_void_p(stream.cuda_stream))
+        elif config is None:
             rc = lib.klp_fwd(*args, ctypes.c_void_p(stream.cuda_stream))
         else:
             w, u, sp, fl = (int(c) for c in config)
@@ -196,9 +209,12 @@ def _backward_checks(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logi
 
 
 def bwd_launch(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits,
-               config=None) -> None:
-    """Backward into caller-allocated ``d_logits``; ``config`` as in fwd_launch."""
+               config=None, temperature=None) -> None:
+    """Backward into caller-allocated ``d_logits``; ``config`` and
+    ``temperature`` as in fwd_launch (the gradient is with respect to the
+    unscaled logits)."""
     rows, N, V = _backward_checks(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits)
+    temp = _temperature(temperature, config)
     if N == 0:
         return
     dev = logits.device
@@ -207,7 +223,9 @@ def bwd_launch(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits,
         args = [_ptr(logits), DTYPE_CODES[logits.dtype], N, V, rows[0], rows[1], rows[2],
                 _ptr(targets), _ptr(lse), _ptr(entropy), _ptr(g_logp), _ptr(g_ent),
                 _ptr(g_lse), _ptr(d_logits)]
-        if config is None:
+        if temp is not None:
+            rc = lib.klp_bwd_temp(*args[:8], temp, *args[8:], ctypes.c_void_p(stream.cuda_stream))
+        elif config is None:
             rc = lib.klp_bwd(*args, ctypes.c_void_p(stream.cuda_stream))
         else:
             w, u, sp, fl = (int(c) for c in config)

@@ -37,6 +37,8 @@ SIGNATURES = {
     "klp_fwd": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "klp_fwd_naive": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp]),
     "klp_bwd": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "klp_fwd_temp": (_i32, _ROWS + [_vp, ctypes.c_float, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "klp_bwd_temp": (_i32, _ROWS + [_vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "klp_debug_fail_next_launches": (None, [_i32]),
     # include/kernel_opt_hip_tuning.h
     "klp_fwd_workspace_bytes_ex": (_sz, [_i64, _i32]),

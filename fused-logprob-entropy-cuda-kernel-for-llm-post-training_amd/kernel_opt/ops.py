@@ -54,11 +54,12 @@ def fused_logprob_entropy_naive(logits: torch.Tensor, targets: torch.Tensor):
     return logprob, entropy, lse
 
 
-def fused_logprob_entropy_forward(logits: torch.Tensor, targets: torch.Tensor):
+def fused_logprob_entropy_forward(logits: torch.Tensor, targets: torch.Tensor,
+                                  temperature: float | None = None):
     """Forward only (no autograd).  Use in benches / no-grad paths."""
     _check_inputs(logits, targets)
     logprob, entropy, lse = _alloc_outputs(targets)
-    _C.fused_logprob_entropy_v1(logits, targets, logprob, entropy, lse)
+    _C.fwd_launch(logits, targets, logprob, entropy, lse, temperature=temperature)
     return logprob, entropy, lse
 
 
@@ -73,11 +74,12 @@ class _FusedLogprobEntropy(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, logits, targets):
+    def forward(ctx, logits, targets, temperature=None):
         _check_inputs(logits, targets)
         logprob, entropy, lse = _alloc_outputs(targets)
-        _C.fused_logprob_entropy_v1(logits, targets, logprob, entropy, lse)
+        _C.fwd_launch(logits, targets, logprob, entropy, lse, temperature=temperature)
         ctx.save_for_backward(logits, targets, lse, entropy)
+        ctx.temperature = temperature
         ctx.set_materialize_grads(False)
         return logprob, entropy, lse
 
@@ -85,18 +87,74 @@ class _FusedLogprobEntropy(torch.autograd.Function):
     def backward(ctx, g_logp, g_ent, g_lse):
         logits, targets, lse, entropy = ctx.saved_tensors
         if not ctx.needs_input_grad[0]:
-            return None, None
+            return None, None, None
 
         def prep(g):
             return None if g is None else g.to(torch.float32, copy=False).contiguous()
 
         d_logits = torch.empty(logits.shape, dtype=logits.dtype, device=logits.device)
-        _C.fused_logprob_entropy_v1_backward(
-            logits, targets, lse, entropy, prep(g_logp), prep(g_ent), prep(g_lse), d_logits)
-        return d_logits, None
+        _C.bwd_launch(logits, targets, lse, entropy, prep(g_logp), prep(g_ent), prep(g_lse),
+                      d_logits, temperature=ctx.temperature)
+        return d_logits, None, None
 
 
-def fused_logprob_entropy(logits: torch.Tensor, targets: torch.Tensor):
+# ---------------------------------------------------------------------------
+# torch.library registration: lets torch.compile trace through the op without
+# a graph break (the reference's autograd.Function breaks the graph,
+# notes/stage3_findings.md:75-94).  Eager calls keep _FusedLogprobEntropy.
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("kernel_opt::fused_logprob_entropy", mutates_args=(),
+                         device_types="cuda")
+def _op_forward(logits: torch.Tensor, targets: torch.Tensor,
+                temperature: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    _check_inputs(logits, targets)
+    logprob, entropy, lse = _alloc_outputs(targets)
+    _C.fwd_launch(logits, targets, logprob, entropy, lse, temperature=temperature)
+    return logprob, entropy, lse
+
+
+@_op_forward.register_fake
+def _(logits, targets, temperature):
+    return tuple(targets.new_empty(targets.shape, dtype=torch.float32) for _ in range(3))
+
+
+@torch.library.custom_op("kernel_opt::fused_logprob_entropy_backward", mutates_args=(),
+                         device_types="cuda")
+def _op_backward(logits: torch.Tensor, targets: torch.Tensor, lse: torch.Tensor,
+                 entropy: torch.Tensor, g_logp: torch.Tensor | None, g_ent: torch.Tensor | None,
+                 g_lse: torch.Tensor | None, temperature: float) -> torch.Tensor:
+    def prep(g):
+        return None if g is None else g.to(torch.float32, copy=False).contiguous()
+
+    d_logits = torch.empty(logits.shape, dtype=logits.dtype, device=logits.device)
+    _C.bwd_launch(logits, targets, lse, entropy, prep(g_logp), prep(g_ent), prep(g_lse),
+                  d_logits, temperature=temperature)
+    return d_logits
+
+
+@_op_backward.register_fake
+def _(logits, targets, lse, entropy, g_logp, g_ent, g_lse, temperature):
+    return torch.empty(logits.shape, dtype=logits.dtype, device=logits.device)
+
+
+def _op_setup_context(ctx, inputs, output):
+    logits, targets, temperature = inputs
+    _logprob, entropy, lse = output
+    ctx.save_for_backward(logits, targets, lse, entropy)
+    ctx.temperature = temperature
+
+
+def _op_backward_rule(ctx, g_logp, g_ent, g_lse):
+    logits, targets, lse, entropy = ctx.saved_tensors
+    d = _op_backward(logits, targets, lse, entropy, g_logp, g_ent, g_lse, ctx.temperature)
+    return d, None, None
+
+
+_op_forward.register_autograd(_op_backward_rule, setup_context=_op_setup_context)
+
+
+def fused_logprob_entropy(logits: torch.Tensor, targets: torch.Tensor,
+                          temperature: float | None = None):
     """Fused logprob + entropy + logsumexp, autograd-aware.
 
     Replaces TRL's ``selective_log_softmax(logits, targets)`` +
@@ -108,7 +166,20 @@ def fused_logprob_entropy(logits: torch.Tensor, targets: torch.Tensor):
                  stride; see the module docstring for the layout rule).
         targets: [...]    int64, contiguous, on the GPU.
 
+        temperature: optional sampling temperature T > 0.  The kernels then
+                 work on ``logits / T`` (each logit multiplied by fp32(1/T) as
+                 it is loaded) and the gradient is taken with respect to the
+                 unscaled ``logits``.  This replaces a separate
+                 ``logits.div_(T)`` pass; ``None`` or 1 is the plain op.
+
     Returns:
         (logprob, entropy, lse), each [...] fp32.  ``targets`` has no gradient.
+
+    Under ``torch.compile`` the call goes through the registered op
+    ``torch.ops.kernel_opt.fused_logprob_entropy`` (traced without a graph
+    break); eagerly it runs the autograd.Function, which skips the dispatcher.
     """
-    return _FusedLogprobEntropy.apply(logits, targets)
+    if torch.compiler.is_compiling():
+        return torch.ops.kernel_opt.fused_logprob_entropy(
+            logits, targets, 1.0 if temperature is None else float(temperature))
+    return _FusedLogprobEntropy.apply(logits, targets, temperature)

@@ -9,11 +9,15 @@ sites listed at reference trainer.py:3-8).
 Multimodal inputs fall back to the parent's eager implementation, as in the
 reference (trainer.py:56-74).
 
-Difference from the reference: the reference launches the kernel once per
-batch element because its kernel needs contiguous rows
-(trainer.py:104-124).  The HIP kernel addresses rows through two strides, so
-the sliced ``[B, L', V]`` completion window is passed in one launch, without
-a copy.  Outputs are the same.
+Differences from the reference, outputs unchanged up to fp32 rounding:
+  - the reference launches the kernel once per batch element because its
+    kernel needs contiguous rows (trainer.py:104-124); the HIP kernel
+    addresses rows through two strides, so the sliced ``[B, L', V]``
+    completion window is passed in one launch, without a copy;
+  - the temperature is fused into the kernel instead of a separate in-place
+    ``logits.div_(temperature)`` pass (trainer.py:101).  The division then
+    happens in fp32 (x * fp32(1/T)) rather than in the logits' dtype, so
+    bf16 logits are not re-rounded to bf16 after the division.
 """
 from __future__ import annotations
 
@@ -78,12 +82,15 @@ class KernelOptGRPOTrainer(GRPOTrainer):
             logits = model(**model_inputs).logits
             logits = logits[:, :-1, :]                 # drop the next-token position
             logits = logits[:, -logits_to_keep:, :]    # keep the completion window
-            logits.div_(self.temperature)              # in place, as TRL does
             completion_ids = input_ids_batch[:, -logits_to_keep:]
             if not completion_ids.is_contiguous():
                 completion_ids = completion_ids.contiguous()
 
-            logps, ents, _lse = fused_logprob_entropy(logits, completion_ids)
+            # The temperature is applied inside the kernel, where TRL (and the
+            # reference, trainer.py:101) first runs logits.div_(temperature)
+            # as a separate read + write pass over the logits.
+            logps, ents, _lse = fused_logprob_entropy(logits, completion_ids,
+                                                      temperature=self.temperature)
             all_logps.append(logps)
             if compute_entropy:
                 all_entropies.append(ents.detach())

@@ -128,6 +128,33 @@ int klp_bwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
             void* stream);
 
 /*
+ * Forward and backward with a sampling temperature T fused in: the logits are
+ * multiplied by 1/T (rounded once to fp32) as they are loaded, and the
+ * backward returns the gradient with respect to the unscaled logits (the
+ * scaled-logit gradient times 1/T).  Saved lse/entropy passed to
+ * klp_bwd_temp are those klp_fwd_temp produced with the same T.  No
+ * counterpart in the reference kernels: they replace the GRPO trainer's
+ * separate in-place `logits.div_(temperature)` pass (reference
+ * python/kernel_opt/trainer.py:101) followed by the plain kernels.
+ * T must be finite and > 0 (KLP_EINVAL otherwise); T = 1 equals
+ * klp_fwd / klp_bwd exactly.  Other arguments as klp_fwd / klp_bwd.
+ */
+int klp_fwd_temp(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                 int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                 const int64_t* targets, float temperature,
+                 float* logprob, float* entropy, float* lse,
+                 void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+int klp_bwd_temp(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                 int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                 const int64_t* targets, float temperature,
+                 const float* lse, const float* entropy,
+                 const float* g_logp, const float* g_ent, const float* g_lse,
+                 void* d_logits,
+                 void* stream);
+
+/*
  * Test hook with no counterpart in the reference: the next `count` compute
  * calls on the calling thread return KLP_ELAUNCH without launching anything,
  * as if hipGetLastError() had reported a failure.  Lets the error path be

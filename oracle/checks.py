@@ -39,7 +39,8 @@ def bits_of(arr: np.ndarray) -> np.ndarray:
     return arr.astype(np.int64)
 
 
-def grad_check(oracle, x_cpu, t_cpu, lse, ent, d_ours, g_logp=None, g_ent=None, g_lse=None):
+def grad_check(oracle, x_cpu, t_cpu, lse, ent, d_ours, g_logp=None, g_ent=None, g_lse=None,
+               temperature=None):
     """Worst normalised gradient error of the kernel against the float64
     oracle's gradient (<= 1 passes); see grad_score for the bar.  `lse` and
     `ent` are the kernel's own saved fp32 values (the oracle's backward takes
@@ -51,12 +52,14 @@ def grad_check(oracle, x_cpu, t_cpu, lse, ent, d_ours, g_logp=None, g_ent=None, 
 
     lse_np, ent_np = np1(lse), np1(ent)
     d_ref = oracle.backward(x_cpu, t_cpu.numpy().reshape(-1), lse_np, ent_np,
-                            g_logp=np1(g_logp), g_ent=np1(g_ent), g_lse=np1(g_lse))
+                            g_logp=np1(g_logp), g_ent=np1(g_ent), g_lse=np1(g_lse),
+                            temperature=temperature)
     return grad_score(oracle, x_cpu, t_cpu, lse_np, ent_np, d_ours, d_ref.reshape(n, -1),
-                      np1(g_logp), np1(g_ent), np1(g_lse))
+                      np1(g_logp), np1(g_ent), np1(g_lse), temperature=temperature)
 
 
-def grad_score(oracle, x_cpu, t_cpu, lse_np, ent_np, d_ours, d_ref, gl=None, ge=None, gs=None):
+def grad_score(oracle, x_cpu, t_cpu, lse_np, ent_np, d_ours, d_ref, gl=None, ge=None, gs=None,
+               temperature=None):
     """Bar: every element within 1 ulp of the output dtype of the float64
     reference value d_ref (rounded to nearest-even for bf16/fp16), except
     where that value is the result of cancellation between larger fp32 terms.
@@ -66,12 +69,19 @@ def grad_score(oracle, x_cpu, t_cpu, lse_np, ent_np, d_ours, d_ref, gl=None, ge=
     i.e. a couple of fp32 ulps of each summand, with exp's argument rounding
     (|x - lse| ulps of p) included.  Any fp32 evaluation of
     p * (g_lse - g_logp - g_ent (log p + H)) + [v == t] g_logp, the
-    reference's own fp32 path included, carries errors of that size.
+    reference's own fp32 path included, carries errors of that size.  With a
+    temperature T, x is the scaled logit fp32(x * fp32(1/T)) and the noise
+    carries the chain-rule factor 1/T.
     Returns (worst score, detail string); a score <= 1 passes."""
     V = x_cpu.shape[-1]
     n = lse_np.size
     t_np = t_cpu.numpy().reshape(-1)
-    x64 = x_cpu.detach().cpu().double().numpy().reshape(n, V)
+    x64 = x_cpu.detach().cpu().float().numpy().reshape(n, V)
+    scale = 1.0
+    if temperature is not None:  # the kernels' scaled logit fp32(x * fp32(1/T))
+        scale = float(np.float32(1.0 / float(temperature)))
+        x64 = x64 * np.float32(scale)
+    x64 = x64.astype(np.float64)
     lp = x64 - lse_np[:, None]
     with np.errstate(invalid="ignore", over="ignore"):
         p = np.where(np.isneginf(x64), 0.0, np.exp(lp))
@@ -84,7 +94,7 @@ def grad_score(oracle, x_cpu, t_cpu, lse_np, ent_np, d_ours, d_ref, gl=None, ge=
              + np.abs(ge_)[:, None] * (np.abs(ent_np)[:, None] + lp_abs))
     onehot = (np.arange(V)[None, :] == t_np[:, None])
     A = A + onehot * np.abs(gl_)[:, None]
-    noise = 2.0 ** -22 * (1.0 + lp_abs) * A
+    noise = 2.0 ** -22 * (1.0 + lp_abs) * A * scale
 
     dt = d_ours.dtype
     d = d_ours.detach().cpu().double().numpy().reshape(n, V)

@@ -19,6 +19,8 @@
  *       peeled first element, per-element recurrence
  *   klp_oracle_backward                        v1 backward       :233-282
  *       d = p (g_lse - g_logp - g_ent (log p + H)) + [v==t] g_logp
+ *   `scale` (forward/backward): temperature 1/T fused into the load, see
+ *       load_scaled(); scale = 1 is the reference computation.
  *
  * One deliberate difference, documented where it applies: in the backward a
  * -inf logit gets gradient 0 (its probability is exactly 0), where the
@@ -75,6 +77,20 @@ static double load_elem(const void* base, int dtype, int64_t idx) {
         case KLP_FP16: return klp_oracle_f16_to_f32(((const uint16_t*)base)[idx]);
         default: return ((const float*)base)[idx];
     }
+}
+
+/* Temperature: the kernels multiply each logit by scale = fp32(1/T) in fp32
+ * as it is loaded (fusing the trainer's logits.div_(temperature),
+ * reference python/kernel_opt/trainer.py:101).  The oracle applies the same
+ * single fp32 rounding, then works in float64. */
+static double load_scaled(const void* base, int dtype, int64_t idx, float scale) {
+    const float x = (float)load_elem(base, dtype, idx);
+#if KLP_MUTANT == 9 /* planted: temperature not applied */
+    (void)scale;
+    return x;
+#else
+    return (double)(x * scale);
+#endif
 }
 
 /* Round a float64 to a binary format with `p` significant bits, minimum
@@ -210,19 +226,26 @@ void klp_oracle_finalize(const double* st, double x_target, double* logp, double
 
 void klp_oracle_forward(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                         int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
-                        const int64_t* targets, double* logp, double* ent, double* lse) {
+                        const int64_t* targets, float scale, double* logp, double* ent,
+                        double* lse) {
 #pragma omp parallel for schedule(dynamic, 4)
     for (int64_t r = 0; r < n_rows; ++r) {
         const int64_t off = row_offset(r, rows_inner, stride_outer, stride_inner);
         const char* row = (const char*)logits + off * (dtype == KLP_FP32 ? 4 : 2);
         const int64_t tgt = targets[r];
-        double st[3];
-        klp_oracle_segment_state(row, dtype, 0, vocab, st);
+        klp_state s = {-INFINITY, 0.0, 0.0};
+        for (int64_t v = 0; v < vocab; ++v) {
+            klp_state e = {load_scaled(row, dtype, v, scale), 1.0, 0.0};
+            s = combine(s, e);
+        }
+        double st[3] = {s.m, s.Z, s.T};
         double x_target = 0.0;
 #if KLP_MUTANT == 4 /* planted: target index off by one */
-        if (tgt + 1 >= 0 && tgt + 1 < vocab) x_target = load_elem(row, dtype, tgt + 1);
-#else
+        if (tgt + 1 >= 0 && tgt + 1 < vocab) x_target = load_scaled(row, dtype, tgt + 1, scale);
+#elif KLP_MUTANT == 10 /* planted: target logit not scaled */
         if (tgt >= 0 && tgt < vocab) x_target = load_elem(row, dtype, tgt);
+#else
+        if (tgt >= 0 && tgt < vocab) x_target = load_scaled(row, dtype, tgt, scale);
 #endif
         klp_oracle_finalize(st, x_target, &logp[r], &ent[r], &lse[r]);
     }
@@ -268,9 +291,9 @@ void klp_oracle_forward_naive(const void* logits, int dtype, int64_t n_rows, int
 /* d_out is a dense [n_rows, vocab] float64 array.  g_* may be NULL (zero). */
 void klp_oracle_backward(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                          int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
-                         const int64_t* targets, const double* lse, const double* ent,
-                         const double* g_logp, const double* g_ent, const double* g_lse,
-                         double* d_out) {
+                         const int64_t* targets, float scale, const double* lse,
+                         const double* ent, const double* g_logp, const double* g_ent,
+                         const double* g_lse, double* d_out) {
 #pragma omp parallel for schedule(dynamic, 4)
     for (int64_t r = 0; r < n_rows; ++r) {
         const int64_t off = row_offset(r, rows_inner, stride_outer, stride_inner);
@@ -287,7 +310,7 @@ void klp_oracle_backward(const void* logits, int dtype, int64_t n_rows, int64_t 
 #endif
         double* d = d_out + r * vocab;
         for (int64_t v = 0; v < vocab; ++v) {
-            const double x = load_elem(row, dtype, v);
+            const double x = load_scaled(row, dtype, v, scale);
             double val;
             if (x == -INFINITY) {
                 val = 0.0; /* p = 0 exactly; the reference writes NaN (0 * inf) */
@@ -305,7 +328,11 @@ void klp_oracle_backward(const void* logits, int dtype, int64_t n_rows, int64_t 
 #else
             if (v == tgt) val += gl;
 #endif
+#if KLP_MUTANT == 11 /* planted: chain-rule factor 1/T dropped */
             d[v] = val;
+#else
+            d[v] = val * (double)scale; /* d/dx = (1/T) d/dx' */
+#endif
         }
     }
 }

@@ -47,9 +47,10 @@ class Oracle:
             path = build(mutant)
         self.path = path
         lib = ctypes.CDLL(path)
-        lib.klp_oracle_forward.argtypes = _ROWS + [_vp, _dp, _dp, _dp]
+        lib.klp_oracle_forward.argtypes = _ROWS + [_vp, ctypes.c_float, _dp, _dp, _dp]
         lib.klp_oracle_forward_naive.argtypes = _ROWS + [_vp, _dp, _dp, _dp]
-        lib.klp_oracle_backward.argtypes = _ROWS + [_vp, _dp, _dp, _dp, _dp, _dp, _dp]
+        lib.klp_oracle_backward.argtypes = _ROWS + [_vp, ctypes.c_float, _dp, _dp, _dp, _dp, _dp,
+                                                     _dp]
         lib.klp_oracle_round.argtypes = [_dp, _i32, _i64, _vp]
         lib.klp_oracle_combine.argtypes = [_dp, _dp, _dp]
         lib.klp_oracle_segment_state.argtypes = [_vp, _i32, _i64, _i64, _dp]
@@ -99,23 +100,37 @@ class Oracle:
         return a
 
     # -- API ---------------------------------------------------------------
-    def forward(self, logits, targets, dtype=None, naive: bool = False):
-        """(logp, entropy, lse) float64 for dense [..., V] logits."""
+    def forward(self, logits, targets, dtype=None, naive: bool = False, temperature=None):
+        """(logp, entropy, lse) float64 for dense [..., V] logits; with a
+        temperature T the logits are first multiplied by fp32(1/T) in fp32."""
         arr, code = self._as_storage(logits, dtype)
         V = arr.shape[-1]
         n = arr.size // V
         tg = np.ascontiguousarray(np.asarray(targets, dtype=np.int64).reshape(-1))
         assert tg.size == n
         outs = [np.empty(n, np.float64) for _ in range(3)]
-        fn = self.lib.klp_oracle_forward_naive if naive else self.lib.klp_oracle_forward
-        fn(arr.ctypes.data, code, n, V, max(n, 1), 0, V, tg.ctypes.data,
-           *[self._dptr(o) for o in outs])
+        if naive:
+            assert temperature is None
+            self.lib.klp_oracle_forward_naive(arr.ctypes.data, code, n, V, max(n, 1), 0, V,
+                                              tg.ctypes.data, *[self._dptr(o) for o in outs])
+        else:
+            self.lib.klp_oracle_forward(arr.ctypes.data, code, n, V, max(n, 1), 0, V,
+                                        tg.ctypes.data, self.scale_of(temperature),
+                                        *[self._dptr(o) for o in outs])
         shape = arr.shape[:-1]
         return tuple(o.reshape(shape) for o in outs)
 
+    @staticmethod
+    def scale_of(temperature):
+        """fp32(1/T), as the kernels compute it (1.0 for None)."""
+        if temperature is None:
+            return 1.0
+        return float(np.float32(1.0 / float(temperature)))
+
     def backward(self, logits, targets, lse, ent, g_logp=None, g_ent=None, g_lse=None,
-                 dtype=None):
-        """float64 d_logits, dense, shaped like logits."""
+                 dtype=None, temperature=None):
+        """float64 d_logits with respect to the unscaled logits, dense, shaped
+        like logits."""
         arr, code = self._as_storage(logits, dtype)
         V = arr.shape[-1]
         n = arr.size // V
@@ -124,7 +139,8 @@ class Oracle:
         gl, ge, gs = self._f64(g_logp, n), self._f64(g_ent, n), self._f64(g_lse, n)
         out = np.empty(arr.shape, np.float64)
         self.lib.klp_oracle_backward(arr.ctypes.data, code, n, V, max(n, 1), 0, V,
-                                     tg.ctypes.data, self._dptr(lse64), self._dptr(ent64),
+                                     tg.ctypes.data, self.scale_of(temperature),
+                                     self._dptr(lse64), self._dptr(ent64),
                                      self._dptr(gl), self._dptr(ge), self._dptr(gs),
                                      self._dptr(out))
         return out

@@ -375,10 +375,56 @@ def pin_down_conversions(o):
     return None
 
 
+def _scaled(x32, T):
+    """numpy's own fp32 product x * fp32(1/T), as float64."""
+    s = np.float32(1.0 / T)
+    return (x32.astype(np.float32) * s).astype(np.float64), float(s)
+
+
+def pin_temperature_forward(o):
+    """Temperature T: brute force on the logits scaled by fp32(1/T) in numpy;
+    T = 1 is exactly the plain forward."""
+    x, t = _case("randn", 2001, n=4, k=50)
+    for T in (0.7, 1.3, 2.0):
+        xs, _ = _scaled(x, T)
+        got = o.forward(x, t, dtype="fp32", temperature=T)
+        ref = brute_forward(xs, t)
+        for g, r, nm in zip(got, ref, ("logp", "entropy", "lse")):
+            msg = _close(g, r, 1e-11, f"temperature {T} {nm}")
+            if msg:
+                return msg
+    a = o.forward(x, t, dtype="fp32", temperature=1.0)
+    b = o.forward(x, t, dtype="fp32")
+    if not all(np.array_equal(u, v) for u, v in zip(a, b)):
+        return "temperature 1 must equal the plain forward"
+    return None
+
+
+def pin_temperature_backward(o):
+    """d/dx of L(x / T) = (1/T) * (the softmax-Jacobian gradient at x / T)."""
+    V = 60
+    x, t = _case("randn", V, n=3, k=51)
+    gl, ge, gs = _grads(3, 6)
+    for T in (0.6, 1.7):
+        xs, s = _scaled(x, T)
+        lp, h, l = brute_forward(xs, t)
+        d = o.backward(x, t, l, h, g_logp=gl, g_ent=ge, g_lse=gs, dtype="fp32", temperature=T)
+        for i in range(3):
+            p = np.exp(xs[i] - l[i])
+            J = np.diag(p) - np.outer(p, p)
+            e_t = np.zeros(V)
+            e_t[t[i]] = 1.0
+            ref = s * (gl[i] * (e_t - p) + gs[i] * p - ge[i] * (J.T @ (np.log(p) + 1.0)))
+            msg = _close(d[i], ref, 1e-13, f"temperature {T} jacobian row {i}")
+            if msg:
+                return msg
+    return None
+
+
 ALL_PINS = [
     pin_brute_force, pin_uniform, pin_two_element, pin_spike, pin_shift_and_permutation,
     pin_targets_out_of_range, pin_target_value, pin_negative_infinity, pin_nan_propagates,
     pin_combine_associative, pin_naive_matches, pin_backward_finite_difference,
     pin_backward_jacobian, pin_backward_sum_and_nones, pin_backward_negative_infinity,
-    pin_up_conversions, pin_down_conversions,
+    pin_up_conversions, pin_down_conversions, pin_temperature_forward, pin_temperature_backward,
 ]

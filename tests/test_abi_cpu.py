@@ -189,3 +189,20 @@ def test_package_surface_matches_reference():
         assert callable(getattr(kernel_opt._C, name))
     with pytest.raises(AttributeError):
         kernel_opt.does_not_exist  # noqa: B018
+
+
+def test_temperature_must_be_finite_and_positive():
+    from kernel_opt._library import KLP_EINVAL, lib
+    for T in (0.0, -1.0, float("inf"), float("nan")):
+        rc = lib.klp_fwd_temp(P, 0, 4, 100, 4, 0, 100, P, T, P, P, P, None, 0, None)
+        assert rc == KLP_EINVAL and "temperature" in _err()
+        rc = lib.klp_bwd_temp(P, 0, 4, 100, 4, 0, 100, P, T, P, P, None, None, None, P, None)
+        assert rc == KLP_EINVAL and "temperature" in _err()
+
+
+def test_torch_library_ops_registered():
+    import kernel_opt  # noqa: F401
+    fwd = str(torch.ops.kernel_opt.fused_logprob_entropy.default._schema)
+    bwd = str(torch.ops.kernel_opt.fused_logprob_entropy_backward.default._schema)
+    assert "float temperature" in fwd and "-> (Tensor, Tensor, Tensor)" in fwd
+    assert "Tensor? g_logp" in bwd and bwd.endswith("-> Tensor")

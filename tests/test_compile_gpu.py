@@ -43,3 +43,37 @@ def test_compile_backward_matches_eager():
     torch._dynamo.reset()
     torch.compile(loss_fn, backend=COMPILE_BACKEND, dynamic=False)(x_c, t).backward()
     assert torch.allclose(x_c.grad, x_e.grad, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("temperature", [None, 0.75])
+def test_compile_fullgraph_no_graph_break(dtype, temperature):
+    """With the torch.library registration, fullgraph=True compiles (it would
+    raise on a graph break), and forward + backward equal eager."""
+    from kernel_opt import fused_logprob_entropy
+    B, S, V = 2, 6, 3001
+    base = seeded_logits((B, S, V), dtype, seed=3, scale=1.5).cuda()
+    t = seeded_targets((B, S), V, seed=3).cuda()
+
+    def loss_fn(x, t):
+        logp, ent, lse = fused_logprob_entropy(x, t, temperature=temperature)
+        return (logp + 0.1 * ent - 0.01 * lse).sum(), logp, ent, lse
+
+    x_e = base.clone().requires_grad_(True)
+    out_e = loss_fn(x_e, t)
+    out_e[0].backward()
+    torch._dynamo.reset()
+    x_c = base.clone().requires_grad_(True)
+    out_c = torch.compile(loss_fn, backend=COMPILE_BACKEND, fullgraph=True, dynamic=False)(x_c, t)
+    out_c[0].backward()
+    for e, c in zip(out_e[1:], out_c[1:]):
+        assert torch.equal(e, c)
+    assert torch.equal(x_c.grad, x_e.grad)
+
+
+def test_opcheck_registered_op():
+    from kernel_opt import ops  # noqa: F401  (registers the ops)
+    x = seeded_logits((3, 5, 777), torch.float32, seed=4).cuda().requires_grad_(True)
+    t = seeded_targets((3, 5), 777, seed=4).cuda()
+    torch.library.opcheck(torch.ops.kernel_opt.fused_logprob_entropy.default, (x, t, 1.0))
+    torch.library.opcheck(torch.ops.kernel_opt.fused_logprob_entropy.default, (x, t, 0.5))

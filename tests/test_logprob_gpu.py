@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from klp_testutil import (FWD_TOL, grad_check, seeded_logits, seeded_targets, storage_bits,
-                          ulp_diff)
+                          ulp_diff)  # noqa: F401
 
 pytestmark = pytest.mark.gpu
 
@@ -531,3 +531,60 @@ def test_hip_graph_capture_and_replay(config, oracle):
         assert junk.isfinite()
         for got, exp in zip((lp, h, l, d), ref):
             assert torch.equal(got, exp), f"replay {rep} differs from eager"
+
+
+# ---------------------------------------------------------------------------
+# Fused temperature (klp_fwd_temp / klp_bwd_temp)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("T", [0.7, 1.5])
+def test_temperature_matches_oracle(dtype, T, oracle):
+    N, V = 12, 20011
+    x_cpu = seeded_logits((N, V), dtype, seed=141)
+    t_cpu = seeded_targets((N,), V, seed=141)
+    x = x_cpu.to(DEV).requires_grad_(True)
+    lp, h, l = _ko().fused_logprob_entropy(x, t_cpu.to(DEV), temperature=T)
+    ref = oracle.forward(x_cpu, t_cpu.numpy(), temperature=T)
+    for nm, o, r in zip(("logp", "entropy", "lse"), (lp, h, l), ref):
+        err = np.abs(o.detach().cpu().double().numpy() - r).max()
+        assert err <= FWD_TOL[dtype], f"{nm}: {err:.3g}"
+    g = torch.Generator().manual_seed(1411)
+    gl, ge = [torch.randn(N, generator=g) * 0.5 for _ in range(2)]
+    (lp * gl.to(DEV) + h * ge.to(DEV)).sum().backward()
+    worst, detail = grad_check(oracle, x_cpu, t_cpu, l.detach(), h.detach(), x.grad,
+                               g_logp=gl, g_ent=ge, temperature=T)
+    assert worst <= 1.0, detail
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_temperature_matches_eager_division(dtype):
+    """Against the reference's eager composition logits / T -> formulas, with
+    autograd through the division (fp32 eager path)."""
+    B, S, V = 2, 8, 8192
+    base = seeded_logits((B, S, V), dtype, seed=151).to(DEV)
+    t = seeded_targets((B, S), V, seed=151).to(DEV)
+    T = 0.8
+    gl = torch.full((B, S), 0.4, device=DEV)
+    ge = torch.full((B, S), -0.2, device=DEV)
+    xr = base.float().clone().requires_grad_(True)
+    lp_r, h_r, l_r = _eager().ref_fp32(xr / T, t)
+    (lp_r * gl + h_r * ge).sum().backward()
+    x = base.clone().requires_grad_(True)
+    lp, h, l = _ko().fused_logprob_entropy(x, t, temperature=T)
+    (lp * gl + h * ge).sum().backward()
+    for a, b in ((lp, lp_r), (h, h_r), (l, l_r)):
+        assert (a - b).abs().max().item() <= FWD_TOL[dtype]
+    atol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert torch.allclose(x.grad.float(), xr.grad, atol=atol, rtol=atol)
+
+
+def test_temperature_one_is_the_plain_op():
+    N, V = 16, 5003
+    x = seeded_logits((N, V), torch.bfloat16, seed=161).to(DEV)
+    t = seeded_targets((N,), V, seed=161).to(DEV)
+    a = _ko().fused_logprob_entropy_forward(x, t)
+    b = _ko().fused_logprob_entropy_forward(x, t, temperature=1.0)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    with pytest.raises(RuntimeError, match="temperature"):
+        _ko().fused_logprob_entropy_forward(x, t, temperature=0.0)

@@ -23,8 +23,11 @@ def trainer_mod(monkeypatch):
     import kernel_opt.trainer as tr
     from oracle.eager_ref import ref_forward_pt
 
-    def cpu_fused(logits, targets):  # the op's contract, evaluated eagerly in fp32
-        return ref_forward_pt(logits.float(), targets)
+    def cpu_fused(logits, targets, temperature=None):  # the op's contract, eagerly in fp32
+        x = logits.float()
+        if temperature is not None:
+            x = x * torch.tensor(1.0 / temperature, dtype=torch.float32)
+        return ref_forward_pt(x, targets)
 
     monkeypatch.setattr(tr, "fused_logprob_entropy", cpu_fused)
     yield tr
