@@ -19,8 +19,9 @@ Algorithmic bytes per launch (s = bytes per logit, N rows, V vocab):
 Timing (HIP events on the stream the kernels run on): `ms_per_step` is one
 event pair around K interleaved forward+backward steps, divided by K; the
 per-kernel `fwd_ms` / `bwd_ms` are one event pair around K back-to-back
-launches of that kernel, divided by K.  With --flush a 1 GiB buffer is
-overwritten before every launch and each launch is timed on its own.  The
+launches of that kernel, divided by K.  With --flush a 1 GiB buffer is read
+(or, with --flush-mode write, overwritten) before every launch and each
+launch is timed on its own.  The
 roofline object reports the dominant kernel, the backward (it moves twice the
 forward's bytes); `traffic` is the HBM bytes per launch that rocprofv3's
 FETCH_SIZE / WRITE_SIZE counters measured for that launch shape, scaled by
@@ -56,8 +57,8 @@ HBM_PEAK_TBPS = 8.0
 # (profiles/klp_C2_bf16_hbm_traffic.md).  Keyed by workload, kernel and
 # launch shape (waves, unroll, splits, flags); reported only for that shape.
 MEASURED_TRAFFIC = {
-    ("C2", "fwd", (4, 4, 1, 0)): 311760691,
-    ("C2", "bwd", (16, 2, 8, 1)): 623333215,
+    ("C2", "fwd", (4, 4, 1, 0)): 311769737,
+    ("C2", "bwd", (16, 2, 8, 1)): 623324882,
 }
 ROW_BLOCK = 256  # rows per seeded generator block
 
@@ -215,7 +216,10 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
     ap.add_argument("--flush", action="store_true",
-                    help="overwrite a 1 GiB buffer before every launch (cold Infinity Cache)")
+                    help="run through a 1 GiB buffer before every launch (cold Infinity Cache)")
+    ap.add_argument("--flush-mode", choices=("read", "write"), default="read",
+                    help="read: sum the buffer (evicts with clean lines); write: fill it "
+                         "(leaves up to the cache size of dirty lines for the next kernel)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=1024,
                     help="rows of the workload the CPU baseline times (whole batch elements)")
@@ -250,7 +254,7 @@ def main(argv=None):
     d_logits = torch.empty(logits.shape, dtype=logits.dtype, device=dev)
     fcfg = tuple(int(v) for v in args.fwd_config.split(",")) if args.fwd_config else None
     bcfg = tuple(int(v) for v in args.bwd_config.split(",")) if args.bwd_config else None
-    flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev) if args.flush else None
+    flush_buf = torch.ones(1 << 30, dtype=torch.uint8, device=dev) if args.flush else None
 
     def fwd():
         _C.fwd_launch(logits, targets, logp, ent, lse, config=fcfg)
@@ -285,11 +289,17 @@ def main(argv=None):
         torch.cuda.synchronize()
         return a.elapsed_time(b) / K
 
+    def flush(k):
+        if args.flush_mode == "read":
+            flush_buf.view(torch.int64).sum()
+        else:
+            flush_buf.fill_(k & 0xFF)
+
     def timed_each(fn):
-        """Per-launch ms with the Infinity Cache overwritten before each launch."""
+        """Per-launch ms with the Infinity Cache flushed before each launch."""
         ts = []
         for k in range(K):
-            flush_buf.fill_(k & 0xFF)
+            flush(k)
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record(stream)
@@ -357,7 +367,8 @@ def main(argv=None):
                                f"backward launch per step",
                    "global_batch": B, "seq_len": S, "vocab": V, "n_rows": N,
                    "parallelism": "single-gpu",
-                   "infinity_cache": "flushed" if args.flush else "warm"},
+                   "infinity_cache": (f"flushed ({args.flush_mode} 1 GiB before each launch)"
+                                      if args.flush else "warm")},
         "fwd_ms": round(fwd_avg, 5),
         "bwd_ms": round(bwd_avg, 5),
         "fwd_tbps": round(fwd_tbps, 4),

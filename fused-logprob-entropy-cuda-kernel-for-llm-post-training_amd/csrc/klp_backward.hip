@@ -115,7 +115,9 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t idx = i0 + tid + u * NTHREADS;
-            if (idx < ve) v[u] = load16<true>(vin + idx);
+            // Temporal loads here (non-temporal in the forward): measured best
+            // for a forward followed by a backward over the same logits.
+            if (idx < ve) v[u] = load16<false>(vin + idx);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {

@@ -52,8 +52,9 @@ struct BwdParams {
 
 // Launch shape: `waves` wave64s per workgroup, `unroll` 16-byte loads per
 // thread per iteration, `splits` workgroups per row.  `flags` selects kernel
-// variants: bit 0 (backward only) = non-temporal gradient stores.  Loads of
-// logits are always non-temporal.
+// variants: bit 0 (backward only) = non-temporal gradient stores.  The
+// forward reads logits with non-temporal loads, the backward with ordinary
+// ones.
 struct FwdConfig {
     int waves;
     int unroll;
