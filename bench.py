@@ -209,6 +209,56 @@ def cpu_baseline(name: str, max_rows: int, logits_gpu, targets_gpu, g_logp, g_en
 # ---------------------------------------------------------------------------
 # GPU timing
 # ---------------------------------------------------------------------------
+def _eager_grpo(logp, old, adv, mask, ref, eps_low, eps_high, beta):
+    """The GRPO loss as a chain of eager torch ops ("grpo" normaliser, token
+    level): the path klp_grpo_* replaces, timed beside it."""
+    coef_1 = torch.exp(logp - old)
+    coef_2 = torch.clamp(coef_1, 1 - eps_low, 1 + eps_high)
+    per_token = -torch.min(coef_1 * adv.unsqueeze(1), coef_2 * adv.unsqueeze(1))
+    kl = torch.exp(ref - logp) - (ref - logp) - 1
+    per_token = per_token + beta * kl
+    return ((per_token * mask).sum(-1) / mask.sum(-1).clamp(min=1.0)).mean()
+
+
+def grpo_timing(dev, K, B=16, S=2048):
+    """Forward + backward of the GRPO loss on [B, S] per-token log-probs
+    (C4's batch shape): fused launches against the eager chain."""
+    from kernel_opt import fused_grpo_loss
+    g = torch.Generator(device="cpu").manual_seed(2024)
+    new = (torch.randn(B, S, generator=g) - 2.0).to(dev)
+    old = (new.cpu() + 0.3 * torch.randn(B, S, generator=g)).to(dev)
+    ref = (new.cpu() + 0.3 * torch.randn(B, S, generator=g)).to(dev)
+    adv = torch.randn(B, generator=g).to(dev)
+    mask = (torch.rand(B, S, generator=g) < 0.7).float().to(dev)
+    lp = new.clone().requires_grad_(True)
+
+    def fused():
+        loss, _ = fused_grpo_loss(lp, old, adv, mask, ref, eps_low=0.2, eps_high=0.28,
+                                  beta=0.04, loss_type="grpo")
+        loss.backward()
+
+    def eager():
+        _eager_grpo(lp, old, adv, mask, ref, 0.2, 0.28, 0.04).backward()
+
+    res = {}
+    for name, fn in (("fused", fused), ("eager", eager)):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(K):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        res[name] = a.elapsed_time(b) / K * 1e3
+    return {"shape": [B, S], "loss_type": "grpo", "beta": 0.04,
+            "fused_fwd_bwd_us": round(res["fused"], 2),
+            "eager_fwd_bwd_us": round(res["eager"], 2),
+            "note": "loss + loss.backward() per iteration, end to end from Python"}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,6 +275,8 @@ def main(argv=None):
                     help="rows of the workload the CPU baseline times (whole batch elements)")
     ap.add_argument("--fwd-config", default=None, help="waves,unroll,splits,flags")
     ap.add_argument("--bwd-config", default=None, help="waves,unroll,splits,flags")
+    ap.add_argument("--no-grpo", action="store_true",
+                    help="skip the GRPO-loss timing (fused klp_grpo_* against the eager chain)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run torch's copy of a buffer the size of the logits (known "
                          "traffic, for scaling HBM counters)")
@@ -345,6 +397,8 @@ def main(argv=None):
             "fwd_bwd_ms": round(c["fwd_bwd_ms"], 3),
         }
 
+    grpo = None if args.no_grpo else grpo_timing(dev, K)
+
     B, S, _ = cfg["shape"]
     fwd_used = fcfg or _C.default_config("fwd", logits.dtype, N, V)
     bwd_used = bcfg or _C.default_config("bwd", logits.dtype, N, V)
@@ -391,6 +445,7 @@ def main(argv=None):
             "fwd_algorithmic_bytes": fb,
         },
         "cpu_baseline": cpu,
+        "grpo_loss": grpo,
     }
     print(json.dumps(out))
     return 0

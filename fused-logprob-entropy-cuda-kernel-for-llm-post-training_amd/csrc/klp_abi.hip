@@ -245,6 +245,67 @@ int bwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
                         "backward");
 }
 
+size_t grpo_workspace_bytes(int64_t n_seqs) {
+    if (n_seqs <= 0) return 0;
+    return (static_cast<size_t>(n_seqs) * klp::kGrpoRowWords + 1) * sizeof(float);
+}
+
+bool finite_nonneg(float v) { return v >= 0.0f && v != INFINITY; }
+
+// Shared checks and parameter block of klp_grpo_fwd / klp_grpo_bwd.
+int grpo_setup(const float* logp, const float* old_logp, const float* ref_logp,
+               const float* advantages, const float* mask, int64_t n_seqs, int64_t seq_len,
+               float eps_low, float eps_high, float beta, float norm_const, int loss_type,
+               int level, int adv_per_token, void* workspace, size_t workspace_bytes,
+               klp::GrpoParams* p) {
+    if (n_seqs < 1 || n_seqs > (int64_t{1} << 31) - 1)
+        return fail(KLP_EINVAL, "n_seqs must be in [1, 2^31-1], got %lld",
+                    static_cast<long long>(n_seqs));
+    if (seq_len < 0) return fail(KLP_EINVAL, "seq_len must be >= 0");
+    int rc;
+    if ((rc = check_f32(logp, "logp")) != KLP_OK) return rc;
+    if ((rc = check_f32(old_logp, "old_logp")) != KLP_OK) return rc;
+    if ((rc = check_f32(advantages, "advantages")) != KLP_OK) return rc;
+    if (ref_logp && (rc = check_f32(ref_logp, "ref_logp")) != KLP_OK) return rc;
+    if (mask && (rc = check_f32(mask, "mask")) != KLP_OK) return rc;
+    if (!finite_nonneg(eps_low) || !finite_nonneg(eps_high))
+        return fail(KLP_EINVAL, "eps_low and eps_high must be finite and >= 0");
+    if (!(beta == beta) || beta == INFINITY || beta == -INFINITY)
+        return fail(KLP_EINVAL, "beta must be finite");
+    if (loss_type != KLP_GRPO_LOSS_GRPO && loss_type != KLP_GRPO_LOSS_BNPO &&
+        loss_type != KLP_GRPO_LOSS_FIXED)
+        return fail(KLP_EINVAL, "unknown loss_type %d", loss_type);
+    if (loss_type == KLP_GRPO_LOSS_FIXED && !(norm_const > 0.0f && norm_const != INFINITY))
+        return fail(KLP_EINVAL, "norm_const must be finite and > 0 for KLP_GRPO_LOSS_FIXED");
+    if (level != KLP_GRPO_TOKEN && level != KLP_GRPO_SEQUENCE)
+        return fail(KLP_EINVAL, "unknown importance level %d", level);
+    const size_t need = grpo_workspace_bytes(n_seqs);
+    if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 4))
+        return fail(KLP_EWORKSPACE,
+                    "workspace missing, too small or not 4-byte aligned: have %zu bytes, need %zu",
+                    workspace_bytes, need);
+    p->logp = logp;
+    p->old_logp = old_logp;
+    p->ref_logp = ref_logp;
+    p->adv = advantages;
+    p->mask = mask;
+    p->B = n_seqs;
+    p->S = seq_len;
+    p->eps_low = eps_low;
+    p->eps_high = eps_high;
+    p->beta = beta;
+    p->norm_const = norm_const;
+    p->loss_type = loss_type;
+    p->level = level;
+    p->adv_per_token = adv_per_token != 0;
+    p->ws = static_cast<float*>(workspace);
+    p->loss = nullptr;
+    p->stats = nullptr;
+    p->grad_loss = nullptr;
+    p->d_logp = nullptr;
+    return KLP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -373,6 +434,46 @@ void klp_default_config(int which, int dtype, int64_t n_rows, int64_t vocab, int
     if (unroll) *unroll = c.unroll;
     if (splits) *splits = c.splits;
     if (flags) *flags = c.flags;
+}
+
+size_t klp_grpo_workspace_bytes(int64_t n_seqs) { return grpo_workspace_bytes(n_seqs); }
+
+int klp_grpo_fwd(const float* logp, const float* old_logp, const float* ref_logp,
+                 const float* advantages, const float* mask, int64_t n_seqs, int64_t seq_len,
+                 float eps_low, float eps_high, float beta, float norm_const, int loss_type,
+                 int level, int adv_per_token, float* loss, float* stats, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+    klp::GrpoParams p;
+    int rc = grpo_setup(logp, old_logp, ref_logp, advantages, mask, n_seqs, seq_len, eps_low,
+                        eps_high, beta, norm_const, loss_type, level, adv_per_token, workspace,
+                        workspace_bytes, &p);
+    if (rc != KLP_OK) return rc;
+    if ((rc = check_f32(loss, "loss")) != KLP_OK) return rc;
+    if (stats && (rc = check_f32(stats, "stats")) != KLP_OK) return rc;
+    p.loss = loss;
+    p.stats = stats;
+    if (injected_failure("grpo forward")) return KLP_ELAUNCH;
+    return after_launch(klp::launch_grpo_fwd(p, static_cast<hipStream_t>(stream)),
+                        "grpo forward");
+}
+
+int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp,
+                 const float* advantages, const float* mask, int64_t n_seqs, int64_t seq_len,
+                 float eps_low, float eps_high, float beta, float norm_const, int loss_type,
+                 int level, int adv_per_token, const float* grad_loss, float* d_logp,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+    klp::GrpoParams p;
+    int rc = grpo_setup(logp, old_logp, ref_logp, advantages, mask, n_seqs, seq_len, eps_low,
+                        eps_high, beta, norm_const, loss_type, level, adv_per_token, workspace,
+                        workspace_bytes, &p);
+    if (rc != KLP_OK) return rc;
+    if ((rc = check_f32(d_logp, "d_logp")) != KLP_OK) return rc;
+    if (grad_loss && (rc = check_f32(grad_loss, "grad_loss")) != KLP_OK) return rc;
+    p.grad_loss = grad_loss;
+    p.d_logp = d_logp;
+    if (injected_failure("grpo backward")) return KLP_ELAUNCH;
+    return after_launch(klp::launch_grpo_bwd(p, static_cast<hipStream_t>(stream)),
+                        "grpo backward");
 }
 
 }  // extern "C"

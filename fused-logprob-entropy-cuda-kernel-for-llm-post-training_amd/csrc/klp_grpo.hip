@@ -1,0 +1,257 @@
+// klp_grpo.hip — the GRPO policy loss over per-token log-probabilities
+// ("K2 fused_grpo_loss" in the reference's plan, notes/PLAN.md:59; the loss
+// itself is written out in examples/compare_one_step.py:232-236, and is the
+// loss TRL's GRPOTrainer applies to the output of the fused logprob kernel).
+//
+// Per token (b, s) with mask m, advantage A, new / old / reference
+// log-probabilities lp, lo, lr:
+//   w     = lp - lo                      (token level), or the row's masked
+//           mean of lp - lo              (sequence level),
+//   c1    = exp(w),  c2 = clamp(c1, 1 - eps_low, 1 + eps_high),
+//   loss  = -min(c1 * A, c2 * A) + beta * (exp(lr - lp) - (lr - lp) - 1).
+// The batch loss is the masked sum of the per-token losses divided by
+//   "grpo":  B * max(sum_s m, 1) per row (mean over rows of row means),
+//   "bnpo":  max(sum m, 1) over the batch,
+//   "fixed": a caller-given constant (TRL's dr_grpo and dapo normalisers).
+// The gradient with respect to lp follows PyTorch's rules for the eager
+// expression: at a tie of min() each side gets half, clamp() passes the
+// gradient on its closed interval.
+//
+// Launches: klp_grpo_rows_kernel (one workgroup per row: row sums into the
+// workspace), klp_grpo_finish_kernel (one workgroup: the batch sums in a
+// fixed order, the loss and statistics), klp_grpo_bwd_kernel (one workgroup
+// per row: the gradient, scaled by the upstream gradient of the loss).  All
+// reductions have a fixed order, so results do not depend on timing.
+#include "klp_launch.h"
+
+namespace klp {
+
+namespace {
+
+constexpr int kGrpoThreads = 256;
+
+__device__ __forceinline__ float mask_at(const GrpoParams& p, int64_t i) {
+    return p.mask ? p.mask[i] : 1.0f;
+}
+
+__device__ __forceinline__ float adv_at(const GrpoParams& p, int64_t b, int64_t i) {
+    return p.adv_per_token ? p.adv[i] : p.adv[b];
+}
+
+struct TokenLoss {
+    float loss;   // per-token loss
+    float dw;     // d loss / d w (w = the log importance weight)
+    float dlp;    // d loss / d lp through the KL term only
+    float kl;     // KL estimate (0 when beta == 0 or no reference)
+    float low;    // 1 if clipped at 1 - eps_low with A < 0
+    float high;   // 1 if clipped at 1 + eps_high with A > 0
+};
+
+__device__ __forceinline__ TokenLoss token_loss(const GrpoParams& p, float w, float adv,
+                                                float lp, float lr, bool has_ref) {
+    TokenLoss r;
+    const float lo_b = 1.0f - p.eps_low;
+    const float hi_b = 1.0f + p.eps_high;
+    const float c1 = expf(w);
+    const float c2 = fminf(fmaxf(c1, lo_b), hi_b);
+    const float a = c1 * adv;
+    const float b = c2 * adv;
+    // d a / d w = c1 * adv; d b / d w = c1 * adv inside [lo_b, hi_b], else 0.
+    const float da = c1 * adv;
+    const float db = (c1 >= lo_b && c1 <= hi_b) ? da : 0.0f;
+    float dmin;
+    if (a < b) dmin = da;
+    else if (b < a) dmin = db;
+    else dmin = 0.5f * da + 0.5f * db;
+    r.loss = -fminf(a, b);
+    r.dw = -dmin;
+    r.kl = 0.0f;
+    r.dlp = 0.0f;
+    if (has_ref) {
+        const float d = lr - lp;
+        const float e = expf(d);
+        r.kl = e - d - 1.0f;
+        r.loss += p.beta * r.kl;
+        r.dlp = p.beta * (1.0f - e);
+    }
+    r.low = (c1 < lo_b && adv < 0.0f) ? 1.0f : 0.0f;
+    r.high = (c1 > hi_b && adv > 0.0f) ? 1.0f : 0.0f;
+    return r;
+}
+
+// Block-wide sums of K values, fixed order (xor-shuffle tree within waves,
+// waves in order through LDS).  Every thread returns the totals.
+template <int K>
+__device__ __forceinline__ void block_sum(float (&v)[K]) {
+    __shared__ float red[kGrpoThreads / 64][K];
+    __shared__ float tot[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v[k] += __shfl_xor(v[k], off, 64);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    if (lane == 0)
+#pragma unroll
+        for (int k = 0; k < K; ++k) red[wave][k] = v[k];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            float s = red[0][k];
+            for (int w = 1; w < kGrpoThreads / 64; ++w) s += red[w][k];
+            tot[k] = s;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = tot[k];
+    __syncthreads();
+}
+
+// The row's log importance weight at sequence level: masked mean of lp - lo.
+__device__ __forceinline__ void row_sequence_weight(const GrpoParams& p, int64_t b, float* w_row,
+                                                    float* m_row) {
+    const int64_t base = b * p.S;
+    float v[2] = {0.0f, 0.0f};
+    for (int64_t s = threadIdx.x; s < p.S; s += kGrpoThreads) {
+        const float m = mask_at(p, base + s);
+        v[0] += (p.logp[base + s] - p.old_logp[base + s]) * m;
+        v[1] += m;
+    }
+    block_sum<2>(v);
+    *m_row = v[1];
+    *w_row = v[0] / fmaxf(v[1], 1.0f);
+}
+
+}  // namespace
+
+// Workspace words per row, and at the end of the row block the batch sums
+// written by klp_grpo_finish_kernel.
+//   row b:  [0] sum loss*m  [1] sum m  [2] sum kl*m  [3] sum low*m
+//           [4] sum high*m
+//   tail :  [0] sum m over the batch
+__global__ __launch_bounds__(kGrpoThreads) void klp_grpo_rows_kernel(GrpoParams p) {
+    const int64_t b = blockIdx.x;
+    const int64_t base = b * p.S;
+    const bool has_ref = p.ref_logp != nullptr && p.beta != 0.0f;
+    float w_row = 0.0f, m_row = 0.0f;
+    if (p.level == KLP_GRPO_SEQUENCE) row_sequence_weight(p, b, &w_row, &m_row);
+    float v[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t s = threadIdx.x; s < p.S; s += kGrpoThreads) {
+        const int64_t i = base + s;
+        const float m = mask_at(p, i);
+        const float lp = p.logp[i];
+        const float w = (p.level == KLP_GRPO_SEQUENCE) ? w_row : lp - p.old_logp[i];
+        const TokenLoss t = token_loss(p, w, adv_at(p, b, i), lp,
+                                       has_ref ? p.ref_logp[i] : 0.0f, has_ref);
+        v[0] += t.loss * m;
+        v[1] += m;
+        v[2] += t.kl * m;
+        v[3] += t.low * m;
+        v[4] += t.high * m;
+    }
+    block_sum<5>(v);
+    if (threadIdx.x == 0) {
+        float* row = p.ws + b * kGrpoRowWords;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) row[k] = v[k];
+    }
+}
+
+// Batch sums in a fixed order: thread j adds rows j, j + 256, ... in order,
+// then the block tree.  loss, then stats = {mean kl, low-clip fraction,
+// high-clip fraction, clipped fraction}, each a masked mean over all tokens.
+__global__ __launch_bounds__(kGrpoThreads) void klp_grpo_finish_kernel(GrpoParams p) {
+    float v[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t b = threadIdx.x; b < p.B; b += kGrpoThreads) {
+        const float* row = p.ws + b * kGrpoRowWords;
+        // "grpo": mean over rows of the row's masked mean.
+        v[0] += row[0] / fmaxf(row[1], 1.0f);
+        v[1] += row[0];
+        v[2] += row[1];
+        v[3] += row[2];
+        v[4] += row[3];
+        v[5] += row[4];
+    }
+    block_sum<6>(v);
+    if (threadIdx.x != 0) return;
+    float loss;
+    if (p.loss_type == KLP_GRPO_LOSS_GRPO) loss = v[0] / static_cast<float>(p.B);
+    else if (p.loss_type == KLP_GRPO_LOSS_BNPO) loss = v[1] / fmaxf(v[2], 1.0f);
+    else loss = v[1] / p.norm_const;
+    const float den = fmaxf(v[2], 1.0f);
+    p.loss[0] = loss;
+    if (p.stats) {
+        p.stats[0] = v[3] / den;
+        p.stats[1] = v[4] / den;
+        p.stats[2] = v[5] / den;
+        p.stats[3] = (v[4] + v[5]) / den;
+    }
+    p.ws[p.B * kGrpoRowWords] = v[2];
+}
+
+// d loss / d lp for every token, times the upstream gradient of the loss
+// (a device scalar, or 1 when null).  Reads the row sums of the forward.
+__global__ __launch_bounds__(kGrpoThreads) void klp_grpo_bwd_kernel(GrpoParams p) {
+    const int64_t b = blockIdx.x;
+    const int64_t base = b * p.S;
+    const bool has_ref = p.ref_logp != nullptr && p.beta != 0.0f;
+    const float g = p.grad_loss ? p.grad_loss[0] : 1.0f;
+    // Weight of a token's loss in the batch loss, per unit mask.
+    float scale;
+    if (p.loss_type == KLP_GRPO_LOSS_GRPO)
+        scale = 1.0f / (static_cast<float>(p.B) * fmaxf(p.ws[b * kGrpoRowWords + 1], 1.0f));
+    else if (p.loss_type == KLP_GRPO_LOSS_BNPO)
+        scale = 1.0f / fmaxf(p.ws[p.B * kGrpoRowWords], 1.0f);
+    else
+        scale = 1.0f / p.norm_const;
+    scale *= g;
+
+    if (p.level == KLP_GRPO_SEQUENCE) {
+        // Every token shares w = sum_s (lp - lo) m / max(sum m, 1): the
+        // ratio term's gradient is (sum_s' scale m_s' dw_s') * m_s / max(sum m, 1).
+        float w_row, m_row;
+        row_sequence_weight(p, b, &w_row, &m_row);
+        float v[1] = {0.0f};
+        for (int64_t s = threadIdx.x; s < p.S; s += kGrpoThreads) {
+            const int64_t i = base + s;
+            const float m = mask_at(p, i);
+            const TokenLoss t = token_loss(p, w_row, adv_at(p, b, i), p.logp[i],
+                                           has_ref ? p.ref_logp[i] : 0.0f, has_ref);
+            v[0] += t.dw * m;
+        }
+        block_sum<1>(v);
+        const float row_term = v[0] * scale / fmaxf(m_row, 1.0f);
+        for (int64_t s = threadIdx.x; s < p.S; s += kGrpoThreads) {
+            const int64_t i = base + s;
+            const float m = mask_at(p, i);
+            const TokenLoss t = token_loss(p, w_row, adv_at(p, b, i), p.logp[i],
+                                           has_ref ? p.ref_logp[i] : 0.0f, has_ref);
+            p.d_logp[i] = row_term * m + t.dlp * m * scale;
+        }
+        return;
+    }
+    for (int64_t s = threadIdx.x; s < p.S; s += kGrpoThreads) {
+        const int64_t i = base + s;
+        const float m = mask_at(p, i);
+        const float lp = p.logp[i];
+        const TokenLoss t = token_loss(p, lp - p.old_logp[i], adv_at(p, b, i), lp,
+                                       has_ref ? p.ref_logp[i] : 0.0f, has_ref);
+        p.d_logp[i] = (t.dw + t.dlp) * m * scale;
+    }
+}
+
+hipError_t launch_grpo_fwd(const GrpoParams& p, hipStream_t stream) {
+    hipError_t e = launch_kernel(klp_grpo_rows_kernel, dim3(static_cast<unsigned>(p.B)),
+                                 dim3(kGrpoThreads), stream, p);
+    if (e != hipSuccess) return e;
+    return launch_kernel(klp_grpo_finish_kernel, dim3(1), dim3(kGrpoThreads), stream, p);
+}
+
+hipError_t launch_grpo_bwd(const GrpoParams& p, hipStream_t stream) {
+    return launch_kernel(klp_grpo_bwd_kernel, dim3(static_cast<unsigned>(p.B)),
+                         dim3(kGrpoThreads), stream, p);
+}
+
+}  // namespace klp

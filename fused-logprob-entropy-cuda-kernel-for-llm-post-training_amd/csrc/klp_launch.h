@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/kernel_opt_hip.h"
 #include "klp_device.h"
 
 namespace klp {
@@ -71,9 +72,36 @@ inline hipError_t launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block,
     return hipGetLastError();
 }
 
+// GRPO loss (klp_grpo.hip).  Arrays are float32 [B, S] unless noted.
+struct GrpoParams {
+    const float* logp;
+    const float* old_logp;
+    const float* ref_logp;   // nullable
+    const float* adv;        // [B], or [B, S] when adv_per_token
+    const float* mask;       // nullable (all ones)
+    int64_t B;
+    int64_t S;
+    float eps_low;
+    float eps_high;
+    float beta;
+    float norm_const;
+    int loss_type;           // klp_grpo_loss_type
+    int level;               // klp_grpo_level
+    int adv_per_token;
+    float* ws;               // [B * kGrpoRowWords + 1]
+    float* loss;             // forward: [1]
+    float* stats;            // forward: [4], nullable
+    const float* grad_loss;  // backward: device scalar, nullable (1)
+    float* d_logp;           // backward: [B, S]
+};
+// Workspace words per row of the GRPO loss (5 used, padded).
+constexpr int kGrpoRowWords = 8;
+
 hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream);
 hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream);
 hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, hipStream_t stream);
+hipError_t launch_grpo_fwd(const GrpoParams& p, hipStream_t stream);
+hipError_t launch_grpo_bwd(const GrpoParams& p, hipStream_t stream);
 bool fwd_config_supported(const FwdConfig& c);
 bool bwd_config_supported(const BwdConfig& c);
 

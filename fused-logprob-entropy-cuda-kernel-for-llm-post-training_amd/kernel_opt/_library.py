@@ -26,6 +26,10 @@ DTYPE_CODES = {torch.bfloat16: KLP_BF16, torch.float16: KLP_FP16, torch.float32:
 # klp_status values
 KLP_OK, KLP_EINVAL, KLP_EDTYPE, KLP_ELAUNCH, KLP_EWORKSPACE = 0, 1, 2, 3, 4
 
+# klp_grpo_loss_type / klp_grpo_level values
+KLP_GRPO_LOSS_GRPO, KLP_GRPO_LOSS_BNPO, KLP_GRPO_LOSS_FIXED = 0, 1, 2
+KLP_GRPO_TOKEN, KLP_GRPO_SEQUENCE = 0, 1
+
 # Every symbol the public headers declare, with its ctypes signature.
 _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
 _ROWS = [_vp, _i32, _i64, _i64, _i64, _i64, _i64]  # logits, dtype, N, V, rows_inner, s_outer, s_inner
@@ -40,6 +44,11 @@ SIGNATURES = {
     "klp_fwd_temp": (_i32, _ROWS + [_vp, ctypes.c_float, _vp, _vp, _vp, _vp, _sz, _vp]),
     "klp_bwd_temp": (_i32, _ROWS + [_vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "klp_debug_fail_next_launches": (None, [_i32]),
+    "klp_grpo_workspace_bytes": (_sz, [_i64]),
+    "klp_grpo_fwd": (_i32, [_vp] * 5 + [_i64, _i64] + [ctypes.c_float] * 4 + [_i32] * 3
+                     + [_vp, _vp, _vp, _sz, _vp]),
+    "klp_grpo_bwd": (_i32, [_vp] * 5 + [_i64, _i64] + [ctypes.c_float] * 4 + [_i32] * 3
+                     + [_vp, _vp, _vp, _sz, _vp]),
     # include/kernel_opt_hip_tuning.h
     "klp_fwd_workspace_bytes_ex": (_sz, [_i64, _i32]),
     "klp_fwd_ex": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _sz, _i32, _i32, _i32, _i32, _vp]),

@@ -155,6 +155,68 @@ int klp_bwd_temp(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                  void* stream);
 
 /*
+ * GRPO policy loss over per-token log-probabilities.  The reference plans it
+ * as kernel "K2 fused_grpo_loss" (notes/PLAN.md:59) but ships it only as
+ * eager PyTorch (examples/compare_one_step.py:232-236, the clipped surrogate
+ * with a masked mean).  These entry points have no counterpart in
+ * csrc/bindings.cpp.
+ *
+ * Inputs are float32, contiguous, [n_seqs, seq_len] (row b = one completion):
+ *   logp      new per-token log-probabilities (the differentiated input);
+ *   old_logp  log-probabilities of the sampling policy;
+ *   ref_logp  reference-model log-probabilities, or NULL (no KL term);
+ *   advantages [n_seqs], or [n_seqs, seq_len] when adv_per_token != 0;
+ *   mask      completion mask (0 / 1 as float), or NULL for all ones.
+ * Per token, with w = logp - old_logp (level KLP_GRPO_TOKEN) or the row's
+ * masked mean of logp - old_logp (KLP_GRPO_SEQUENCE):
+ *   c1 = exp(w), c2 = clamp(c1, 1 - eps_low, 1 + eps_high),
+ *   loss_tok = -min(c1 * A, c2 * A) + beta * (exp(r - logp) - (r - logp) - 1)
+ * with r = ref_logp (the KL term is dropped when ref_logp is NULL or
+ * beta == 0).  The loss is the masked sum of loss_tok divided by:
+ *   KLP_GRPO_LOSS_GRPO   n_seqs * max(row mask sum, 1), row by row;
+ *   KLP_GRPO_LOSS_BNPO   max(batch mask sum, 1);
+ *   KLP_GRPO_LOSS_FIXED  norm_const (> 0).
+ * klp_grpo_fwd writes loss[0] and, if stats != NULL, stats[0..3] = masked
+ * means of the KL estimate, of "clipped low" (c1 < 1 - eps_low and A < 0),
+ * of "clipped high" (c1 > 1 + eps_high and A > 0), and of either.
+ * klp_grpo_bwd writes d_logp = grad_loss[0] * d loss / d logp (grad_loss is
+ * a device scalar, NULL meaning 1).  It reads the row sums klp_grpo_fwd left
+ * in `workspace`: pass the same workspace, unchanged, with the same inputs.
+ * Both need a workspace of klp_grpo_workspace_bytes(n_seqs) bytes, 4-byte
+ * aligned, without initialisation.  eps_low and eps_high must be >= 0.
+ */
+typedef enum klp_grpo_loss_type {
+    KLP_GRPO_LOSS_GRPO = 0,
+    KLP_GRPO_LOSS_BNPO = 1,
+    KLP_GRPO_LOSS_FIXED = 2
+} klp_grpo_loss_type;
+
+typedef enum klp_grpo_level {
+    KLP_GRPO_TOKEN = 0,
+    KLP_GRPO_SEQUENCE = 1
+} klp_grpo_level;
+
+size_t klp_grpo_workspace_bytes(int64_t n_seqs);
+
+int klp_grpo_fwd(const float* logp, const float* old_logp, const float* ref_logp,
+                 const float* advantages, const float* mask,
+                 int64_t n_seqs, int64_t seq_len,
+                 float eps_low, float eps_high, float beta, float norm_const,
+                 int loss_type, int level, int adv_per_token,
+                 float* loss, float* stats,
+                 void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp,
+                 const float* advantages, const float* mask,
+                 int64_t n_seqs, int64_t seq_len,
+                 float eps_low, float eps_high, float beta, float norm_const,
+                 int loss_type, int level, int adv_per_token,
+                 const float* grad_loss, float* d_logp,
+                 void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+/*
  * Test hook with no counterpart in the reference: the next `count` compute
  * calls on the calling thread return KLP_ELAUNCH without launching anything,
  * as if hipGetLastError() had reported a failure.  Lets the error path be

@@ -17,6 +17,13 @@ TEST INFRASTRUCTURE ONLY (tests/, smoke(), bench.py's cpu_baseline leg).
   Its outputs are not pinned against TRL itself (TRL cannot be imported
   here); it serves as the CPU baseline that is timed, not as a correctness
   oracle.
+* ``reference_grpo_loss`` — the reference's GRPO loss, verbatim in meaning
+  (examples/compare_one_step.py:232-236).
+* ``eager_grpo_loss``     — the generalised GRPO loss of klp_grpo_fwd as a
+  chain of eager torch ops (the form TRL's GRPOTrainer writes it in; its
+  variants beyond the reference's formula are not pinned against TRL, which
+  is absent here).  Differentiated by torch autograd, it pins the gradient
+  of oracle/grpo_oracle.py independently of that hand derivation.
 """
 from __future__ import annotations
 
@@ -68,3 +75,41 @@ def trl_entropy_from_logits(logits: torch.Tensor, chunk_size: int = 128) -> torc
 def trl_eager(logits: torch.Tensor, targets: torch.Tensor):
     """The eager forward the fused kernel replaces: (logp, entropy)."""
     return trl_selective_log_softmax(logits, targets), trl_entropy_from_logits(logits)
+
+
+def reference_grpo_loss(new_logp, old_logp, advantages, mask, eps_clip=0.2):
+    ratio = (new_logp - old_logp).exp()
+    surr = -torch.minimum(ratio * advantages,
+                          ratio.clamp(1 - eps_clip, 1 + eps_clip) * advantages)
+    return (surr * mask).sum() / mask.sum()
+
+
+def eager_grpo_loss(logp, old_logp, advantages, mask=None, ref_logp=None, eps_low=0.2,
+                    eps_high=None, beta=0.0, loss_type="bnpo", level="token", norm_const=1.0):
+    eh = eps_low if eps_high is None else eps_high
+    m = torch.ones_like(logp) if mask is None else mask
+    A = advantages.unsqueeze(1) if advantages.dim() == 1 else advantages
+    log_ratio = logp - old_logp
+    if level == "sequence":
+        w = ((log_ratio * m).sum(-1) / m.sum(-1).clamp(min=1.0)).unsqueeze(-1)
+    else:
+        w = log_ratio
+    coef_1 = torch.exp(w)
+    coef_2 = torch.clamp(coef_1, 1 - eps_low, 1 + eh)
+    per_token = -torch.min(coef_1 * A, coef_2 * A)
+    kl = torch.zeros_like(logp)
+    if ref_logp is not None and beta != 0.0:
+        kl = torch.exp(ref_logp - logp) - (ref_logp - logp) - 1
+        per_token = per_token + beta * kl
+    if loss_type == "grpo":
+        loss = ((per_token * m).sum(-1) / m.sum(-1).clamp(min=1.0)).mean()
+    elif loss_type == "bnpo":
+        loss = (per_token * m).sum() / m.sum().clamp(min=1.0)
+    else:
+        loss = (per_token * m).sum() / norm_const
+    den = m.sum().clamp(min=1.0)
+    low = ((coef_1 < 1 - eps_low) & (A < 0)).to(logp.dtype)
+    high = ((coef_1 > 1 + eh) & (A > 0)).to(logp.dtype)
+    stats = torch.stack([(kl * m).sum() / den, (low * m).sum() / den, (high * m).sum() / den,
+                         ((low + high) * m).sum() / den])
+    return loss, stats.detach()

@@ -206,3 +206,36 @@ def test_torch_library_ops_registered():
     bwd = str(torch.ops.kernel_opt.fused_logprob_entropy_backward.default._schema)
     assert "float temperature" in fwd and "-> (Tensor, Tensor, Tensor)" in fwd
     assert "Tensor? g_logp" in bwd and bwd.endswith("-> Tensor")
+
+
+def test_grpo_validation_errors():
+    from kernel_opt._library import KLP_EINVAL, KLP_ELAUNCH, KLP_EWORKSPACE, lib
+    ws = lib.klp_grpo_workspace_bytes(4)
+    assert ws == (4 * 8 + 1) * 4 and lib.klp_grpo_workspace_bytes(0) == 0
+
+    def fwd(**kw):
+        a = dict(logp=P, old=P, ref=None, adv=P, mask=None, B=4, S=10, el=0.2, eh=0.2, beta=0.0,
+                 norm=1.0, kind=1, level=0, per_tok=0, loss=P, stats=None, ws=P, ws_bytes=ws)
+        a.update(kw)
+        return lib.klp_grpo_fwd(a["logp"], a["old"], a["ref"], a["adv"], a["mask"], a["B"],
+                                a["S"], a["el"], a["eh"], a["beta"], a["norm"], a["kind"],
+                                a["level"], a["per_tok"], a["loss"], a["stats"], a["ws"],
+                                a["ws_bytes"], None)
+    assert fwd(B=0) == KLP_EINVAL and "n_seqs" in _err()
+    assert fwd(S=-1) == KLP_EINVAL
+    assert fwd(logp=None) == KLP_EINVAL and "logp" in _err()
+    assert fwd(el=-0.1) == KLP_EINVAL and "eps_low" in _err()
+    assert fwd(beta=float("nan")) == KLP_EINVAL and "beta" in _err()
+    assert fwd(kind=7) == KLP_EINVAL and "loss_type" in _err()
+    assert fwd(kind=2, norm=0.0) == KLP_EINVAL and "norm_const" in _err()
+    assert fwd(level=3) == KLP_EINVAL and "level" in _err()
+    assert fwd(ws_bytes=ws - 4) == KLP_EWORKSPACE and "workspace" in _err()
+    assert fwd(loss=None) == KLP_EINVAL and "loss" in _err()
+    lib.klp_debug_fail_next_launches(1)
+    try:
+        assert fwd() == KLP_ELAUNCH and "grpo forward" in _err()
+    finally:
+        lib.klp_debug_fail_next_launches(0)
+    rc = lib.klp_grpo_bwd(P, P, None, P, None, 4, 10, 0.2, 0.2, 0.0, 1.0, 1, 0, 0, None, None,
+                          P, ws, None)
+    assert rc == KLP_EINVAL and "d_logp" in _err()
