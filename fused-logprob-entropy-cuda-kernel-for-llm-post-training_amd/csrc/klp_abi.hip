@@ -306,6 +306,25 @@ int grpo_setup(const float* logp, const float* old_logp, const float* ref_logp,
     return KLP_OK;
 }
 
+// Fused LM head: vocab tiles per workgroup chunk, chosen so that the grid
+// holds about four rounds of one workgroup per CU (256 CUs).
+void lmh_plan(int64_t n_tokens, int64_t vocab, int64_t* tiles_per_chunk, int64_t* n_chunks) {
+    const int64_t tb = klp::lmh_token_blocks(n_tokens);
+    const int64_t vt = klp::lmh_vocab_tiles(vocab);
+    int64_t tpc = (tb * vt) / (256 * 4);
+    if (tpc < 1) tpc = 1;
+    if (tpc > 16) tpc = 16;
+    *tiles_per_chunk = tpc;
+    *n_chunks = (vt + tpc - 1) / tpc;
+}
+
+size_t lmh_workspace_bytes(int64_t n_tokens, int64_t vocab) {
+    if (n_tokens <= 0 || vocab <= 0) return 0;
+    int64_t tpc, nc;
+    lmh_plan(n_tokens, vocab, &tpc, &nc);
+    return static_cast<size_t>(nc) * static_cast<size_t>(n_tokens) * 4 * sizeof(float);
+}
+
 }  // namespace
 
 extern "C" {
@@ -474,6 +493,68 @@ int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp
     if (injected_failure("grpo backward")) return KLP_ELAUNCH;
     return after_launch(klp::launch_grpo_bwd(p, static_cast<hipStream_t>(stream)),
                         "grpo backward");
+}
+
+size_t klp_lmh_workspace_bytes(int64_t n_tokens, int64_t vocab, int64_t dim) {
+    (void)dim;
+    return lmh_workspace_bytes(n_tokens, vocab);
+}
+
+int klp_lmh_fwd(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight,
+                int64_t n_tokens, int64_t vocab, int64_t dim, const int64_t* targets,
+                float temperature, float* logprob, float* entropy, float* lse, void* workspace,
+                size_t workspace_bytes, void* stream) {
+    if (n_tokens < 0) return fail(KLP_EINVAL, "n_tokens must be >= 0");
+    if (vocab < 1) return fail(KLP_EINVAL, "vocab must be >= 1, got %lld",
+                               static_cast<long long>(vocab));
+    if (dim < 64 || dim % 64 != 0)
+        return fail(KLP_EINVAL, "dim must be a positive multiple of 64, got %lld",
+                    static_cast<long long>(dim));
+    if (ld_hidden < dim || ld_weight < dim || ld_hidden % 8 != 0 || ld_weight % 8 != 0)
+        return fail(KLP_EINVAL, "row strides must be >= dim and multiples of 8 elements");
+    if (n_tokens > (int64_t{1} << 31) - 1 || vocab > (int64_t{1} << 31) - 1)
+        return fail(KLP_EINVAL, "n_tokens and vocab must be below 2^31");
+    float scale;
+    if (!scale_from_temperature(temperature, &scale)) return KLP_EINVAL;
+    if (n_tokens == 0) return ok();
+    if (hidden == nullptr || weight == nullptr || targets == nullptr)
+        return fail(KLP_EINVAL, "hidden, weight and targets must be non-null");
+    if (!aligned(hidden, 16) || !aligned(weight, 16))
+        return fail(KLP_EINVAL, "hidden and weight must be 16-byte aligned");
+    if (!aligned(targets, 8)) return fail(KLP_EINVAL, "targets pointer is not 8-byte aligned");
+    int rc;
+    if ((rc = check_f32(logprob, "logprob")) != KLP_OK) return rc;
+    if ((rc = check_f32(entropy, "entropy")) != KLP_OK) return rc;
+    if ((rc = check_f32(lse, "lse")) != KLP_OK) return rc;
+    const size_t need = lmh_workspace_bytes(n_tokens, vocab);
+    if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 16))
+        return fail(KLP_EWORKSPACE,
+                    "workspace missing, too small or not 16-byte aligned: have %zu bytes, need %zu",
+                    workspace_bytes, need);
+    klp::LmhParams p;
+    p.hidden = static_cast<const uint16_t*>(hidden);
+    p.ld_hidden = ld_hidden;
+    p.weight = static_cast<const uint16_t*>(weight);
+    p.ld_weight = ld_weight;
+    p.n_tokens = n_tokens;
+    p.vocab = vocab;
+    p.dim = dim;
+    p.targets = targets;
+    p.scale = scale;
+    p.partials = static_cast<float*>(workspace);
+    p.n_tblocks = klp::lmh_token_blocks(n_tokens);
+    p.n_vtiles = klp::lmh_vocab_tiles(vocab);
+    lmh_plan(n_tokens, vocab, &p.tiles_per_chunk, &p.n_chunks);
+    p.logprob = logprob;
+    p.entropy = entropy;
+    p.lse = lse;
+    const int64_t blocks = (p.n_chunks + 7) / 8 * 8 * p.n_tblocks;
+    if (blocks > (int64_t{1} << 31) - 1)
+        return fail(KLP_EINVAL, "grid of %lld workgroups is too large",
+                    static_cast<long long>(blocks));
+    if (injected_failure("lm-head forward")) return KLP_ELAUNCH;
+    return after_launch(klp::launch_lmh_fwd(p, static_cast<hipStream_t>(stream)),
+                        "lm-head forward");
 }
 
 }  // extern "C"

@@ -97,6 +97,30 @@ struct GrpoParams {
 // Workspace words per row of the GRPO loss (5 used, padded).
 constexpr int kGrpoRowWords = 8;
 
+// Fused LM head forward (klp_lmhead.hip).
+struct LmhParams {
+    const uint16_t* hidden;  // bf16 [n_tokens, ld_hidden], first `dim` columns used
+    int64_t ld_hidden;
+    const uint16_t* weight;  // bf16 [vocab, ld_weight]
+    int64_t ld_weight;
+    int64_t n_tokens;
+    int64_t vocab;
+    int64_t dim;             // K, a multiple of 64
+    const int64_t* targets;  // [n_tokens]
+    float scale;             // 1 / temperature
+    float* partials;         // [n_chunks, n_tokens] float4 (m, z, t, target logit)
+    int64_t n_tblocks;       // ceil(n_tokens / 128)
+    int64_t n_vtiles;        // ceil(vocab / 256)
+    int64_t tiles_per_chunk;
+    int64_t n_chunks;        // ceil(n_vtiles / tiles_per_chunk)
+    float* logprob;
+    float* entropy;
+    float* lse;
+};
+int64_t lmh_token_blocks(int64_t n_tokens);
+int64_t lmh_vocab_tiles(int64_t vocab);
+hipError_t launch_lmh_fwd(const LmhParams& p, hipStream_t stream);
+
 hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream);
 hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream);
 hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, hipStream_t stream);

@@ -44,6 +44,9 @@ SIGNATURES = {
     "klp_fwd_temp": (_i32, _ROWS + [_vp, ctypes.c_float, _vp, _vp, _vp, _vp, _sz, _vp]),
     "klp_bwd_temp": (_i32, _ROWS + [_vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "klp_debug_fail_next_launches": (None, [_i32]),
+    "klp_lmh_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "klp_lmh_fwd": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, ctypes.c_float,
+                           _vp, _vp, _vp, _vp, _sz, _vp]),
     "klp_grpo_workspace_bytes": (_sz, [_i64]),
     "klp_grpo_fwd": (_i32, [_vp] * 5 + [_i64, _i64] + [ctypes.c_float] * 4 + [_i32] * 3
                      + [_vp, _vp, _vp, _sz, _vp]),

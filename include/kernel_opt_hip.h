@@ -217,6 +217,30 @@ int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp
                  void* stream);
 
 /*
+ * Fused LM head + per-token logprob / entropy, forward.  No counterpart in the
+ * reference, which names it as its follow-up (a Liger-style fused linear +
+ * loss, docs/FINAL_REPORT.md:439-450): instead of logits = hidden @ weight^T
+ * followed by klp_fwd, one MFMA GEMM folds each block of logits into the
+ * online softmax state as it is produced, so the [n_tokens, vocab] logits
+ * are never written.
+ *   hidden  bf16 [n_tokens, ld_hidden] (first `dim` columns), 16-byte aligned;
+ *   weight  bf16 [vocab, ld_weight] (nn.Linear layout), 16-byte aligned;
+ *   dim a positive multiple of 64; ld_hidden, ld_weight >= dim, multiples of 8;
+ *   targets int64 [n_tokens]; outputs float32 [n_tokens] as klp_fwd;
+ *   temperature T > 0: logits are fp32(sum) * fp32(1/T).
+ * Logits are the fp32 MFMA sums (not rounded to bf16 as a bf16 GEMM output
+ * would be).  The workspace (klp_lmh_workspace_bytes bytes, 16-byte aligned,
+ * no initialisation) holds per-(token, vocab chunk) partial states; launches
+ * sharing one must be ordered on one stream.
+ */
+size_t klp_lmh_workspace_bytes(int64_t n_tokens, int64_t vocab, int64_t dim);
+
+int klp_lmh_fwd(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight,
+                int64_t n_tokens, int64_t vocab, int64_t dim, const int64_t* targets,
+                float temperature, float* logprob, float* entropy, float* lse,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Test hook with no counterpart in the reference: the next `count` compute
  * calls on the calling thread return KLP_ELAUNCH without launching anything,
  * as if hipGetLastError() had reported a failure.  Lets the error path be

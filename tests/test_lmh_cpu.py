@@ -1,0 +1,69 @@
+"""CPU pins of the float64 LM-head oracle (oracle/lmh_oracle.py)."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from oracle import lmh_oracle
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16).view(torch.int16) \
+        .numpy().view(np.uint16)
+
+
+def test_matches_c_oracle_on_exact_integer_logits(oracle):
+    """Small-integer hidden / weight: every logit is an integer below 2^24,
+    exact in fp32, so the C oracle of the logprob forward sees the same
+    logits and must agree to float64 rounding."""
+    g = np.random.default_rng(1)
+    N, V, D = 9, 777, 64
+    h = bf16_bits(g.integers(-3, 4, (N, D)))
+    w = bf16_bits(g.integers(-2, 3, (V, D)))
+    t = g.integers(-2, V + 2, N)
+    lp, ent, lse = lmh_oracle.forward(h, w, t)
+    x = lmh_oracle.logits(h, w).astype(np.float32)
+    assert np.array_equal(x.astype(np.float64), lmh_oracle.logits(h, w))
+    r_lp, r_ent, r_lse = oracle.forward(x, t, dtype="fp32")
+    np.testing.assert_allclose(lp, r_lp, rtol=0, atol=1e-12)
+    np.testing.assert_allclose(ent, r_ent, rtol=0, atol=1e-12)
+    np.testing.assert_allclose(lse, r_lse, rtol=0, atol=1e-12)
+
+
+def test_matches_python_loop():
+    g = np.random.default_rng(2)
+    N, V, D = 3, 7, 64
+    h = bf16_bits(g.normal(0, 1, (N, D)))
+    w = bf16_bits(g.normal(0, 0.3, (V, D)))
+    t = np.array([0, 6, 3])
+    lp, ent, lse = lmh_oracle.forward(h, w, t, temperature=0.7)
+    hf, wf = lmh_oracle.bf16_to_f64(h), lmh_oracle.bf16_to_f64(w)
+    s = float(np.float32(1 / 0.7))
+    for n in range(N):
+        xs = [math.fsum(hf[n, k] * wf[v, k] for k in range(D)) * s for v in range(V)]
+        m = max(xs)
+        z = math.fsum(math.exp(x - m) for x in xs)
+        l = m + math.log(z)
+        e = l - math.fsum(math.exp(x - l) * x for x in xs)
+        assert abs(lse[n] - l) < 1e-12 and abs(ent[n] - e) < 1e-12
+        assert abs(lp[n] - (xs[t[n]] - l)) < 1e-12
+
+
+def test_uniform_rows_closed_form():
+    g = np.random.default_rng(3)
+    N, V, D = 4, 1000, 128
+    h = bf16_bits(g.normal(0, 1, (N, D)))
+    w = np.tile(bf16_bits(g.normal(0, 0.1, (1, D))), (V, 1))
+    lp, ent, lse = lmh_oracle.forward(h, w, np.zeros(N, np.int64))
+    np.testing.assert_allclose(ent, math.log(V), rtol=0, atol=1e-12)
+    np.testing.assert_allclose(lp, -math.log(V), rtol=0, atol=1e-12)
+
+
+def test_out_of_range_targets_give_minus_lse():
+    g = np.random.default_rng(4)
+    h = bf16_bits(g.normal(0, 1, (3, 64)))
+    w = bf16_bits(g.normal(0, 0.2, (50, 64)))
+    lp, _, lse = lmh_oracle.forward(h, w, np.array([-100, 50, 1000]))
+    np.testing.assert_array_equal(lp, -lse)
