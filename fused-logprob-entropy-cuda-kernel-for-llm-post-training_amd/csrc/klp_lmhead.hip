@@ -9,19 +9,21 @@
 // without writing the [N, V] logits anywhere.  hidden is bf16 [N, D] and
 // weight bf16 [V, D] (nn.Linear's layout), both K-contiguous.
 //
-// klp_lmh_fwd_kernel: one workgroup (4 waves) per (token block of 128,
-// vocab chunk of `tiles_per_chunk` tiles of 256 rows).  Per vocab tile it
-// computes the 256 x 128 block of logits^T with v_mfma_f32_32x32x16_bf16:
+// klp_lmh_fwd_kernel: one workgroup (4 waves, 2 x 2) per (token block of
+// 256, vocab chunk of `tiles_per_chunk` tiles of 256 rows).  Per vocab tile
+// it computes the 256 x 256 block of logits^T with v_mfma_f32_32x32x16_bf16,
+// each wave a 128 x 128 part of it (16 accumulator blocks, 256 AGPRs):
 //  - the transposed orientation puts vocab rows on the MFMA's M side, so a
 //    lane's 16 accumulator values all belong to one token (its N column):
 //    the online softmax update runs lane-locally, with no cross-lane
 //    reduction until the end of the chunk;
-//  - K advances in steps of 64 through two LDS buffers (48 KB each):
-//    global loads for step s+1 are issued into registers before step s is
-//    multiplied, and written to the other buffer after it;
-//  - LDS rows are 128 bytes; the 16-byte chunk index is XOR-swizzled with
-//    the row index so that the MFMA operand reads of 8 consecutive rows hit
-//    8 different bank groups;
+//  - K advances in steps of 32 through a ring of 5 LDS stages (32 KB each,
+//    all 160 KB of LDS), filled by direct global -> LDS copies
+//    (global_load_lds_dwordx4, no register staging) issued 4 stages ahead of
+//    the multiply; the ring runs across tile boundaries;
+//  - LDS rows are 64 bytes; the 16-byte chunk index is XOR-swizzled with
+//    the row index so that the MFMA operand reads of 8 consecutive rows
+//    cover all 32 banks once;
 //  - after each tile the block's logits are folded into per-lane
 //    (m, z, t) states (absorb() of klp_device.h) and the target logit is
 //    captured if it lies in the tile.
@@ -43,31 +45,75 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBV = 256;     // vocab rows per tile
-constexpr int kBT = 128;     // tokens per block
-constexpr int kBK = 64;      // K per LDS stage
+constexpr int kVB = 4;              // 32-row vocab blocks per wave
+constexpr int kTB = 4;              // 32-token blocks per wave
+constexpr int kBV = 2 * kVB * 32;   // vocab rows per tile (2 waves along vocab): 256
+constexpr int kBT = 2 * kTB * 32;   // tokens per block (2 waves along tokens): 256
+#ifndef KLP_LMH_BK
+#define KLP_LMH_BK 32
+#endif
+#ifndef KLP_LMH_RING
+#define KLP_LMH_RING 5
+#endif
+#ifndef KLP_LMH_AUX
+#define KLP_LMH_AUX 0
+#endif
+constexpr int kBK = KLP_LMH_BK;     // K per LDS stage
+constexpr int kRing = KLP_LMH_RING; // LDS stages (prefetch distance kRing - 1)
 constexpr int kThreads = 256;
-constexpr int kRowBytes = kBK * 2;                       // 128
-constexpr int kStageBytes = (kBV + kBT) * kRowBytes;     // 48 KB
-constexpr int kWChunks = kBV * kRowBytes / 16 / kThreads;  // 16-byte loads per thread: 8
-constexpr int kHChunks = kBT * kRowBytes / 16 / kThreads;  // 4
+constexpr int kRowBytes = kBK * 2;
+constexpr int kChunksPerRow = kRowBytes / 16;
+constexpr int kWBytes = kBV * kRowBytes;
+constexpr int kStageBytes = (kBV + kBT) * kRowBytes;
+// One global_load_lds_dwordx4 moves 64 lanes x 16 B = 1 KB of LDS rows.
+constexpr int kRowsPerCopy = 1024 / kRowBytes;
+constexpr int kWCopies = kBV / kRowsPerCopy / (kThreads / 64);    // per wave per stage
+constexpr int kHCopies = kBT / kRowsPerCopy / (kThreads / 64);
+constexpr int kCopiesPerStage = kWCopies + kHCopies;              // vmcnt units per stage
+static_assert(kRing * kStageBytes <= 160 * 1024, "LDS holds 160 KB");
+static_assert(kCopiesPerStage * (kRing - 2) <= 63, "vmcnt counts up to 63");
 
-__device__ __forceinline__ int swz(int row, int chunk) {
-    return row * kRowBytes + ((chunk ^ (row & 7)) << 4);
+// LDS byte offset of 16-byte chunk `c` of row `row`.  The chunk index is
+// XOR-swizzled with f(row) (bits 0..3 of the row only): the MFMA operand
+// reads (one chunk of 16 consecutive rows per pass) are then free of bank
+// conflicts whether the LDS serves 8 or 16 lanes x 16 B per cycle.
+__device__ __forceinline__ int swz_f(int row) {
+    if constexpr (kChunksPerRow == 4) return ((row >> 1) & 3) ^ ((row >> 3) & 1);
+    else return (row & 7) ^ ((row >> 3) & 1);
+}
+__device__ __forceinline__ int swz(int row, int c) {
+    return row * kRowBytes + ((c ^ swz_f(row)) << 4);
+}
+
+// s_waitcnt with vmcnt = n (0..63) and no wait on the other counters.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Wait until at most min(N, ahead) stages of copies issued after the
+// current one are outstanding (vmcnt takes an immediate, hence the chain).
+template <int N>
+__device__ __forceinline__ void wait_stages(int ahead) {
+    if constexpr (N > 0) {
+        if (ahead >= N) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(N * kCopiesPerStage));
+            return;
+        }
+        wait_stages<N - 1>(ahead);
+    } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    }
 }
 
 }  // namespace
 
 __global__ __launch_bounds__(kThreads) void klp_lmh_fwd_kernel(LmhParams p) {
-    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kStageBytes];
-    __shared__ Stat merge_stat[2][kBT];
-    __shared__ float merge_xt[2][kBT];
+    // The ring takes all 160 KB of LDS; the end-of-chunk merge reuses it.
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[kRing * kStageBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wv = wave & 1;   // vocab half (128 rows) of the tile
-    const int wt = wave >> 1;  // token half (64 tokens) of the block
+    const int wt = wave >> 1;  // token half (128 tokens) of the block
 
     // Workgroup -> (token block, vocab chunk), XCD-aware (see above).
     const int64_t bid = blockIdx.x;
@@ -78,141 +124,142 @@ __global__ __launch_bounds__(kThreads) void klp_lmh_fwd_kernel(LmhParams p) {
     if (chunk >= p.n_chunks) return;  // padding workgroups of the last round
 
     const int64_t tok0 = tb * kBT;
-    const int64_t K = p.dim;
-    const int n_ksteps = static_cast<int>(K / kBK);
-
-    // This thread's global -> LDS copy slots: 16-byte chunk c of the stage,
-    // row c / 8, column chunk c % 8.
-    const uint16_t* hbase[kHChunks];
-    bool hvalid[kHChunks];
-#pragma unroll
-    for (int j = 0; j < kHChunks; ++j) {
-        const int c = tid + j * kThreads;
-        const int64_t n = tok0 + c / 8;
-        hvalid[j] = n < p.n_tokens;
-        hbase[j] = p.hidden + (hvalid[j] ? n : 0) * p.ld_hidden + (c % 8) * 8;
-    }
-
-    // Per-lane states for the lane's two tokens (token block column
-    // wt*64 + j*32 + lane%32, j = 0, 1).
-    Stat st[2] = {stat_empty(), stat_empty()};
-    float xt[2] = {0.0f, 0.0f};
-    int64_t my_tok[2], my_tgt[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        my_tok[j] = tok0 + wt * 64 + j * 32 + (lane & 31);
-        my_tgt[j] = (my_tok[j] < p.n_tokens) ? p.targets[my_tok[j]] : -1;
-    }
-
+    const int n_ksteps = static_cast<int>(p.dim / kBK);
     const int64_t tile_first = chunk * p.tiles_per_chunk;
     int64_t tile_end = tile_first + p.tiles_per_chunk;
     if (tile_end > p.n_vtiles) tile_end = p.n_vtiles;
+    const int n_stages = static_cast<int>(tile_end - tile_first) * n_ksteps;
 
-    for (int64_t vt = tile_first; vt < tile_end; ++vt) {
-        const int64_t v0 = vt * kBV;
-        const uint16_t* wbase[kWChunks];
-        bool wvalid[kWChunks];
+    // Copy slots.  Copy q of the W part covers tile rows q * kRowsPerCopy ..
+    // + kRowsPerCopy - 1; this wave issues q = wave + 4j.  Lane l fills LDS
+    // row q * kRowsPerCopy + l / kChunksPerRow, chunk l % kChunksPerRow, which
+    // holds global chunk (l % kChunksPerRow) ^ swz_f(row) of that row (swz_f
+    // reads row bits 0..3, the same for every j).  Rows past the end of the
+    // matrix are clamped to its last row (valid memory; their logits are
+    // masked or their outputs never written).
+    const int lrow = lane / kChunksPerRow;
+    const int gchunk = (lane % kChunksPerRow) ^ swz_f(wave * kRowsPerCopy + lrow);
+    const uint16_t* hsrc[kHCopies];
 #pragma unroll
-        for (int j = 0; j < kWChunks; ++j) {
-            const int c = tid + j * kThreads;
-            const int64_t v = v0 + c / 8;
-            wvalid[j] = v < p.vocab;
-            wbase[j] = p.weight + (wvalid[j] ? v : 0) * p.ld_weight + (c % 8) * 8;
+    for (int j = 0; j < kHCopies; ++j) {
+        int64_t n = tok0 + (wave + 4 * j) * kRowsPerCopy + lrow;
+        if (n > p.n_tokens - 1) n = p.n_tokens - 1;
+        hsrc[j] = p.hidden + n * p.ld_hidden + gchunk * 8;
+    }
+
+    Stat st[kTB];
+    float xt[kTB];
+    int64_t my_tgt[kTB];
+#pragma unroll
+    for (int j = 0; j < kTB; ++j) {
+        st[j] = stat_empty();
+        xt[j] = 0.0f;
+        const int64_t tok = tok0 + wt * (kTB * 32) + j * 32 + (lane & 31);
+        my_tgt[j] = (tok < p.n_tokens) ? p.targets[tok] : -1;
+    }
+
+    // Issue the copies of global stage g (tile tile_first + g / n_ksteps,
+    // K step g % n_ksteps) into ring slot g % kRing.
+    auto issue = [&](int g) {
+        const int64_t vt = tile_first + g / n_ksteps;
+        const int64_t koff = static_cast<int64_t>(g % n_ksteps) * kBK;
+        unsigned char* dst = lds + (g % kRing) * kStageBytes;
+#pragma unroll
+        for (int j = 0; j < kWCopies; ++j) {
+            const int q = wave + 4 * j;
+            int64_t v = vt * kBV + q * kRowsPerCopy + lrow;
+            if (v > p.vocab - 1) v = p.vocab - 1;
+            __builtin_amdgcn_global_load_lds(p.weight + v * p.ld_weight + gchunk * 8 + koff,
+                                             dst + q * 1024, 16, 0, KLP_LMH_AUX);
         }
+#pragma unroll
+        for (int j = 0; j < kHCopies; ++j) {
+            const int q = wave + 4 * j;
+            __builtin_amdgcn_global_load_lds(hsrc[j] + koff, dst + kWBytes + q * 1024, 16, 0,
+                                             KLP_LMH_AUX);
+        }
+    };
 
-        f32x16 acc[4][2];
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+    for (int g = 0; g < kRing - 1; ++g)
+        if (g < n_stages) issue(g);
+
+    int g = 0;  // global stage index, runs across tiles
+    for (int64_t vt = tile_first; vt < tile_end; ++vt) {
+        f32x16 acc[kVB][kTB];
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+        for (int a = 0; a < kVB; ++a)
+#pragma unroll
+            for (int b = 0; b < kTB; ++b)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
-        u32x4 wreg[kWChunks], hreg[kHChunks];
-        auto gload = [&](int ks) {
-            const int64_t koff = static_cast<int64_t>(ks) * kBK;
-#pragma unroll
-            for (int j = 0; j < kWChunks; ++j)
-                wreg[j] = wvalid[j] ? *reinterpret_cast<const u32x4*>(wbase[j] + koff)
-                                    : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int j = 0; j < kHChunks; ++j)
-                hreg[j] = hvalid[j] ? *reinterpret_cast<const u32x4*>(hbase[j] + koff)
-                                    : u32x4{0u, 0u, 0u, 0u};
-        };
-        auto lstore = [&](int buf) {
-            unsigned char* base = lds + buf * kStageBytes;
-#pragma unroll
-            for (int j = 0; j < kWChunks; ++j) {
-                const int c = tid + j * kThreads;
-                *reinterpret_cast<u32x4*>(base + swz(c / 8, c % 8)) = wreg[j];
-            }
-#pragma unroll
-            for (int j = 0; j < kHChunks; ++j) {
-                const int c = tid + j * kThreads;
-                *reinterpret_cast<u32x4*>(base + kBV * kRowBytes + swz(c / 8, c % 8)) = hreg[j];
-            }
-        };
-        auto compute = [&](int buf) {
-            const unsigned char* wl = lds + buf * kStageBytes;
-            const unsigned char* hl = wl + kBV * kRowBytes;
+        for (int ks_stage = 0; ks_stage < n_ksteps; ++ks_stage, ++g) {
+            // Stage g has landed once at most the copies of the stages issued
+            // after it (up to kRing - 2 of them) are outstanding; then the
+            // barrier makes every wave's copies visible and frees slot
+            // (g - 1) % kRing for the copies of stage g + kRing - 1.
+            wait_stages<kRing - 2>(n_stages - 1 - g);
+            __builtin_amdgcn_s_barrier();
+            if (g + kRing - 1 < n_stages) issue(g + kRing - 1);
+
+            const unsigned char* wl = lds + (g % kRing) * kStageBytes;
+            const unsigned char* hl = wl + kWBytes;
 #pragma unroll
             for (int ks = 0; ks < kBK / 16; ++ks) {
-                const int ch = ks * 2 + (lane >> 5);
-                bf16x8 af[4], bfr[2];
+                const int c = ks * 2 + (lane >> 5);
+                bf16x8 af[kVB], bfr[kTB];
 #pragma unroll
-                for (int a = 0; a < 4; ++a) {
-                    const int row = wv * 128 + a * 32 + (lane & 31);
-                    af[a] = *reinterpret_cast<const bf16x8*>(wl + swz(row, ch));
-                }
+                for (int a = 0; a < kVB; ++a)
+                    af[a] = *reinterpret_cast<const bf16x8*>(
+                        wl + swz(wv * (kVB * 32) + a * 32 + (lane & 31), c));
 #pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const int row = wt * 64 + b * 32 + (lane & 31);
-                    bfr[b] = *reinterpret_cast<const bf16x8*>(hl + swz(row, ch));
-                }
+                for (int b = 0; b < kTB; ++b)
+                    bfr[b] = *reinterpret_cast<const bf16x8*>(
+                        hl + swz(wt * (kTB * 32) + b * 32 + (lane & 31), c));
 #pragma unroll
-                for (int a = 0; a < 4; ++a)
+                for (int a = 0; a < kVB; ++a)
 #pragma unroll
-                    for (int b = 0; b < 2; ++b)
+                    for (int b = 0; b < kTB; ++b)
                         acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b],
                                                                            acc[a][b], 0, 0, 0);
             }
-        };
-
-        gload(0);
-        lstore(0);
-        __syncthreads();
-        for (int ks = 0; ks < n_ksteps; ++ks) {
-            const int buf = ks & 1;
-            if (ks + 1 < n_ksteps) gload(ks + 1);
-            compute(buf);
-            if (ks + 1 < n_ksteps) lstore(buf ^ 1);
-            __syncthreads();
         }
 
-        // Fold the tile into the lane's token states.  Accumulator r of block
-        // (a, b) holds vocab row v0 + wv*128 + a*32 + 8*(r/4) + 4*(lane/32) + r%4.
+        // Tile done: fold it into the lane's token states, one 32-row block
+        // at a time.  Accumulator r of block (a, b) holds tile row
+        // wv*128 + a*32 + 8*(r/4) + 4*(lane/32) + r%4 (vocab row v0 + that).
+        const int64_t v0 = vt * kBV;
+        const int64_t vlim64 = p.vocab - v0;
+        const int vlim = vlim64 < kBV ? static_cast<int>(vlim64) : kBV;
+        const int lrow0 = wv * (kVB * 32) + 4 * (lane >> 5);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            float x[64];
+        for (int b = 0; b < kTB; ++b) {
+            const int64_t trel64 = my_tgt[b] - v0;
+            const int trel = (trel64 >= 0 && trel64 < kBV) ? static_cast<int>(trel64) : -1;
 #pragma unroll
-            for (int a = 0; a < 4; ++a)
+            for (int a = 0; a < kVB; ++a) {
+                float x[16];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int64_t v = v0 + wv * 128 + a * 32 + 8 * (r / 4) + 4 * (lane >> 5) +
-                                      (r % 4);
+                    const int row = lrow0 + a * 32 + 8 * (r / 4) + (r % 4);
                     const float val = acc[a][b][r] * p.scale;
-                    x[a * 16 + r] = (v < p.vocab) ? val : -INFINITY;
-                    if (v == my_tgt[b]) xt[b] = val;
+                    x[r] = (row < vlim) ? val : -INFINITY;
+                    if (row == trel) xt[b] = val;
                 }
-            absorb<64, true>(st[b], x);
+                absorb<16, true>(st[b], x);
+            }
         }
     }
 
     // Merge lane l with lane l + 32 (same token, other vocab rows), then the
-    // two vocab-half waves of each token half through LDS.
+    // two vocab-half waves of each token half through LDS (the ring's memory:
+    // every wave is past its last read of it once all reach the barrier).
+    __syncthreads();
+    Stat (*merge_stat)[kBT] = reinterpret_cast<Stat (*)[kBT]>(lds);
+    float (*merge_xt)[kBT] = reinterpret_cast<float (*)[kBT]>(lds + 2 * kBT * sizeof(Stat));
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < kTB; ++b) {
         Stat o;
         o.m = __shfl_xor(st[b].m, 32, 64);
         o.z = __shfl_xor(st[b].z, 32, 64);
@@ -221,7 +268,7 @@ __global__ __launch_bounds__(kThreads) void klp_lmh_fwd_kernel(LmhParams p) {
         st[b] = (lane < 32) ? combine(st[b], o) : combine(o, st[b]);
         xt[b] += oxt;  // at most one of the two is non-zero
         if (lane < 32) {
-            const int col = wt * 64 + b * 32 + lane;
+            const int col = wt * (kTB * 32) + b * 32 + lane;
             merge_stat[wv][col] = st[b];
             merge_xt[wv][col] = xt[b];
         }
