@@ -500,10 +500,11 @@ size_t klp_lmh_workspace_bytes(int64_t n_tokens, int64_t vocab, int64_t dim) {
     return lmh_workspace_bytes(n_tokens, vocab);
 }
 
-int klp_lmh_fwd(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight,
-                int64_t n_tokens, int64_t vocab, int64_t dim, const int64_t* targets,
-                float temperature, float* logprob, float* entropy, float* lse, void* workspace,
-                size_t workspace_bytes, void* stream) {
+// Checks shared by klp_lmh_fwd and klp_lmh_bwd_logits; fills the GEMM part
+// of `p`.  Returns KLP_OK, or an error (after fail()).
+int lmh_setup(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight,
+              int64_t n_tokens, int64_t vocab, int64_t dim, const int64_t* targets,
+              float temperature, klp::LmhParams* p) {
     if (n_tokens < 0) return fail(KLP_EINVAL, "n_tokens must be >= 0");
     if (vocab < 1) return fail(KLP_EINVAL, "vocab must be >= 1, got %lld",
                                static_cast<long long>(vocab));
@@ -516,13 +517,72 @@ int klp_lmh_fwd(const void* hidden, int64_t ld_hidden, const void* weight, int64
         return fail(KLP_EINVAL, "n_tokens and vocab must be below 2^31");
     float scale;
     if (!scale_from_temperature(temperature, &scale)) return KLP_EINVAL;
-    if (n_tokens == 0) return ok();
+    if (n_tokens == 0) return KLP_OK;
     if (hidden == nullptr || weight == nullptr || targets == nullptr)
         return fail(KLP_EINVAL, "hidden, weight and targets must be non-null");
     if (!aligned(hidden, 16) || !aligned(weight, 16))
         return fail(KLP_EINVAL, "hidden and weight must be 16-byte aligned");
     if (!aligned(targets, 8)) return fail(KLP_EINVAL, "targets pointer is not 8-byte aligned");
-    int rc;
+    *p = klp::LmhParams{};
+    p->hidden = static_cast<const uint16_t*>(hidden);
+    p->ld_hidden = ld_hidden;
+    p->weight = static_cast<const uint16_t*>(weight);
+    p->ld_weight = ld_weight;
+    p->n_tokens = n_tokens;
+    p->vocab = vocab;
+    p->dim = dim;
+    p->targets = targets;
+    p->scale = scale;
+    p->n_tblocks = klp::lmh_token_blocks(n_tokens);
+    p->n_vtiles = klp::lmh_vocab_tiles(vocab);
+    lmh_plan(n_tokens, vocab, &p->tiles_per_chunk, &p->n_chunks);
+    const int64_t blocks = (p->n_chunks + 7) / 8 * 8 * p->n_tblocks;
+    if (blocks > (int64_t{1} << 31) - 1)
+        return fail(KLP_EINVAL, "grid of %lld workgroups is too large",
+                    static_cast<long long>(blocks));
+    return KLP_OK;
+}
+
+int klp_lmh_bwd_logits(const void* hidden, int64_t ld_hidden, const void* weight,
+                       int64_t ld_weight, int64_t n_tokens, int64_t vocab, int64_t dim,
+                       const int64_t* targets, float temperature, const float* lse,
+                       const float* entropy, const float* g_logp, const float* g_ent,
+                       const float* g_lse, void* d_logits, int64_t ld_d, void* stream) {
+    klp::LmhParams p;
+    int rc = lmh_setup(hidden, ld_hidden, weight, ld_weight, n_tokens, vocab, dim, targets,
+                       temperature, &p);
+    if (rc != KLP_OK) return rc;
+    if (n_tokens == 0) return ok();
+    if ((rc = check_f32(lse, "lse")) != KLP_OK) return rc;
+    if ((rc = check_f32(entropy, "entropy")) != KLP_OK) return rc;
+    if (g_logp && (rc = check_f32(g_logp, "g_logp")) != KLP_OK) return rc;
+    if (g_ent && (rc = check_f32(g_ent, "g_ent")) != KLP_OK) return rc;
+    if (g_lse && (rc = check_f32(g_lse, "g_lse")) != KLP_OK) return rc;
+    if (d_logits == nullptr || !aligned(d_logits, 8) || ld_d < vocab || ld_d % 4 != 0)
+        return fail(KLP_EINVAL,
+                    "d_logits must be non-null and 8-byte aligned, with a row stride >= vocab "
+                    "and a multiple of 4 elements");
+    p.saved_lse = lse;
+    p.saved_entropy = entropy;
+    p.g_logp = g_logp;
+    p.g_ent = g_ent;
+    p.g_lse = g_lse;
+    p.d_logits = static_cast<uint16_t*>(d_logits);
+    p.ld_d = ld_d;
+    if (injected_failure("lm-head backward")) return KLP_ELAUNCH;
+    return after_launch(klp::launch_lmh_dlogits(p, static_cast<hipStream_t>(stream)),
+                        "lm-head backward");
+}
+
+int klp_lmh_fwd(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight,
+                int64_t n_tokens, int64_t vocab, int64_t dim, const int64_t* targets,
+                float temperature, float* logprob, float* entropy, float* lse, void* workspace,
+                size_t workspace_bytes, void* stream) {
+    klp::LmhParams p;
+    int rc = lmh_setup(hidden, ld_hidden, weight, ld_weight, n_tokens, vocab, dim, targets,
+                       temperature, &p);
+    if (rc != KLP_OK) return rc;
+    if (n_tokens == 0) return ok();
     if ((rc = check_f32(logprob, "logprob")) != KLP_OK) return rc;
     if ((rc = check_f32(entropy, "entropy")) != KLP_OK) return rc;
     if ((rc = check_f32(lse, "lse")) != KLP_OK) return rc;
@@ -531,27 +591,10 @@ int klp_lmh_fwd(const void* hidden, int64_t ld_hidden, const void* weight, int64
         return fail(KLP_EWORKSPACE,
                     "workspace missing, too small or not 16-byte aligned: have %zu bytes, need %zu",
                     workspace_bytes, need);
-    klp::LmhParams p;
-    p.hidden = static_cast<const uint16_t*>(hidden);
-    p.ld_hidden = ld_hidden;
-    p.weight = static_cast<const uint16_t*>(weight);
-    p.ld_weight = ld_weight;
-    p.n_tokens = n_tokens;
-    p.vocab = vocab;
-    p.dim = dim;
-    p.targets = targets;
-    p.scale = scale;
     p.partials = static_cast<float*>(workspace);
-    p.n_tblocks = klp::lmh_token_blocks(n_tokens);
-    p.n_vtiles = klp::lmh_vocab_tiles(vocab);
-    lmh_plan(n_tokens, vocab, &p.tiles_per_chunk, &p.n_chunks);
     p.logprob = logprob;
     p.entropy = entropy;
     p.lse = lse;
-    const int64_t blocks = (p.n_chunks + 7) / 8 * 8 * p.n_tblocks;
-    if (blocks > (int64_t{1} << 31) - 1)
-        return fail(KLP_EINVAL, "grid of %lld workgroups is too large",
-                    static_cast<long long>(blocks));
     if (injected_failure("lm-head forward")) return KLP_ELAUNCH;
     return after_launch(klp::launch_lmh_fwd(p, static_cast<hipStream_t>(stream)),
                         "lm-head forward");

@@ -20,19 +20,6 @@
 
 namespace klp {
 
-struct RowGrad {
-    float lse, lse_hi, lse_lo, g_ent, g_logp, c0;
-};
-
-// Gradient with respect to the (temperature-scaled) logit x; the chain-rule
-// factor 1/T for the unscaled logit is applied by the caller.
-__device__ __forceinline__ float grad_one(float x, const RowGrad& g) {
-    const float lp = fmax_nan(x - g.lse, kNegBig);
-    const float arg = fmaf(x, kLog2e, -g.lse_hi) - g.lse_lo;
-    const float p = exp2_hw(arg);
-    return p * fmaf(-g.g_ent, lp, g.c0);
-}
-
 template <int DT, int WAVES, int U, bool kNtStore, bool kScaled>
 __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
     typedef typename Traits<DT>::elem elem;
@@ -49,15 +36,8 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
     elem* dp = static_cast<elem*>(p.d_logits) + row * vocab;
     const int64_t tgt = p.targets[row];
 
-    RowGrad g;
-    g.lse = p.lse[row];
-    const float ent = p.entropy[row];
-    g.g_logp = p.g_logp ? p.g_logp[row] : 0.0f;
-    g.g_ent = p.g_ent ? p.g_ent[row] : 0.0f;
-    const float g_lse = p.g_lse ? p.g_lse[row] : 0.0f;
-    g.c0 = g_lse - g.g_logp - g.g_ent * ent;
-    g.lse_hi = g.lse * kLog2e;
-    g.lse_lo = fmaf(g.lse, kLog2e, -g.lse_hi);
+    const RowGrad g = row_grad(p.lse[row], p.entropy[row], p.g_logp ? p.g_logp[row] : 0.0f,
+                               p.g_ent ? p.g_ent[row] : 0.0f, p.g_lse ? p.g_lse[row] : 0.0f);
 
     const uintptr_t in_addr = reinterpret_cast<uintptr_t>(rp);
     const uintptr_t out_addr = reinterpret_cast<uintptr_t>(dp);

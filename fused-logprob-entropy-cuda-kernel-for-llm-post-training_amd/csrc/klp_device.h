@@ -257,4 +257,34 @@ __device__ __forceinline__ RowOut finalize(const Stat s, float x_target) {
     return r;
 }
 
+// Per-row constants of the backward (reference csrc/fused_logprob.cu:233-238,
+// the hoisted constant at :271): c0 = g_lse - g_logp - g_ent * H, and lse
+// times log2(e) split into a rounded head and its exact fma remainder.
+struct RowGrad {
+    float lse, lse_hi, lse_lo, g_ent, g_logp, c0;
+};
+
+__device__ __forceinline__ RowGrad row_grad(float lse, float ent, float g_logp, float g_ent,
+                                            float g_lse) {
+    RowGrad g;
+    g.lse = lse;
+    g.g_logp = g_logp;
+    g.g_ent = g_ent;
+    g.c0 = g_lse - g_logp - g_ent * ent;
+    g.lse_hi = lse * kLog2e;
+    g.lse_lo = fmaf(lse, kLog2e, -g.lse_hi);
+    return g;
+}
+
+// Gradient with respect to the (temperature-scaled) logit x, without the
+// one-hot term; the chain-rule factor 1/T for the unscaled logit is applied
+// by the caller.  p = 2^(x*log2e - lse*log2e) with one rounding in the
+// exponent; lp is clamped so that a -inf logit gives exactly 0.
+__device__ __forceinline__ float grad_one(float x, const RowGrad& g) {
+    const float lp = fmax_nan(x - g.lse, kNegBig);
+    const float arg = fmaf(x, kLog2e, -g.lse_hi) - g.lse_lo;
+    const float p = exp2_hw(arg);
+    return p * fmaf(-g.g_ent, lp, g.c0);
+}
+
 }  // namespace klp

@@ -116,10 +116,19 @@ struct LmhParams {
     float* logprob;
     float* entropy;
     float* lse;
+    // d_logits (backward) only:
+    const float* g_logp;     // nullable
+    const float* g_ent;      // nullable
+    const float* g_lse;      // nullable
+    const float* saved_lse;  // [n_tokens], as the forward wrote it
+    const float* saved_entropy;
+    uint16_t* d_logits;      // bf16 [n_tokens, ld_d], ld_d a multiple of 4
+    int64_t ld_d;
 };
 int64_t lmh_token_blocks(int64_t n_tokens);
 int64_t lmh_vocab_tiles(int64_t vocab);
 hipError_t launch_lmh_fwd(const LmhParams& p, hipStream_t stream);
+hipError_t launch_lmh_dlogits(const LmhParams& p, hipStream_t stream);
 
 hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream);
 hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream);

@@ -105,7 +105,11 @@ __device__ __forceinline__ void wait_stages(int ahead) {
 
 }  // namespace
 
-__global__ __launch_bounds__(kThreads) void klp_lmh_fwd_kernel(LmhParams p) {
+// kGrad == false: the forward (partial states per vocab chunk).
+// kGrad == true: the backward's d_logits: the same logits tiles, turned into
+// the gradient of klp_bwd (grad_one, klp_device.h) and written as bf16.
+template <bool kGrad>
+__global__ __launch_bounds__(kThreads) void klp_lmh_kernel(LmhParams p) {
     // The ring takes all 160 KB of LDS; the end-of-chunk merge reuses it.
     __shared__ __attribute__((aligned(1024))) unsigned char lds[kRing * kStageBytes];
 
@@ -150,12 +154,20 @@ __global__ __launch_bounds__(kThreads) void klp_lmh_fwd_kernel(LmhParams p) {
     Stat st[kTB];
     float xt[kTB];
     int64_t my_tgt[kTB];
+    RowGrad rg[kTB];
 #pragma unroll
     for (int j = 0; j < kTB; ++j) {
         st[j] = stat_empty();
         xt[j] = 0.0f;
         const int64_t tok = tok0 + wt * (kTB * 32) + j * 32 + (lane & 31);
-        my_tgt[j] = (tok < p.n_tokens) ? p.targets[tok] : -1;
+        const bool ok = tok < p.n_tokens;
+        my_tgt[j] = ok ? p.targets[tok] : -1;
+        if constexpr (kGrad) {
+            rg[j] = ok ? row_grad(p.saved_lse[tok], p.saved_entropy[tok],
+                                  p.g_logp ? p.g_logp[tok] : 0.0f,
+                                  p.g_ent ? p.g_ent[tok] : 0.0f, p.g_lse ? p.g_lse[tok] : 0.0f)
+                       : row_grad(0.0f, 0.0f, 0.0f, 0.0f, 0.0f);
+        }
     }
 
     // Issue the copies of global stage g (tile tile_first + g / n_ksteps,
@@ -226,10 +238,46 @@ __global__ __launch_bounds__(kThreads) void klp_lmh_fwd_kernel(LmhParams p) {
             }
         }
 
+        const int64_t v0 = vt * kBV;
+        if constexpr (kGrad) {
+            // d_logits of the tile: accumulator r of block (a, b) holds tile
+            // row wv*128 + a*32 + 8*(r/4) + 4*(lane/32) + r%4 of token column
+            // b*32 + lane%32; rows 4q .. 4q + 3 go out as one 8-byte store.
+            const int lrow0 = wv * (kVB * 32) + 4 * (lane >> 5);
+#pragma unroll
+            for (int b = 0; b < kTB; ++b) {
+                const int64_t tok = tok0 + wt * (kTB * 32) + b * 32 + (lane & 31);
+                if (tok >= p.n_tokens) continue;
+                uint16_t* drow = p.d_logits + tok * p.ld_d;
+#pragma unroll
+                for (int a = 0; a < kVB; ++a) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int64_t vq = v0 + lrow0 + a * 32 + 8 * q;
+                        if (vq >= p.vocab) continue;
+                        float d[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            float g = grad_one(acc[a][b][4 * q + i] * p.scale, rg[b]);
+                            if (vq + i == my_tgt[b]) g += rg[b].g_logp;
+                            if (vq + i >= p.vocab) g = 0.0f;
+                            d[i] = g * p.scale;
+                        }
+                        const bf16x2 lo = __builtin_convertvector(f32x2{d[0], d[1]}, bf16x2);
+                        const bf16x2 hi = __builtin_convertvector(f32x2{d[2], d[3]}, bf16x2);
+                        uint2 w;
+                        w.x = __builtin_bit_cast(uint32_t, lo);
+                        w.y = __builtin_bit_cast(uint32_t, hi);
+                        *reinterpret_cast<uint2*>(drow + vq) = w;
+                    }
+                }
+            }
+            continue;
+        }
+
         // Tile done: fold it into the lane's token states, one 32-row block
         // at a time.  Accumulator r of block (a, b) holds tile row
         // wv*128 + a*32 + 8*(r/4) + 4*(lane/32) + r%4 (vocab row v0 + that).
-        const int64_t v0 = vt * kBV;
         const int64_t vlim64 = p.vocab - v0;
         const int vlim = vlim64 < kBV ? static_cast<int>(vlim64) : kBV;
         const int lrow0 = wv * (kVB * 32) + 4 * (lane >> 5);
@@ -251,6 +299,8 @@ __global__ __launch_bounds__(kThreads) void klp_lmh_fwd_kernel(LmhParams p) {
             }
         }
     }
+
+    if constexpr (kGrad) return;
 
     // Merge lane l with lane l + 32 (same token, other vocab rows), then the
     // two vocab-half waves of each token half through LDS (the ring's memory:
@@ -310,12 +360,19 @@ __global__ __launch_bounds__(256) void klp_lmh_combine_kernel(LmhParams p) {
 int64_t lmh_token_blocks(int64_t n_tokens) { return (n_tokens + kBT - 1) / kBT; }
 int64_t lmh_vocab_tiles(int64_t vocab) { return (vocab + kBV - 1) / kBV; }
 
+hipError_t launch_lmh_dlogits(const LmhParams& p, hipStream_t stream) {
+    const int64_t chunks8 = (p.n_chunks + 7) / 8 * 8;
+    return launch_kernel(klp_lmh_kernel<true>,
+                         dim3(static_cast<unsigned>(chunks8 * p.n_tblocks)), dim3(kThreads),
+                         stream, p);
+}
+
 hipError_t launch_lmh_fwd(const LmhParams& p, hipStream_t stream) {
     // Round the chunk count up to a multiple of 8 (one per XCD per round);
     // padding workgroups exit at once.
     const int64_t chunks8 = (p.n_chunks + 7) / 8 * 8;
     const int64_t blocks = chunks8 * p.n_tblocks;
-    hipError_t e = launch_kernel(klp_lmh_fwd_kernel, dim3(static_cast<unsigned>(blocks)),
+    hipError_t e = launch_kernel(klp_lmh_kernel<false>, dim3(static_cast<unsigned>(blocks)),
                                  dim3(kThreads), stream, p);
     if (e != hipSuccess) return e;
     return launch_kernel(klp_lmh_combine_kernel,

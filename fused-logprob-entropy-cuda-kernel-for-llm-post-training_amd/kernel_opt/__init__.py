@@ -11,7 +11,10 @@ from .ops import (  # noqa: F401
     fused_logprob_entropy_naive,
 )
 from .grpo import fused_grpo_loss  # noqa: F401
-from .lmhead import fused_linear_logprob_entropy_forward  # noqa: F401
+from .lmhead import (  # noqa: F401
+    fused_linear_logprob_entropy,
+    fused_linear_logprob_entropy_forward,
+)
 
 
 # Lazy import so users without trl can still use the kernels.

@@ -47,6 +47,8 @@ SIGNATURES = {
     "klp_lmh_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "klp_lmh_fwd": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, ctypes.c_float,
                            _vp, _vp, _vp, _vp, _sz, _vp]),
+    "klp_lmh_bwd_logits": (_i32, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, ctypes.c_float,
+                                  _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
     "klp_grpo_workspace_bytes": (_sz, [_i64]),
     "klp_grpo_fwd": (_i32, [_vp] * 5 + [_i64, _i64] + [ctypes.c_float] * 4 + [_i32] * 3
                      + [_vp, _vp, _vp, _sz, _vp]),

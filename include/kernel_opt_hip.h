@@ -241,6 +241,25 @@ int klp_lmh_fwd(const void* hidden, int64_t ld_hidden, const void* weight, int64
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The backward's d_logits for the fused LM head: recomputes each block of
+ * logits exactly as klp_lmh_fwd did (same MFMA order, hence the same fp32
+ * values behind the saved lse / entropy) and writes
+ *   d_logits[n, v] = klp_bwd's gradient of that logit (times 1/T),
+ * rounded to bf16, into `d_logits` (bf16 [n_tokens, ld_d], 8-byte aligned,
+ * ld_d >= vocab and a multiple of 4).  Columns vocab .. round_up(vocab, 4) - 1
+ * are written with 0 (stores go out four columns at a time); columns past
+ * them are not touched.
+ * d_hidden = d_logits @ weight and d_weight = d_logits^T @ hidden are then
+ * plain GEMMs for the caller.  lse / entropy are klp_lmh_fwd's outputs for
+ * the same inputs and temperature; g_logp / g_ent / g_lse may be NULL.
+ */
+int klp_lmh_bwd_logits(const void* hidden, int64_t ld_hidden, const void* weight,
+                       int64_t ld_weight, int64_t n_tokens, int64_t vocab, int64_t dim,
+                       const int64_t* targets, float temperature, const float* lse,
+                       const float* entropy, const float* g_logp, const float* g_ent,
+                       const float* g_lse, void* d_logits, int64_t ld_d, void* stream);
+
+/*
  * Test hook with no counterpart in the reference: the next `count` compute
  * calls on the calling thread return KLP_ELAUNCH without launching anything,
  * as if hipGetLastError() had reported a failure.  Lets the error path be

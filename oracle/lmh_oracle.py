@@ -14,6 +14,9 @@ Pinned in tests/test_lmh_cpu.py against the float64 C oracle of the
 logprob forward (oracle/klp_oracle.c) on integer inputs whose logits are
 exact in fp32, against a pure-Python loop on tiny shapes, and against the
 uniform closed form (identical weight rows: entropy = lse - x = log V).
+`backward` (the reference's closed form, csrc/fused_logprob.cu:233-238,
+chained through the linear layer) is pinned against float64 torch autograd
+of the eager formulas.
 """
 from __future__ import annotations
 
@@ -57,3 +60,31 @@ def magnitude(hidden_bits, weight_bits):
     """Per-token max over v of sum_k |h_k w_k|: the scale of the fp32
     accumulation error of each logit."""
     return (np.abs(bf16_to_f64(hidden_bits)) @ np.abs(bf16_to_f64(weight_bits)).T).max(axis=1)
+
+
+def backward(hidden_bits, weight_bits, targets, g_logp=None, g_ent=None, g_lse=None,
+             temperature=None):
+    """(d_hidden, d_weight, d_logits) float64 for upstream gradients of
+    (logprob, entropy, lse); None means zero.  d_logits is with respect to
+    the unscaled logits hidden @ weight^T."""
+    h = bf16_to_f64(hidden_bits)
+    w = bf16_to_f64(weight_bits)
+    s = scale_of(temperature)
+    x = (h @ w.T) * s
+    N, V = x.shape
+    m = x.max(axis=1, keepdims=True)
+    lse = m[:, 0] + np.log(np.exp(x - m).sum(axis=1))
+    lp = x - lse[:, None]
+    p = np.exp(lp)
+    ent = -(p * lp).sum(axis=1)
+    z = np.zeros(N)
+    gl = z if g_logp is None else np.asarray(g_logp, np.float64).reshape(-1)
+    ge = z if g_ent is None else np.asarray(g_ent, np.float64).reshape(-1)
+    gs = z if g_lse is None else np.asarray(g_lse, np.float64).reshape(-1)
+    c0 = gs - gl - ge * ent
+    d = p * (c0[:, None] - ge[:, None] * lp)
+    t = np.asarray(targets, np.int64).reshape(-1)
+    ok = (t >= 0) & (t < V)
+    d[np.arange(N)[ok], t[ok]] += gl[ok]
+    d *= s
+    return d @ w, d.T @ h, d

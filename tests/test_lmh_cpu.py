@@ -67,3 +67,30 @@ def test_out_of_range_targets_give_minus_lse():
     w = bf16_bits(g.normal(0, 0.2, (50, 64)))
     lp, _, lse = lmh_oracle.forward(h, w, np.array([-100, 50, 1000]))
     np.testing.assert_array_equal(lp, -lse)
+
+
+def test_backward_matches_float64_autograd():
+    g = np.random.default_rng(5)
+    N, V, D = 6, 40, 64
+    h = bf16_bits(g.normal(0, 1, (N, D)))
+    w = bf16_bits(g.normal(0, 0.3, (V, D)))
+    t = np.array([0, 39, 5, -100, 17, 40])
+    gl, ge, gs = (g.normal(0, 1, N) for _ in range(3))
+    T = 0.8
+    dh, dw, _ = lmh_oracle.backward(h, w, t, gl, ge, gs, temperature=T)
+    H = torch.tensor(lmh_oracle.bf16_to_f64(h), requires_grad=True)
+    W = torch.tensor(lmh_oracle.bf16_to_f64(w), requires_grad=True)
+    x = (H @ W.T) * lmh_oracle.scale_of(T)
+    lsm = torch.log_softmax(x, dim=-1)
+    tt = torch.tensor(t)
+    valid = (tt >= 0) & (tt < V)
+    xt = torch.where(valid, x.gather(1, tt.clamp(0, V - 1)[:, None])[:, 0], torch.zeros(N,
+                                                                                 dtype=x.dtype))
+    lse = torch.logsumexp(x, dim=-1)
+    logp = xt - lse
+    ent = -(lsm.exp() * lsm).sum(-1)
+    loss = (logp * torch.tensor(gl)).sum() + (ent * torch.tensor(ge)).sum() \
+        + (lse * torch.tensor(gs)).sum()
+    loss.backward()
+    np.testing.assert_allclose(dh, H.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dw, W.grad.numpy(), rtol=1e-10, atol=1e-12)

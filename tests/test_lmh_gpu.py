@@ -118,3 +118,103 @@ def test_invalid_arguments_raise():
         fused_linear_logprob_entropy_forward(h, w, t)
     with pytest.raises(RuntimeError, match="bfloat16"):
         fused_linear_logprob_entropy_forward(h.float(), w, t)
+
+
+# ---------------------------------------------------------------------------
+# Backward (klp_lmh_bwd_logits + library GEMMs)
+# ---------------------------------------------------------------------------
+def _grads(N, V, seed):
+    g = torch.Generator().manual_seed(seed)
+    return tuple(torch.randn(N, generator=g) for _ in range(3))
+
+
+def _bwd_check(h, w, t, gl, ge, gs, temperature=None, need_w=True):
+    from kernel_opt import fused_linear_logprob_entropy
+    hd = h.to(DEV).requires_grad_(True)
+    wd = w.to(DEV).requires_grad_(need_w)
+    lp, ent, lse = fused_linear_logprob_entropy(hd, wd, t.to(DEV), temperature)
+    loss = 0
+    for out, gg in ((lp, gl), (ent, ge), (lse, gs)):
+        if gg is not None:
+            loss = loss + (out * gg.to(DEV)).sum()
+    loss.backward()
+    ref_dh, ref_dw, ref_dl = lmh_oracle.backward(
+        bits(h), bits(w), t.numpy(), *(None if gg is None else gg.numpy() for gg in (gl, ge, gs)),
+        temperature=temperature)
+    hf, wf = lmh_oracle.bf16_to_f64(bits(h)), lmh_oracle.bf16_to_f64(bits(w))
+    # bf16 rounding of d_logits and of the GEMM outputs (fp32 accumulation)
+    bound_h = 2.0 ** -7 * (np.abs(ref_dl) @ np.abs(wf)) + 2.0 ** -8 * np.abs(ref_dh) + 1e-7
+    err_h = np.abs(hd.grad.float().cpu().numpy() - ref_dh)
+    assert np.all(err_h <= bound_h), f"d_hidden err {err_h.max():.3g}"
+    if need_w:
+        bound_w = 2.0 ** -7 * (np.abs(ref_dl).T @ np.abs(hf)) + 2.0 ** -8 * np.abs(ref_dw) + 1e-7
+        err_w = np.abs(wd.grad.float().cpu().numpy() - ref_dw)
+        assert np.all(err_w <= bound_w), f"d_weight err {err_w.max():.3g}"
+    else:
+        assert wd.grad is None
+
+
+@pytest.mark.parametrize("N,V,D", [(130, 1000, 256), (64, 4099, 192), (300, 2001, 128)])
+def test_backward_matches_oracle(N, V, D):
+    h, w, t = make(N, V, D, seed=20 + N)
+    t[::9] = -100
+    _bwd_check(h, w, t, *_grads(N, V, 21))
+
+
+def test_backward_temperature_and_partial_grads():
+    h, w, t = make(100, 3000, 256, seed=22)
+    gl, ge, _ = _grads(100, 3000, 23)
+    _bwd_check(h, w, t, gl, None, None, temperature=0.7)
+    _bwd_check(h, w, t, None, ge, None, need_w=False)
+
+
+def test_backward_d_logits_against_oracle():
+    """The recomputed d_logits, rounded once to bf16, against the float64
+    closed form: within one bf16 rounding of each value plus the fp32
+    evaluation noise of its row."""
+    import ctypes
+    from kernel_opt import fused_linear_logprob_entropy_forward
+    from kernel_opt._library import lib
+    N, V, D = 96, 3001, 192
+    h, w, t = make(N, V, D, seed=24)
+    gl, ge, gs = _grads(N, V, 25)
+    hd, wd, td = h.to(DEV), w.to(DEV), t.to(DEV)
+    lp, ent, lse = fused_linear_logprob_entropy_forward(hd, wd, td)
+    ld = (V + 3) // 4 * 4 + 8
+    d = torch.full((N, ld), 7.0, dtype=torch.bfloat16, device=DEV)
+    G = [x.to(DEV) for x in (gl, ge, gs)]
+    P = lambda x: ctypes.c_void_p(x.data_ptr())
+    rc = lib.klp_lmh_bwd_logits(P(hd), D, P(wd), D, N, V, D, P(td), 1.0, P(lse), P(ent),
+                                P(G[0]), P(G[1]), P(G[2]), P(d), ld,
+                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    got = d[:, :V].float().cpu().numpy()
+    v4 = (V + 3) // 4 * 4
+    assert torch.all(d[:, V:v4].cpu() == 0.0)  # the last group of four, zero-filled
+    assert torch.all(d[:, v4:].cpu() == 7.0)   # columns past it untouched
+    _, _, ref = lmh_oracle.backward(bits(h), bits(w), t.numpy(), gl.numpy(), ge.numpy(),
+                                    gs.numpy())
+    row_noise = 2.0 ** -20 * np.abs(ref).max(axis=1, keepdims=True)
+    assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + row_noise)
+
+
+def test_backward_matches_unfused_path():
+    """Same gradients as logits = hidden @ weight^T followed by the
+    autograd logprob kernel, up to the bf16 rounding of the logits."""
+    from kernel_opt import fused_linear_logprob_entropy, fused_logprob_entropy
+    h, w, t = make(200, 5000, 256, seed=26)
+    gl, ge, _ = _grads(200, 5000, 27)
+    res = []
+    for fused in (True, False):
+        hd = h.to(DEV).requires_grad_(True)
+        wd = w.to(DEV).requires_grad_(True)
+        td = t.to(DEV)
+        if fused:
+            lp, ent, _ = fused_linear_logprob_entropy(hd, wd, td)
+        else:
+            lp, ent, _ = fused_logprob_entropy(hd @ wd.T, td)
+        ((lp * gl.to(DEV)).sum() + (ent * ge.to(DEV)).sum()).backward()
+        res.append((hd.grad.float(), wd.grad.float()))
+    for a, b in zip(res[0], res[1]):
+        scale = b.abs().max()
+        assert (a - b).abs().max() <= 0.05 * scale
