@@ -51,6 +51,7 @@ for _p in (PKG_DIR, ROOT):
 import torch  # noqa: E402
 
 HBM_PEAK_TBPS = 8.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
 # each scaled by the counter's reading for a plain copy of known size
@@ -259,6 +260,64 @@ def grpo_timing(dev, K, B=16, S=2048):
             "note": "loss + loss.backward() per iteration, end to end from Python"}
 
 
+def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
+    """The fused LM head (hidden @ weight^T folded into the logprob/entropy
+    reduction, klp_lmh_*) against the unfused path (a bf16 library matmul,
+    then the logprob kernels) on Qwen2.5-7B's head shape with C2's 1024
+    tokens; random weights.  Forward, and forward + backward with upstream
+    gradients on logprob and entropy."""
+    from kernel_opt import (fused_linear_logprob_entropy, fused_linear_logprob_entropy_forward,
+                            fused_logprob_entropy, fused_logprob_entropy_forward)
+    g = torch.Generator(device=dev).manual_seed(3584)
+    h = torch.randn(N, D, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
+    w = (torch.randn(V, D, device=dev, generator=g) / D ** 0.5 * 3).to(torch.bfloat16)
+    w.requires_grad_(True)
+    t = torch.randint(0, V, (N,), device=dev, generator=g)
+    gl = torch.randn(N, device=dev, generator=g)
+    ge = torch.randn(N, device=dev, generator=g)
+
+    def fb(fused):
+        h.grad = None
+        w.grad = None
+        if fused:
+            lp, ent, _ = fused_linear_logprob_entropy(h, w, t)
+        else:
+            lp, ent, _ = fused_logprob_entropy(h @ w.T, t)
+        ((lp * gl).sum() + (ent * ge).sum()).backward()
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(K):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / K
+
+    with torch.no_grad():
+        f_fwd = timed(lambda: fused_linear_logprob_entropy_forward(h, w, t))
+        u_fwd = timed(lambda: fused_logprob_entropy_forward(h @ w.T, t))
+    f_fb = timed(lambda: fb(True))
+    u_fb = timed(lambda: fb(False))
+    flops = 2 * N * V * D
+    out = {"shape": {"tokens": N, "vocab": V, "hidden": D}, "dtype": "bf16 in, fp32 accumulate",
+           "fused_fwd_ms": round(f_fwd, 4), "unfused_fwd_ms": round(u_fwd, 4),
+           "fused_fwd_tflops": round(flops / (f_fwd * 1e-3) / 1e12, 1),
+           "fused_fwd_bwd_ms": round(f_fb, 4), "unfused_fwd_bwd_ms": round(u_fb, 4),
+           "roofline_fwd": {"bound": "mfma", "achieved": round(flops / (f_fwd * 1e-3) / 1e12, 1),
+                            "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(flops / (f_fwd * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                                          4)},
+           "note": "unfused = bf16 library matmul to [N, V] logits, then klp_fwd / klp_bwd"}
+    del h, w
+    torch.cuda.empty_cache()
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -275,6 +334,8 @@ def main(argv=None):
                     help="rows of the workload the CPU baseline times (whole batch elements)")
     ap.add_argument("--fwd-config", default=None, help="waves,unroll,splits,flags")
     ap.add_argument("--bwd-config", default=None, help="waves,unroll,splits,flags")
+    ap.add_argument("--no-lmhead", action="store_true",
+                    help="skip the fused LM-head timing (klp_lmh_* against matmul + logprob)")
     ap.add_argument("--no-grpo", action="store_true",
                     help="skip the GRPO-loss timing (fused klp_grpo_* against the eager chain)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -398,6 +459,7 @@ def main(argv=None):
         }
 
     grpo = None if args.no_grpo else grpo_timing(dev, K)
+    lmhead = None if args.no_lmhead else lmhead_timing(dev)
 
     B, S, _ = cfg["shape"]
     fwd_used = fcfg or _C.default_config("fwd", logits.dtype, N, V)
@@ -446,6 +508,7 @@ def main(argv=None):
         },
         "cpu_baseline": cpu,
         "grpo_loss": grpo,
+        "lm_head": lmhead,
     }
     print(json.dumps(out))
     return 0

@@ -29,8 +29,8 @@
 //    captured if it lies in the tile.
 // At the end of the chunk, lanes l and l+32 (same token) and the two waves
 // of a token half merge; the chunk's partial state per token goes to the
-// workspace.  klp_lmh_combine_kernel merges the chunks of each token in
-// chunk order (a fixed order) and applies the output formulas.
+// workspace.  klp_lmh_combine_kernel merges the chunks of each token (one
+// wave per token, a fixed order) and applies the output formulas.
 //
 // Workgroup order: workgroup b runs on XCD b % 8 (round-robin dispatch).
 // Consecutive workgroups of one XCD take the token blocks of one vocab
@@ -334,17 +334,22 @@ __global__ __launch_bounds__(kThreads) void klp_lmh_kernel(LmhParams p) {
     }
 }
 
-// One thread per token: merge the chunks in chunk order, take the target
-// logit from the chunk that holds the target.
+// One wave per token: lane l merges chunks l, l + 64, l + 128, ... in order,
+// the lanes then merge in the fixed xor-butterfly order of wave_reduce (so the
+// result does not depend on timing), and lane 0 takes the target logit from
+// the chunk that holds the target.
 __global__ __launch_bounds__(256) void klp_lmh_combine_kernel(LmhParams p) {
-    const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (n >= p.n_tokens) return;
     const float4* part = reinterpret_cast<const float4*>(p.partials);
     Stat acc = stat_empty();
-    for (int64_t c = 0; c < p.n_chunks; ++c) {
+    for (int64_t c = lane; c < p.n_chunks; c += 64) {
         const float4 q = part[c * p.n_tokens + n];
         acc = combine(acc, Stat{q.x, q.y, q.z});
     }
+    acc = wave_reduce(acc);
+    if (lane != 0) return;
     const int64_t tgt = p.targets[n];
     float x_target = 0.0f;
     if (tgt >= 0 && tgt < p.vocab) {
@@ -376,8 +381,7 @@ hipError_t launch_lmh_fwd(const LmhParams& p, hipStream_t stream) {
                                  dim3(kThreads), stream, p);
     if (e != hipSuccess) return e;
     return launch_kernel(klp_lmh_combine_kernel,
-                         dim3(static_cast<unsigned>((p.n_tokens + 255) / 256)), dim3(256),
-                         stream, p);
+                         dim3(static_cast<unsigned>((p.n_tokens + 3) / 4)), dim3(256), stream, p);
 }
 
 }  // namespace klp
