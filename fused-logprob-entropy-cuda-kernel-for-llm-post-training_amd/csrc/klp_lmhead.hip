@@ -217,25 +217,34 @@ __global__ __launch_bounds__(kThreads) void klp_lmh_kernel(LmhParams p) {
 
             const unsigned char* wl = lds + (g % kRing) * kStageBytes;
             const unsigned char* hl = wl + kWBytes;
+            // All operand fragments of the stage are read first, then the
+            // MFMAs run; the scheduling groups below keep that order (left
+            // alone, the scheduler reuses one register quad for the A
+            // fragments and waits for each read in turn).
+            constexpr int kKS = kBK / 16;
+            bf16x8 af[kKS][kVB], bfr[kKS][kTB];
 #pragma unroll
-            for (int ks = 0; ks < kBK / 16; ++ks) {
+            for (int ks = 0; ks < kKS; ++ks) {
                 const int c = ks * 2 + (lane >> 5);
-                bf16x8 af[kVB], bfr[kTB];
 #pragma unroll
                 for (int a = 0; a < kVB; ++a)
-                    af[a] = *reinterpret_cast<const bf16x8*>(
+                    af[ks][a] = *reinterpret_cast<const bf16x8*>(
                         wl + swz(wv * (kVB * 32) + a * 32 + (lane & 31), c));
 #pragma unroll
                 for (int b = 0; b < kTB; ++b)
-                    bfr[b] = *reinterpret_cast<const bf16x8*>(
+                    bfr[ks][b] = *reinterpret_cast<const bf16x8*>(
                         hl + swz(wt * (kTB * 32) + b * 32 + (lane & 31), c));
+            }
+#pragma unroll
+            for (int ks = 0; ks < kKS; ++ks)
 #pragma unroll
                 for (int a = 0; a < kVB; ++a)
 #pragma unroll
                     for (int b = 0; b < kTB; ++b)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b],
-                                                                           acc[a][b], 0, 0, 0);
-            }
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            af[ks][a], bfr[ks][b], acc[a][b], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, kKS * (kVB + kTB), 0);  // DS reads
+            __builtin_amdgcn_sched_group_barrier(0x008, kKS * kVB * kTB, 0);    // MFMAs
         }
 
         const int64_t v0 = vt * kBV;
