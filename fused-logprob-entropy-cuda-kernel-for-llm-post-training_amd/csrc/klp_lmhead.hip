@@ -1,7 +1,7 @@
-// klp_lmhead.hip — fused LM head + per-token logprob / entropy (forward),
-// for gfx950.  The reference names this as its natural follow-up (a
-// Liger-style fused linear + loss, docs/FINAL_REPORT.md:439-450) and does not
-// build it.
+// klp_lmhead.hip — fused LM head + per-token logprob / entropy (forward, and
+// the backward's d_logits), for gfx950.  The reference names this as its
+// natural follow-up (a Liger-style fused linear + loss,
+// docs/FINAL_REPORT.md:439-450) and does not build it.
 //
 //   logits[n, v] = scale * sum_k hidden[n, k] * weight[v, k]      (fp32)
 //   logprob[n] = logits[n, t_n] - lse[n],  entropy[n], lse[n]  as klp_fwd
@@ -9,7 +9,7 @@
 // without writing the [N, V] logits anywhere.  hidden is bf16 [N, D] and
 // weight bf16 [V, D] (nn.Linear's layout), both K-contiguous.
 //
-// klp_lmh_fwd_kernel: one workgroup (4 waves, 2 x 2) per (token block of
+// klp_lmh_kernel<false> (forward): one workgroup (4 waves, 2 x 2) per (token block of
 // 256, vocab chunk of `tiles_per_chunk` tiles of 256 rows).  Per vocab tile
 // it computes the 256 x 256 block of logits^T with v_mfma_f32_32x32x16_bf16,
 // each wave a 128 x 128 part of it (16 accumulator blocks, 256 AGPRs):
@@ -22,8 +22,9 @@
 //    (global_load_lds_dwordx4, no register staging) issued 4 stages ahead of
 //    the multiply; the ring runs across tile boundaries;
 //  - LDS rows are 64 bytes; the 16-byte chunk index is XOR-swizzled with
-//    the row index so that the MFMA operand reads of 8 consecutive rows
-//    cover all 32 banks once;
+//    row bits 0..3 (swz_f) so that the MFMA operand reads are free of bank
+//    conflicts;
+//  - a stage's operand fragments are all read before its MFMAs run;
 //  - after each tile the block's logits are folded into per-lane
 //    (m, z, t) states (absorb() of klp_device.h) and the target logit is
 //    captured if it lies in the tile.
@@ -31,6 +32,9 @@
 // of a token half merge; the chunk's partial state per token goes to the
 // workspace.  klp_lmh_combine_kernel merges the chunks of each token (one
 // wave per token, a fixed order) and applies the output formulas.
+//
+// klp_lmh_kernel<true> (backward) runs the same tiles and replaces the fold
+// with the gradient of klp_bwd, written to d_logits as bf16.
 //
 // Workgroup order: workgroup b runs on XCD b % 8 (round-robin dispatch).
 // Consecutive workgroups of one XCD take the token blocks of one vocab
@@ -49,17 +53,11 @@ constexpr int kVB = 4;              // 32-row vocab blocks per wave
 constexpr int kTB = 4;              // 32-token blocks per wave
 constexpr int kBV = 2 * kVB * 32;   // vocab rows per tile (2 waves along vocab): 256
 constexpr int kBT = 2 * kTB * 32;   // tokens per block (2 waves along tokens): 256
-#ifndef KLP_LMH_BK
-#define KLP_LMH_BK 32
-#endif
-#ifndef KLP_LMH_RING
-#define KLP_LMH_RING 5
-#endif
-#ifndef KLP_LMH_AUX
-#define KLP_LMH_AUX 0
-#endif
-constexpr int kBK = KLP_LMH_BK;     // K per LDS stage
-constexpr int kRing = KLP_LMH_RING; // LDS stages (prefetch distance kRing - 1)
+// K per LDS stage and LDS stages in the ring.  Measured: 64-wide stages (whole
+// 128-byte lines per row, a ring of 2) and non-temporal / sc0 copies were no
+// faster.
+constexpr int kBK = 32;
+constexpr int kRing = 5;
 constexpr int kThreads = 256;
 constexpr int kRowBytes = kBK * 2;
 constexpr int kChunksPerRow = kRowBytes / 16;
@@ -182,13 +180,12 @@ __global__ __launch_bounds__(kThreads) void klp_lmh_kernel(LmhParams p) {
             int64_t v = vt * kBV + q * kRowsPerCopy + lrow;
             if (v > p.vocab - 1) v = p.vocab - 1;
             __builtin_amdgcn_global_load_lds(p.weight + v * p.ld_weight + gchunk * 8 + koff,
-                                             dst + q * 1024, 16, 0, KLP_LMH_AUX);
+                                             dst + q * 1024, 16, 0, 0);
         }
 #pragma unroll
         for (int j = 0; j < kHCopies; ++j) {
             const int q = wave + 4 * j;
-            __builtin_amdgcn_global_load_lds(hsrc[j] + koff, dst + kWBytes + q * 1024, 16, 0,
-                                             KLP_LMH_AUX);
+            __builtin_amdgcn_global_load_lds(hsrc[j] + koff, dst + kWBytes + q * 1024, 16, 0, 0);
         }
     };
 
