@@ -219,15 +219,37 @@ __device__ __forceinline__ bool needs_clamped_rescan(const Stat& s) {
     return __builtin_isnan(s.t) && !__builtin_isnan(s.z);
 }
 
+// The state of the partner lane under DPP control `Ctrl` (a lane move
+// within a row of 16 lanes, a few cycles; no LDS round trip).
+template <int Ctrl>
+__device__ __forceinline__ Stat stat_dpp(const Stat& s) {
+    Stat o;
+    o.m = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s.m), Ctrl, 0xF, 0xF,
+                                                     false));
+    o.z = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s.z), Ctrl, 0xF, 0xF,
+                                                     false));
+    o.t = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s.t), Ctrl, 0xF, 0xF,
+                                                     false));
+    return o;
+}
+
+__device__ __forceinline__ Stat stat_shfl_xor(const Stat& s, int off) {
+    return Stat{__shfl_xor(s.m, off, 64), __shfl_xor(s.z, off, 64), __shfl_xor(s.t, off, 64)};
+}
+
+// Merge the states of all 64 lanes; every lane returns the total.  combine()
+// is commutative bit for bit, so both lanes of a pair compute the same merge
+// and the result depends on nothing but the fixed pairing order: within a
+// row, lanes are paired by DPP quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror and row_mirror (the partner always holds the other half of
+// the group merged so far); across rows by xor-16 and xor-32 shuffles.
 __device__ __forceinline__ Stat wave_reduce(Stat s) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        Stat o;
-        o.m = __shfl_xor(s.m, off, 64);
-        o.z = __shfl_xor(s.z, off, 64);
-        o.t = __shfl_xor(s.t, off, 64);
-        s = combine(s, o);
-    }
+    s = combine(s, stat_dpp<0xB1>(s));   // quad_perm [1, 0, 3, 2]
+    s = combine(s, stat_dpp<0x4E>(s));   // quad_perm [2, 3, 0, 1]
+    s = combine(s, stat_dpp<0x141>(s));  // row_half_mirror
+    s = combine(s, stat_dpp<0x140>(s));  // row_mirror
+    s = combine(s, stat_shfl_xor(s, 16));
+    s = combine(s, stat_shfl_xor(s, 32));
     return s;
 }
 
