@@ -495,6 +495,79 @@ int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp
                         "grpo backward");
 }
 
+int64_t klp_grpo_step_max_vocab(int dtype) {
+    if (dtype != KLP_BF16 && dtype != KLP_FP16 && dtype != KLP_FP32) return 0;
+    return int64_t{klp::kGrpoStepMaxVec} * klp::kGrpoStepThreads * (16 / elem_bytes(dtype));
+}
+
+int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                  int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                  const int64_t* targets, float temperature, const float* old_logp,
+                  const float* ref_logp, const float* advantages, const float* tok_weight,
+                  int64_t seq_len, float eps_low, float eps_high, float beta, int adv_per_token,
+                  float* logprob, float* entropy, float* lse, float* loss_tok, void* d_logits,
+                  void* stream) {
+    int rc = check_rows(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
+                        targets);
+    if (rc != KLP_OK) return rc;
+    float scale;
+    if (!scale_from_temperature(temperature, &scale)) return KLP_EINVAL;
+    if (n_rows == 0) return ok();
+    if (seq_len < 1 || n_rows % seq_len != 0)
+        return fail(KLP_EINVAL, "n_rows (%lld) must be a positive multiple of seq_len (%lld)",
+                    static_cast<long long>(n_rows), static_cast<long long>(seq_len));
+    if (vocab > klp_grpo_step_max_vocab(dtype))
+        return fail(KLP_EINVAL, "vocab %lld exceeds the fused GRPO step's row capacity %lld",
+                    static_cast<long long>(vocab),
+                    static_cast<long long>(klp_grpo_step_max_vocab(dtype)));
+    const int64_t esz = elem_bytes(dtype);
+    if ((vocab * esz) % 16 != 0 || !aligned(logits, 16) || (stride_inner * esz) % 16 != 0 ||
+        (n_rows > rows_inner && (stride_outer * esz) % 16 != 0))
+        return fail(KLP_EINVAL,
+                    "fused GRPO step needs 16-byte aligned rows whose length is a multiple of "
+                    "16 bytes");
+    if ((rc = check_f32(old_logp, "old_logp")) != KLP_OK) return rc;
+    if ((rc = check_f32(advantages, "advantages")) != KLP_OK) return rc;
+    if ((rc = check_f32(tok_weight, "tok_weight")) != KLP_OK) return rc;
+    if (ref_logp && (rc = check_f32(ref_logp, "ref_logp")) != KLP_OK) return rc;
+    if ((rc = check_f32(logprob, "logprob")) != KLP_OK) return rc;
+    if ((rc = check_f32(entropy, "entropy")) != KLP_OK) return rc;
+    if (lse && (rc = check_f32(lse, "lse")) != KLP_OK) return rc;
+    if ((rc = check_f32(loss_tok, "loss_tok")) != KLP_OK) return rc;
+    if (d_logits == nullptr || !aligned(d_logits, 16))
+        return fail(KLP_EINVAL, "d_logits must be non-null and 16-byte aligned");
+    if (!finite_nonneg(eps_low) || !finite_nonneg(eps_high))
+        return fail(KLP_EINVAL, "eps_low and eps_high must be finite and >= 0");
+    if (!(beta == beta) || beta == INFINITY || beta == -INFINITY)
+        return fail(KLP_EINVAL, "beta must be finite");
+    if ((rc = check_grid(n_rows, 1, klp::kGrpoStepThreads)) != KLP_OK) return rc;
+
+    klp::GrpoStepParams p;
+    p.logits = logits;
+    p.rm = klp::RowMap{rows_inner, stride_outer, stride_inner};
+    p.n_rows = n_rows;
+    p.vocab = vocab;
+    p.targets = targets;
+    p.scale = scale;
+    p.old_logp = old_logp;
+    p.ref_logp = ref_logp;
+    p.adv = advantages;
+    p.tok_weight = tok_weight;
+    p.seq_len = seq_len;
+    p.eps_low = eps_low;
+    p.eps_high = eps_high;
+    p.beta = beta;
+    p.adv_per_token = adv_per_token != 0;
+    p.logprob = logprob;
+    p.entropy = entropy;
+    p.lse = lse;
+    p.loss_tok = loss_tok;
+    p.d_logits = d_logits;
+    if (injected_failure("grpo step")) return KLP_ELAUNCH;
+    return after_launch(klp::launch_grpo_step(dtype, p, static_cast<hipStream_t>(stream)),
+                        "grpo step");
+}
+
 size_t klp_lmh_workspace_bytes(int64_t n_tokens, int64_t vocab, int64_t dim) {
     (void)dim;
     return lmh_workspace_bytes(n_tokens, vocab);

@@ -22,6 +22,7 @@
 // fixed order, the loss and statistics), klp_grpo_bwd_kernel (one workgroup
 // per row: the gradient, scaled by the upstream gradient of the loss).  All
 // reductions have a fixed order, so results do not depend on timing.
+#include "klp_grpo_terms.h"
 #include "klp_launch.h"
 
 namespace klp {
@@ -38,45 +39,9 @@ __device__ __forceinline__ float adv_at(const GrpoParams& p, int64_t b, int64_t 
     return p.adv_per_token ? p.adv[i] : p.adv[b];
 }
 
-struct TokenLoss {
-    float loss;   // per-token loss
-    float dw;     // d loss / d w (w = the log importance weight)
-    float dlp;    // d loss / d lp through the KL term only
-    float kl;     // KL estimate (0 when beta == 0 or no reference)
-    float low;    // 1 if clipped at 1 - eps_low with A < 0
-    float high;   // 1 if clipped at 1 + eps_high with A > 0
-};
-
 __device__ __forceinline__ TokenLoss token_loss(const GrpoParams& p, float w, float adv,
                                                 float lp, float lr, bool has_ref) {
-    TokenLoss r;
-    const float lo_b = 1.0f - p.eps_low;
-    const float hi_b = 1.0f + p.eps_high;
-    const float c1 = expf(w);
-    const float c2 = fminf(fmaxf(c1, lo_b), hi_b);
-    const float a = c1 * adv;
-    const float b = c2 * adv;
-    // d a / d w = c1 * adv; d b / d w = c1 * adv inside [lo_b, hi_b], else 0.
-    const float da = c1 * adv;
-    const float db = (c1 >= lo_b && c1 <= hi_b) ? da : 0.0f;
-    float dmin;
-    if (a < b) dmin = da;
-    else if (b < a) dmin = db;
-    else dmin = 0.5f * da + 0.5f * db;
-    r.loss = -fminf(a, b);
-    r.dw = -dmin;
-    r.kl = 0.0f;
-    r.dlp = 0.0f;
-    if (has_ref) {
-        const float d = lr - lp;
-        const float e = expf(d);
-        r.kl = e - d - 1.0f;
-        r.loss += p.beta * r.kl;
-        r.dlp = p.beta * (1.0f - e);
-    }
-    r.low = (c1 < lo_b && adv < 0.0f) ? 1.0f : 0.0f;
-    r.high = (c1 > hi_b && adv > 0.0f) ? 1.0f : 0.0f;
-    return r;
+    return grpo_token_loss(p.eps_low, p.eps_high, p.beta, w, adv, lp, lr, has_ref);
 }
 
 // Block-wide sums of K values, fixed order (xor-shuffle tree within waves,

@@ -97,6 +97,35 @@ struct GrpoParams {
 // Workspace words per row of the GRPO loss (5 used, padded).
 constexpr int kGrpoRowWords = 8;
 
+// Fused GRPO step (klp_grpo_step.hip): one workgroup per row, the row held
+// in registers.  Rows are token rows of a [B, S] batch (n_rows = B * S).
+struct GrpoStepParams {
+    const void* logits;
+    RowMap rm;
+    int64_t n_rows;
+    int64_t vocab;
+    const int64_t* targets;
+    float scale;              // 1 / temperature
+    const float* old_logp;    // [n_rows]
+    const float* ref_logp;    // [n_rows], nullable
+    const float* adv;         // [n_rows / seq_len], or [n_rows] when adv_per_token
+    const float* tok_weight;  // [n_rows]: d batch-loss / d token-loss (mask / normaliser)
+    int64_t seq_len;
+    float eps_low;
+    float eps_high;
+    float beta;
+    int adv_per_token;
+    float* logprob;           // [n_rows]
+    float* entropy;           // [n_rows]
+    float* lse;               // [n_rows], nullable
+    float* loss_tok;          // [n_rows]: tok_weight * token loss
+    void* d_logits;           // dense [n_rows, vocab], logits dtype
+};
+// Most 16-byte vectors one thread of the step kernel holds (1024 threads).
+constexpr int kGrpoStepMaxVec = 19;
+constexpr int kGrpoStepThreads = 1024;
+hipError_t launch_grpo_step(int dtype, const GrpoStepParams& p, hipStream_t stream);
+
 // Fused LM head forward (klp_lmhead.hip).
 struct LmhParams {
     const uint16_t* hidden;  // bf16 [n_tokens, ld_hidden], first `dim` columns used

@@ -11,6 +11,7 @@ from .ops import (  # noqa: F401
     fused_logprob_entropy_naive,
 )
 from .grpo import fused_grpo_loss  # noqa: F401
+from .grpo_step import fused_grpo_step  # noqa: F401
 from .lmhead import (  # noqa: F401
     fused_linear_logprob_entropy,
     fused_linear_logprob_entropy_forward,

@@ -1,0 +1,211 @@
+"""Fused GRPO step: per-token logprob / entropy, GRPO loss and d_logits in one
+pass over the logits.
+
+The reference's GRPO step runs, one after another, the logprob kernel
+(python/kernel_opt/trainer.py:38-130), the eager loss
+(examples/compare_one_step.py:232-236) and, in the backward, the logprob
+backward: the logits are read twice (forward, backward) and d_logits written
+once.  With token-level importance weights the gradient of the batch loss
+with respect to a token's log-probability is known as soon as that token's
+log-probability is, so ``klp_grpo_step`` keeps each row of logits in
+registers, computes logprob / entropy, the token's loss and its gradient,
+and writes the row's d_logits at once: one read of the logits instead of two.
+
+``fused_grpo_step`` returns the loss and the per-token log-probabilities and
+entropies; ``loss.backward()`` hands the precomputed d_logits to autograd.
+The same numbers come out of
+
+    logp, ent, _ = fused_logprob_entropy(logits, targets, temperature)
+    loss, _ = fused_grpo_loss(logp, old_logp, advantages, mask, ref_logp, ...)
+
+up to float32 rounding; that composition is also what runs when the fused
+step does not apply (sequence-level importance weights, rows longer than
+``klp_grpo_step_max_vocab``, rows not 16-byte aligned).
+
+Restrictions of the fused path, by construction:
+  * only the loss is differentiable: ``logp`` and ``entropy`` are returned
+    as constants (an extra loss term on them would get no gradient; use the
+    composition above for that);
+  * the backward can run once per forward (no ``retain_graph`` replays);
+  * an upstream gradient other than exactly 1 on the loss (e.g. a loss
+    scaled before ``backward()``) costs one extra pass over d_logits, and
+    telling the two apart reads the scalar back to the host.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _C
+from ._library import DTYPE_CODES, check_status, lib
+from .grpo import fused_grpo_loss
+from .ops import fused_logprob_entropy
+
+__all__ = ["fused_grpo_step", "grpo_token_weights", "grpo_step_launch"]
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def grpo_token_weights(mask: torch.Tensor, loss_type: str = "bnpo",
+                       max_completion_length: int | None = None,
+                       normalizer: float | None = None) -> torch.Tensor:
+    """Weight of each token's loss in the batch loss (float32 ``[B, S]``):
+    the mask divided by the loss type's normaliser, as ``fused_grpo_loss``
+    applies it ("grpo": B * max(row mask sum, 1); "bnpo": max(mask sum, 1);
+    "dr_grpo": B * max_completion_length (default S); "dapo": normalizer)."""
+    m = mask.to(torch.float32)
+    B, S = m.shape
+    if loss_type == "grpo":
+        den = m.sum(dim=1, keepdim=True).clamp(min=1.0) * float(B)
+        return m * (1.0 / den)
+    if loss_type == "bnpo":
+        return m * (1.0 / m.sum().clamp(min=1.0))
+    if loss_type == "dr_grpo":
+        L = S if max_completion_length is None else max_completion_length
+        return m * (1.0 / torch.tensor(float(B * L), dtype=torch.float32, device=m.device))
+    if loss_type == "dapo":
+        if normalizer is None:
+            raise ValueError("loss_type='dapo' needs `normalizer`")
+        return m * (1.0 / torch.tensor(float(normalizer), dtype=torch.float32, device=m.device))
+    raise ValueError(f"unknown loss_type {loss_type!r}")
+
+
+def _fused_supported(logits: torch.Tensor, rows) -> bool:
+    """True when klp_grpo_step accepts these logits (row capacity and
+    16-byte aligned rows of whole 16-byte vectors)."""
+    if rows is None or logits.dtype not in DTYPE_CODES:
+        return False
+    V = logits.size(-1)
+    esz = logits.element_size()
+    if V > lib.klp_grpo_step_max_vocab(DTYPE_CODES[logits.dtype]):
+        return False
+    _, s_outer, s_inner = rows
+    return ((V * esz) % 16 == 0 and logits.data_ptr() % 16 == 0
+            and (s_inner * esz) % 16 == 0 and (s_outer * esz) % 16 == 0)
+
+
+def grpo_step_launch(logits, targets, old, ref, adv, weight, params):
+    """One klp_grpo_step call, no autograd: returns float32 ``logp``,
+    ``entropy``, ``lse``, ``loss_tok`` ``[B, S]`` and ``d_logits`` (dense,
+    logits dtype).  ``old`` / ``ref`` / ``adv`` / ``weight`` are float32,
+    contiguous, on the logits' device; ``params`` = (temperature, eps_low,
+    eps_high, beta, adv_per_token)."""
+    temperature, eps_low, eps_high, beta, per_token = params
+    B, S, V = logits.shape
+    dev = logits.device
+    rows = _C.row_layout(logits)
+    if rows is None:
+        raise RuntimeError("logits must be contiguous")
+    logp, ent, lse, loss_tok = (torch.empty((B, S), dtype=torch.float32, device=dev)
+                                for _ in range(4))
+    d_logits = torch.empty((B, S, V), dtype=logits.dtype, device=dev)
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.klp_grpo_step(_ptr(logits), DTYPE_CODES[logits.dtype], B * S, V, *rows,
+                               _ptr(targets), float(temperature), _ptr(old), _ptr(ref),
+                               _ptr(adv), _ptr(weight), S, eps_low, eps_high, beta, per_token,
+                               _ptr(logp), _ptr(ent), _ptr(lse), _ptr(loss_tok), _ptr(d_logits),
+                               ctypes.c_void_p(stream))
+    check_status(rc)
+    return logp, ent, lse, loss_tok, d_logits
+
+
+class _FusedGrpoStep(torch.autograd.Function):
+
+    @staticmethod
+    def forward(ctx, logits, targets, old, ref, adv, weight, params):
+        logp, ent, _lse, loss_tok, d_logits = grpo_step_launch(logits, targets, old, ref, adv,
+                                                               weight, params)
+        ctx.d_logits = d_logits
+        ctx.mark_non_differentiable(logp, ent)
+        return loss_tok.sum(), logp, ent
+
+    @staticmethod
+    def backward(ctx, g_loss, _g_logp, _g_ent):
+        d = ctx.d_logits
+        if d is None:
+            raise RuntimeError("fused_grpo_step: the backward can run only once per forward "
+                               "(retain_graph replays are not supported)")
+        ctx.d_logits = None
+        if g_loss is None or not ctx.needs_input_grad[0]:
+            return None, None, None, None, None, None, None
+        g = float(g_loss)
+        if g != 1.0:
+            # A Python scalar: torch multiplies in float32 with fp32(g) and
+            # rounds once to d's dtype (a 0-dim device tensor would first be
+            # cast to d's dtype).
+            d = d * g
+        return d, None, None, None, None, None, None
+
+
+def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch.Tensor,
+                    advantages: torch.Tensor, mask: torch.Tensor | None = None,
+                    ref_logp: torch.Tensor | None = None, *, eps_low: float = 0.2,
+                    eps_high: float | None = None, beta: float = 0.0, loss_type: str = "bnpo",
+                    importance_level: str = "token", max_completion_length: int | None = None,
+                    normalizer: float | None = None, temperature: float | None = None,
+                    return_stats: bool = False):
+    """GRPO loss of ``logits`` ``[B, S, V]`` (the completion window, rows as
+    :func:`kernel_opt.fused_logprob_entropy` accepts them) for ``targets``
+    ``[B, S]`` (int64), differentiable in ``logits``.
+
+    The loss arguments are those of :func:`kernel_opt.fused_grpo_loss`;
+    ``temperature`` divides the logits as in ``fused_logprob_entropy``.
+
+    Returns ``(loss, logp, entropy)``, or ``(loss, logp, entropy, stats)``
+    with ``return_stats`` (stats as ``fused_grpo_loss`` returns them).
+    ``logp`` and ``entropy`` are float32 ``[B, S]`` constants when the fused
+    path runs.
+    """
+    if logits.dim() != 3:
+        raise RuntimeError(f"logits must be [B, S, V], got shape {tuple(logits.shape)}")
+    if not logits.is_cuda:
+        raise RuntimeError("logits must be a GPU tensor")
+    B, S, V = logits.shape
+    if tuple(targets.shape) != (B, S):
+        raise RuntimeError(f"targets has shape {tuple(targets.shape)}, expected {(B, S)}")
+    if importance_level not in ("token", "sequence"):
+        raise ValueError(f"importance_level must be 'token' or 'sequence', got {importance_level!r}")
+    t = 1.0 if temperature is None else float(temperature)
+    if not (t > 0.0 and t != float("inf")):
+        raise RuntimeError(f"temperature must be finite and > 0, got {t}")
+    loss_kw = dict(eps_low=eps_low, eps_high=eps_high, beta=beta, loss_type=loss_type,
+                   importance_level=importance_level,
+                   max_completion_length=max_completion_length, normalizer=normalizer)
+
+    rows = _C.row_layout(logits)
+    if (importance_level != "token" or B * S == 0 or not targets.is_contiguous()
+            or targets.dtype != torch.int64 or not _fused_supported(logits, rows)):
+        # The unfused composition: same loss, logp / entropy differentiable.
+        logp, ent, _ = fused_logprob_entropy(logits, targets, temperature)
+        loss, stats = fused_grpo_loss(logp, old_logp, advantages, mask, ref_logp, **loss_kw)
+        return (loss, logp, ent, stats) if return_stats else (loss, logp, ent)
+
+    dev = logits.device
+
+    def f32(x, name, shape):
+        if x.device != dev:
+            raise RuntimeError(f"{name} must be on {dev}")
+        x = x.detach().to(torch.float32)
+        if tuple(x.shape) != shape:
+            raise RuntimeError(f"{name} has shape {tuple(x.shape)}, expected {shape}")
+        return x.contiguous()
+
+    old = f32(old_logp, "old_logp", (B, S))
+    per_token = advantages.dim() != 1
+    adv = f32(advantages, "advantages", (B, S) if per_token else (B,))
+    m = (f32(mask, "mask", (B, S)) if mask is not None
+         else torch.ones((B, S), dtype=torch.float32, device=dev))
+    ref = f32(ref_logp, "ref_logp", (B, S)) if (beta != 0.0 and ref_logp is not None) else None
+    weight = grpo_token_weights(m, loss_type, max_completion_length, normalizer).contiguous()
+    eh = eps_low if eps_high is None else eps_high
+    params = (t, float(eps_low), float(eh), float(beta), int(per_token))
+    loss, logp, ent = _FusedGrpoStep.apply(logits, targets, old, ref, adv, weight, params)
+    if not return_stats:
+        return loss, logp, ent
+    with torch.no_grad():
+        _, stats = fused_grpo_loss(logp, old, adv, m, ref, **loss_kw)
+    return loss, logp, ent, stats

@@ -217,6 +217,46 @@ int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp
                  void* stream);
 
 /*
+ * Fused GRPO step: klp_fwd, the GRPO loss's per-token gradient and klp_bwd in
+ * one pass over the logits.  No counterpart in the reference, whose trainer
+ * runs the logprob kernel (python/kernel_opt/trainer.py:38-130), then the
+ * eager loss (examples/compare_one_step.py:232-236), then the logprob
+ * backward, one after another.  With token-level importance weights the
+ * upstream gradient of a token's log-probability is
+ * tok_weight * d loss_tok / d logp, known as soon as that token's logprob
+ * is, so each workgroup keeps its row of logits in registers, computes
+ * logprob / entropy / lse, then writes the row's d_logits at once: the
+ * logits are read once instead of twice.
+ *   logits, targets, temperature: as klp_fwd_temp (n_rows = n_seqs * seq_len
+ *       token rows, row r of completion r / seq_len);
+ *   old_logp, ref_logp (NULL: no KL term), advantages: as klp_grpo_fwd
+ *       (advantages [n_rows / seq_len], or [n_rows] when adv_per_token);
+ *   tok_weight [n_rows]: the weight of each token's loss in the batch loss,
+ *       mask / normaliser (e.g. mask / max(sum mask, 1) for
+ *       KLP_GRPO_LOSS_BNPO).
+ * Writes logprob, entropy and (unless NULL) lse [n_rows] as klp_fwd;
+ * loss_tok [n_rows] = tok_weight * loss_tok (the batch loss is their sum);
+ * and d_logits (dense [n_rows, vocab], logits dtype, 16-byte aligned) =
+ * d (sum loss_tok) / d logits, exactly klp_bwd's formula with
+ * g_logp = tok_weight * d loss_tok / d logp and g_ent = g_lse = 0.
+ * Only rows of at most klp_grpo_step_max_vocab(dtype) elements whose start
+ * and length are whole 16-byte vectors are supported (row starts 16-byte
+ * aligned, vocab * element size a multiple of 16); anything else returns
+ * KLP_EINVAL, and the caller runs klp_fwd / klp_grpo_fwd / klp_grpo_bwd /
+ * klp_bwd instead.  No workspace.
+ */
+int64_t klp_grpo_step_max_vocab(int dtype);
+
+int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                  int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                  const int64_t* targets, float temperature,
+                  const float* old_logp, const float* ref_logp, const float* advantages,
+                  const float* tok_weight, int64_t seq_len,
+                  float eps_low, float eps_high, float beta, int adv_per_token,
+                  float* logprob, float* entropy, float* lse, float* loss_tok,
+                  void* d_logits, void* stream);
+
+/*
  * Fused LM head + per-token logprob / entropy, forward.  No counterpart in the
  * reference, which names it as its follow-up (a Liger-style fused linear +
  * loss, docs/FINAL_REPORT.md:439-450): instead of logits = hidden @ weight^T

@@ -239,3 +239,48 @@ def test_grpo_validation_errors():
     rc = lib.klp_grpo_bwd(P, P, None, P, None, 4, 10, 0.2, 0.2, 0.0, 1.0, 1, 0, 0, None, None,
                           P, ws, None)
     assert rc == KLP_EINVAL and "d_logp" in _err()
+
+
+def test_grpo_step_validation_errors():
+    """klp_grpo_step rejects what it cannot run before any launch (no GPU
+    needed): the fused path's row-capacity and 16-byte row rules, seq_len,
+    null pointers, loss parameters; an injected launch failure is reported."""
+    from kernel_opt._library import KLP_EDTYPE, KLP_EINVAL, KLP_ELAUNCH, lib
+    assert lib.klp_grpo_step_max_vocab(0) == 19 * 1024 * 8
+    assert lib.klp_grpo_step_max_vocab(1) == 19 * 1024 * 8
+    assert lib.klp_grpo_step_max_vocab(2) == 19 * 1024 * 4
+    assert lib.klp_grpo_step_max_vocab(5) == 0
+    A = ctypes.c_void_p(0x100000)  # 16-byte aligned fake device address
+
+    def step(**kw):
+        a = dict(logits=A, dtype=0, n=8, v=4096, ri=8, so=0, si=4096, tg=A, temp=1.0, old=A,
+                 ref=None, adv=A, w=A, S=4, el=0.2, eh=0.28, beta=0.0, pt=0, lp=A, ent=A,
+                 lse=None, lt=A, d=A)
+        a.update(kw)
+        return lib.klp_grpo_step(a["logits"], a["dtype"], a["n"], a["v"], a["ri"], a["so"],
+                                 a["si"], a["tg"], a["temp"], a["old"], a["ref"], a["adv"],
+                                 a["w"], a["S"], a["el"], a["eh"], a["beta"], a["pt"], a["lp"],
+                                 a["ent"], a["lse"], a["lt"], a["d"], None)
+    assert step(n=0) == 0
+    assert step(dtype=9) == KLP_EDTYPE
+    assert step(temp=0.0) == KLP_EINVAL and "temperature" in _err()
+    assert step(S=3) == KLP_EINVAL and "seq_len" in _err()
+    assert step(S=0) == KLP_EINVAL and "seq_len" in _err()
+    assert step(v=155648 + 8, si=155656) == KLP_EINVAL and "capacity" in _err()
+    assert step(dtype=2, v=77824 + 4, si=77828) == KLP_EINVAL and "capacity" in _err()
+    assert step(v=4100, si=4100) == KLP_EINVAL and "16-byte" in _err()
+    assert step(logits=ctypes.c_void_p(0x100008)) == KLP_EINVAL and "16-byte" in _err()
+    assert step(si=4100) == KLP_EINVAL and "16-byte" in _err()
+    assert step(ri=4, so=8196) == KLP_EINVAL and "16-byte" in _err()
+    assert step(old=None) == KLP_EINVAL and "old_logp" in _err()
+    assert step(w=None) == KLP_EINVAL and "tok_weight" in _err()
+    assert step(lt=None) == KLP_EINVAL and "loss_tok" in _err()
+    assert step(d=None) == KLP_EINVAL and "d_logits" in _err()
+    assert step(d=ctypes.c_void_p(0x100004)) == KLP_EINVAL and "d_logits" in _err()
+    assert step(el=-1.0) == KLP_EINVAL and "eps_low" in _err()
+    assert step(beta=float("inf")) == KLP_EINVAL and "beta" in _err()
+    lib.klp_debug_fail_next_launches(1)
+    try:
+        assert step() == KLP_ELAUNCH and "grpo step" in _err()
+    finally:
+        lib.klp_debug_fail_next_launches(0)

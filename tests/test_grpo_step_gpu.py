@@ -1,0 +1,271 @@
+"""GPU parity of the fused GRPO step (klp_grpo_step.hip), called through the
+C ABI (kernel_opt.grpo_step.grpo_step_launch -> klp_grpo_step).
+
+Bars:
+  * logprob / entropy / lse against the float64 oracle (klp_oracle.c) within
+    the forward tolerance (1e-5 fp32 input, 2e-5 bf16 / fp16 input);
+  * the loss against the float64 GRPO oracle evaluated at the kernel's own
+    log-probabilities, within 1e-5 relative;
+  * d_logits equal, value for value, to klp_bwd's output for the same row
+    statistics and upstream gradient (the step uses klp_bwd's formula), that
+    upstream gradient being klp_grpo_bwd's d_logp at the kernel's
+    log-probabilities; and d_logits within klp_bwd's own bar against the
+    float64 oracle's backward (1 ulp of the output dtype, or the fp32 noise of
+    cancelling terms: klp_testutil.grad_check);
+  * at the C2 size ([4, 256, 152064] bf16) against the unfused composition
+    (fused_logprob_entropy + fused_grpo_loss + backward): loss within 1e-5
+    relative, logprob / entropy within twice the forward tolerance, d_logits
+    within 1 bf16 ulp;
+  * repeated calls are bitwise identical.
+Inputs are generated on the CPU from fixed seeds and copied to the GPU.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from klp_testutil import FWD_TOL, grad_check, storage_bits, ulp_diff
+from oracle.grpo_oracle import grpo_loss
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+IGNORE = -100
+
+
+def _ko():
+    import kernel_opt
+    return kernel_opt
+
+
+def make_case(B, S, V, dtype, seed, adv_per_token=False, neg_inf=False):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(B, S, V, generator=g) * 2.0).to(dtype)
+    if neg_inf:
+        x[0, 0, ::7] = float("-inf")
+        x[-1, -1, : V // 2] = float("-inf")
+    t = torch.randint(0, V, (B, S), generator=g)
+    if S > 1:
+        t[0, 1] = IGNORE
+    mask = (torch.rand(B, S, generator=g) < 0.75).float()
+    mask[0, 0] = 1.0
+    adv = torch.randn((B, S) if adv_per_token else (B,), generator=g)
+    return x, t, mask, adv
+
+
+def old_ref(logp_cpu: torch.Tensor, seed: int):
+    g = torch.Generator().manual_seed(seed + 1)
+    old = logp_cpu + 0.3 * torch.randn(logp_cpu.shape, generator=g)
+    ref = logp_cpu + 0.3 * torch.randn(logp_cpu.shape, generator=g)
+    return old.float(), ref.float()
+
+
+def oracle_kw(loss_type, beta, B, L=None, normalizer=None):
+    kind = loss_type if loss_type in ("grpo", "bnpo") else "fixed"
+    norm = {"dr_grpo": float(B * (L or 1)), "dapo": normalizer}.get(loss_type, 1.0)
+    return dict(eps_low=0.2, eps_high=0.28, beta=beta, loss_type=kind, norm_const=norm)
+
+
+def run_step(x, t, old, adv, mask, ref, loss_type, beta, temperature=None, **extra):
+    """klp_grpo_step on the GPU; returns (logp, ent, lse, loss_tok, d) on the GPU."""
+    from kernel_opt.grpo_step import grpo_step_launch, grpo_token_weights
+    B, S, _ = x.shape
+    w = grpo_token_weights(mask.to(DEV), loss_type, **extra).contiguous()
+    params = (1.0 if temperature is None else temperature, 0.2, 0.28, beta,
+              int(adv.dim() != 1))
+    r = ref.to(DEV) if (beta != 0.0 and ref is not None) else None
+    return grpo_step_launch(x.to(DEV), t.to(DEV), old.to(DEV), r, adv.to(DEV), w, params)
+
+
+def unfused_g_logp(logp, old, adv, mask, ref, loss_type, beta, **extra):
+    """klp_grpo_bwd's d_logp at the given log-probabilities."""
+    lp = logp.detach().clone().requires_grad_(True)
+    loss, _ = _ko().fused_grpo_loss(lp, old.to(DEV), adv.to(DEV), mask.to(DEV),
+                                    None if ref is None else ref.to(DEV), eps_low=0.2,
+                                    eps_high=0.28, beta=beta, loss_type=loss_type, **extra)
+    loss.backward()
+    return lp.grad
+
+
+def unfused_bwd(x, t, lse, ent, g, temperature=None):
+    from kernel_opt import _C
+    d = torch.empty(x.shape, dtype=x.dtype, device=DEV)
+    _C.bwd_launch(x, t, lse, ent, g.contiguous(), None, None, d, temperature=temperature)
+    return d
+
+
+CASES = [
+    # (dtype, B, S, V)
+    (torch.bfloat16, 3, 5, 64),       # fewer vectors than threads
+    (torch.bfloat16, 3, 5, 8192),     # exactly one vector per thread, no partial one
+    (torch.bfloat16, 2, 4, 12000),    # a partial last vector
+    (torch.bfloat16, 1, 3, 152064),   # the C2 vocabulary
+    (torch.bfloat16, 1, 2, 155648),   # the row capacity
+    (torch.float16, 3, 5, 4096),
+    (torch.float16, 1, 3, 152064),
+    (torch.float32, 3, 5, 4096),
+    (torch.float32, 2, 3, 77824),     # the fp32 row capacity
+]
+
+
+@pytest.mark.parametrize("dtype,B,S,V", CASES)
+@pytest.mark.parametrize("loss_type,beta,temperature", [("bnpo", 0.0, None),
+                                                        ("grpo", 0.04, 0.7),
+                                                        ("dr_grpo", 0.0, 1.3)])
+def test_matches_oracle(dtype, B, S, V, loss_type, beta, temperature, oracle):
+    seed = 100 + V % 97 + B
+    print(f"grpo step: dtype={dtype} shape={(B, S, V)} {loss_type} beta={beta} T={temperature}",
+          flush=True)
+    x, t, mask, adv = make_case(B, S, V, dtype, seed, adv_per_token=(loss_type == "grpo"))
+    e_lp, e_ent, e_lse = oracle.forward(x, t.numpy(), temperature=temperature)
+    old, ref = old_ref(torch.tensor(e_lp), seed)
+    extra = dict(max_completion_length=S + 3) if loss_type == "dr_grpo" else {}
+    logp, ent, lse, loss_tok, d = run_step(x, t, old, adv, mask, ref, loss_type, beta,
+                                           temperature, **extra)
+    tol = FWD_TOL[dtype]
+    for name, ours, e in (("logp", logp, e_lp), ("entropy", ent, e_ent), ("lse", lse, e_lse)):
+        err = np.abs(ours.cpu().double().numpy() - e).max()
+        assert err <= tol, f"{name}: {err:.3g} > {tol}"
+
+    okw = oracle_kw(loss_type, beta, B, S + 3)
+    r = ref.numpy() if beta != 0.0 else None
+    k_lp = logp.cpu().double().numpy()
+    e_loss, _, e_g = grpo_loss(k_lp, old.numpy(), adv.numpy(), mask.numpy(), r, **okw)
+    loss = loss_tok.sum().item()
+    assert abs(loss - e_loss) <= 1e-5 * max(1.0, abs(e_loss)), (loss, e_loss)
+
+    g = unfused_g_logp(logp, old, adv, mask, ref if beta != 0.0 else None, loss_type, beta,
+                       **extra)
+    gmax = np.abs(e_g).max()
+    assert np.all(np.abs(g.cpu().double().numpy() - e_g) <= 1e-5 * gmax + 1e-5 * np.abs(e_g))
+    d_ref = unfused_bwd(x.to(DEV), t.to(DEV), lse, ent, g, temperature)
+    assert torch.equal(d, d_ref), "d_logits differ from klp_bwd with the same inputs"
+    worst, detail = grad_check(oracle, x, t, lse, ent, d, g_logp=g, temperature=temperature)
+    assert worst <= 1.0, detail
+
+
+def test_neg_inf_logits_and_masked_rows(oracle):
+    """-inf logits (the clamped rescan) get a zero gradient; masked tokens
+    get an all-zero d_logits row."""
+    B, S, V = 2, 4, 4096
+    x, t, mask, adv = make_case(B, S, V, torch.bfloat16, 7, neg_inf=True)
+    mask[1, 2] = 0.0
+    t[0, 0] = 1        # finite targets in the rows with -inf logits (a -inf
+    t[-1, -1] = V - 1  # target logit would make the token's loss NaN)
+    e_lp, e_ent, e_lse = oracle.forward(x, t.numpy())
+    old, ref = old_ref(torch.tensor(e_lp), 7)
+    logp, ent, lse, _, d = run_step(x, t, old, adv, mask, ref, "bnpo", 0.04)
+    for ours, e in ((logp, e_lp), (ent, e_ent), (lse, e_lse)):
+        assert np.abs(ours.cpu().double().numpy() - e).max() <= 2e-5
+    dc = d.cpu().float()
+    assert torch.all(dc[torch.isinf(x.float())] == 0)
+    assert torch.all(dc[1, 2] == 0)
+    g = unfused_g_logp(logp, old, adv, mask, ref, "bnpo", 0.04)
+    assert torch.equal(d, unfused_bwd(x.to(DEV), t.to(DEV), lse, ent, g))
+
+
+def test_sliced_logits_match_contiguous():
+    """The shifted slice logits[:, :-1, :] runs in place (row strides) with the
+    same results as its contiguous copy."""
+    B, L, V = 3, 6, 8192
+    x_full, _, _, _ = make_case(B, L, V, torch.bfloat16, 9)
+    x_full = x_full.to(DEV)
+    view = x_full[:, :-1, :]
+    S = L - 1
+    _, t, mask, adv = make_case(B, S, V, torch.bfloat16, 10)
+    old = torch.full((B, S), -9.0)
+    a = run_step(view, t, old, adv, mask, None, "grpo", 0.0)
+    b = run_step(view.contiguous(), t, old, adv, mask, None, "grpo", 0.0)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_repeatable():
+    x, t, mask, adv = make_case(2, 8, 152064, torch.bfloat16, 11)
+    old = torch.full((2, 8), -11.0)
+    a = run_step(x, t, old, adv, mask, None, "bnpo", 0.0)
+    b = run_step(x, t, old, adv, mask, None, "bnpo", 0.0)
+    for u, v in zip(a, b):
+        assert torch.equal(u.view(torch.uint8) if u.dtype != torch.float32 else u,
+                           v.view(torch.uint8) if v.dtype != torch.float32 else v)
+
+
+def test_autograd_op():
+    """fused_grpo_step: loss.backward() delivers the kernel's d_logits; a
+    scaled loss scales it; the backward runs once; logp / entropy carry no
+    gradient."""
+    ko = _ko()
+    B, S, V = 2, 6, 4096
+    x, t, mask, adv = make_case(B, S, V, torch.bfloat16, 12)
+    old = torch.full((B, S), -8.0)
+    _, _, _, lt, d = run_step(x, t, old, adv, mask, None, "bnpo", 0.0)
+    xg = x.to(DEV).requires_grad_(True)
+    loss, logp, ent = ko.fused_grpo_step(xg, t.to(DEV), old.to(DEV), adv.to(DEV), mask.to(DEV))
+    assert not logp.requires_grad and not ent.requires_grad
+    assert torch.equal(loss, lt.sum())
+    loss.backward()
+    assert torch.equal(xg.grad, d)
+    with pytest.raises(RuntimeError, match="only once"):
+        loss.backward()
+
+    xg2 = x.to(DEV).requires_grad_(True)
+    loss2, _, _ = ko.fused_grpo_step(xg2, t.to(DEV), old.to(DEV), adv.to(DEV), mask.to(DEV))
+    (loss2 * 0.3).backward()
+    assert torch.equal(xg2.grad, (d.float() * torch.tensor(0.3, device=DEV)).to(d.dtype))
+
+
+def test_fallbacks_match_composition():
+    """Inputs the fused path does not take (vocab not a whole number of
+    16-byte vectors, above the row capacity, sequence-level weights) run the
+    unfused composition, with the same results."""
+    ko = _ko()
+    for V, level in ((1001, "token"), (160000, "token"), (4096, "sequence")):
+        print(f"grpo step fallback: V={V} level={level}", flush=True)
+        x, t, mask, adv = make_case(2, 3, V, torch.bfloat16, 13)
+        old = torch.full((2, 3), -9.0).to(DEV)
+        xa = x.to(DEV).requires_grad_(True)
+        la, lpa, _ = ko.fused_grpo_step(xa, t.to(DEV), old, adv.to(DEV), mask.to(DEV),
+                                        importance_level=level)
+        la.backward()
+        xb = x.to(DEV).requires_grad_(True)
+        lpb, _, _ = ko.fused_logprob_entropy(xb, t.to(DEV))
+        lb, _ = ko.fused_grpo_loss(lpb, old, adv.to(DEV), mask.to(DEV), importance_level=level)
+        lb.backward()
+        assert torch.equal(la, lb) and torch.equal(lpa, lpb)
+        assert torch.equal(xa.grad, xb.grad)
+
+
+def test_c2_matches_unfused_composition():
+    """C2 ([4, 256, 152064] bf16): the fused step against the unfused
+    composition on the same inputs."""
+    ko = _ko()
+    B, S, V = 4, 256, 152064
+    g = torch.Generator(device=DEV).manual_seed(14)
+    x = (torch.randn(B, S, V, generator=g, device=DEV) * 2.0).to(torch.bfloat16)
+    t = torch.randint(0, V, (B, S), generator=g, device=DEV)
+    mask = (torch.rand(B, S, generator=g, device=DEV) < 0.9).float()
+    adv = torch.randn(B, generator=g, device=DEV)
+    with torch.no_grad():
+        lp0, _, _ = ko.fused_logprob_entropy_forward(x, t)
+    old = lp0 + 0.2 * torch.randn(B, S, generator=g, device=DEV)
+    ref = lp0 + 0.2 * torch.randn(B, S, generator=g, device=DEV)
+    kw = dict(eps_low=0.2, eps_high=0.28, beta=0.04, loss_type="grpo")
+
+    xa = x.clone().requires_grad_(True)
+    la, lpa, enta = ko.fused_grpo_step(xa, t, old, adv, mask, ref, **kw)
+    la.backward()
+    xb = x.clone().requires_grad_(True)
+    lpb, entb, _ = ko.fused_logprob_entropy(xb, t)
+    lb, _ = ko.fused_grpo_loss(lpb, old, adv, mask, ref, **kw)
+    lb.backward()
+    assert abs(la.item() - lb.item()) <= 1e-5 * max(1.0, abs(lb.item()))
+    assert (lpa - lpb).abs().max().item() <= 4e-5
+    assert (enta - entb).abs().max().item() <= 4e-5
+    da = xa.grad.view(torch.int16).to(torch.int32)
+    db = xb.grad.view(torch.int16).to(torch.int32)
+
+    def ordered(v):
+        mag = v & 0x7FFF
+        return torch.where(v < 0, -mag, mag)
+    ulps = (ordered(da) - ordered(db)).abs().max().item()
+    assert ulps <= 1, f"d_logits up to {ulps} bf16 ulp from the unfused composition"
