@@ -260,6 +260,80 @@ def grpo_timing(dev, K, B=16, S=2048):
             "note": "loss + loss.backward() per iteration, end to end from Python"}
 
 
+def grpo_step_timing(dev, K, logits, targets):
+    """The fused GRPO step (klp_grpo_step: logprob, GRPO loss gradient and
+    d_logits in one read of the logits) against the unfused kernel chain
+    klp_fwd -> klp_grpo_fwd -> klp_grpo_bwd -> klp_bwd on the same logits,
+    both through the C ABI with preallocated outputs (kernel time only)."""
+    import ctypes
+    from kernel_opt import _C
+    from kernel_opt._library import (DTYPE_CODES, KLP_GRPO_LOSS_GRPO, KLP_GRPO_TOKEN,
+                                     check_status, lib)
+    from kernel_opt.grpo_step import grpo_token_weights
+    B, S, V = logits.shape
+    N = B * S
+    if V > lib.klp_grpo_step_max_vocab(DTYPE_CODES[logits.dtype]):
+        return None
+    g = torch.Generator(device="cpu").manual_seed(77)
+    f32 = lambda *shape: torch.empty(*shape, dtype=torch.float32, device=dev)
+    lp, ent, lse, loss_tok, d_logp = (f32(B, S) for _ in range(5))
+    with torch.no_grad():
+        _C.fwd_launch(logits, targets, lp, ent, lse)
+    old = (lp.cpu() + 0.2 * torch.randn(B, S, generator=g)).to(dev)
+    ref = (lp.cpu() + 0.2 * torch.randn(B, S, generator=g)).to(dev)
+    adv = torch.randn(B, generator=g).to(dev)
+    mask = (torch.rand(B, S, generator=g) < 0.9).float().to(dev)
+    w = grpo_token_weights(mask, "grpo").contiguous()
+    d = torch.empty(logits.shape, dtype=logits.dtype, device=dev)
+    ws = torch.empty(lib.klp_grpo_workspace_bytes(B), dtype=torch.uint8, device=dev)
+    loss = f32(1)
+    rows = _C.row_layout(logits)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    eps_low, eps_high, beta = 0.2, 0.28, 0.04
+    gparams = (eps_low, eps_high, beta, 1.0, KLP_GRPO_LOSS_GRPO, KLP_GRPO_TOKEN, 0)
+
+    def fused():
+        check_status(lib.klp_grpo_step(P(logits), DTYPE_CODES[logits.dtype], N, V, *rows,
+                                       P(targets), 1.0, P(old), P(ref), P(adv), P(w), S,
+                                       eps_low, eps_high, beta, 0, P(lp), P(ent), P(lse),
+                                       P(loss_tok), P(d), st))
+
+    def unfused():
+        _C.fwd_launch(logits, targets, lp, ent, lse)
+        check_status(lib.klp_grpo_fwd(P(lp), P(old), P(ref), P(adv), P(mask), B, S, *gparams,
+                                      P(loss), None, P(ws), ws.numel(), st))
+        check_status(lib.klp_grpo_bwd(P(lp), P(old), P(ref), P(adv), P(mask), B, S, *gparams,
+                                      None, P(d_logp), P(ws), ws.numel(), st))
+        _C.bwd_launch(logits, targets, lse, ent, d_logp, None, None, d)
+
+    res = {}
+    for name, fn in (("fused", fused), ("unfused", unfused)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(K):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        res[name] = a.elapsed_time(b) / K * 1e3
+    nbytes = 2 * logits.numel() * logits.element_size()  # one read + one write
+    tbps = nbytes / (res["fused"] * 1e-6) / 1e12
+    del d
+    torch.cuda.empty_cache()
+    return {"shape": [B, S, V], "loss_type": "grpo", "beta": beta,
+            "fused_us": round(res["fused"], 2), "unfused_us": round(res["unfused"], 2),
+            "speedup": round(res["unfused"] / res["fused"], 3),
+            "fused_algorithmic_bytes": nbytes, "fused_tbps": round(tbps, 4),
+            "fused_pct_peak": round(100 * tbps / HBM_PEAK_TBPS, 2),
+            "note": "fused = klp_grpo_step (logits read once, d_logits written once); "
+                    "unfused = klp_fwd, klp_grpo_fwd, klp_grpo_bwd, klp_bwd (logits read "
+                    "twice); both kernel time through the C ABI, outputs preallocated"}
+
+
 def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
     """The fused LM head (hidden @ weight^T folded into the logprob/entropy
     reduction, klp_lmh_*) against the unfused path (a bf16 library matmul,
@@ -337,7 +411,8 @@ def main(argv=None):
     ap.add_argument("--no-lmhead", action="store_true",
                     help="skip the fused LM-head timing (klp_lmh_* against matmul + logprob)")
     ap.add_argument("--no-grpo", action="store_true",
-                    help="skip the GRPO-loss timing (fused klp_grpo_* against the eager chain)")
+                    help="skip the GRPO timings (the loss kernels against the eager chain, "
+                         "the fused step against the unfused kernels)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run torch's copy of a buffer the size of the logits (known "
                          "traffic, for scaling HBM counters)")
@@ -459,6 +534,7 @@ def main(argv=None):
         }
 
     grpo = None if args.no_grpo else grpo_timing(dev, K)
+    step = None if args.no_grpo else grpo_step_timing(dev, K, logits, targets)
     lmhead = None if args.no_lmhead else lmhead_timing(dev)
 
     B, S, _ = cfg["shape"]
@@ -508,6 +584,7 @@ def main(argv=None):
         },
         "cpu_baseline": cpu,
         "grpo_loss": grpo,
+        "grpo_step": step,
         "lm_head": lmhead,
     }
     print(json.dumps(out))

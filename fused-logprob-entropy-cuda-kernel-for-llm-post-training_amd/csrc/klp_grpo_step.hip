@@ -10,10 +10,10 @@
 //   d[v] = (onehot(v == t) - p_v) * g_logp          (times 1/T).
 // The unfused step reads the logits twice (forward, backward) and writes
 // d_logits once; here one workgroup of 1024 threads keeps its whole row in
-// registers (up to kGrpoStepMaxVec = 19 16-byte vectors per thread, 76 of
-// the 128 VGPRs a 1024-thread workgroup allows: 304 KB, a bf16 row of
-// V <= 155648 or an fp32 row of V <= 77824; 20 vectors spill), so the logits are read once: 2 passes of HBM traffic
-// instead of 3.
+// registers, so the logits are read once: 2 passes of HBM traffic instead
+// of 3.  A thread holds up to kGrpoStepMaxVec = 19 16-byte vectors (76 of the
+// 128 VGPRs a 1024-thread workgroup allows; 20 spill): 304 KB per row, a
+// bf16 row of V <= 155648 or an fp32 row of V <= 77824.
 //
 // Per workgroup (one row):
 //  1. load the row into registers (16-byte loads, non-temporal);
@@ -21,8 +21,8 @@
 //     reduction and the 16 waves in order through LDS;
 //  3. logprob, entropy, lse of the row; the GRPO terms of the token
 //     (grpo_token_loss, shared with klp_grpo.hip); loss_tok = w_t * loss_t;
-//  4. d_logits from the registers (grad_one(), as klp_bwd), non-temporal
-//     16-byte stores.
+//  4. d_logits from the registers (klp_bwd's gradient, which with g_ent = 0
+//     is p * (-g_logp) plus the one-hot term), non-temporal 16-byte stores.
 // Rows too long for the registers, or whose start or length is not a whole
 // number of 16-byte vectors, are rejected by the caller (KLP_EINVAL), which
 // then runs the unfused kernels.
@@ -135,8 +135,10 @@ __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_kernel(GrpoStepPar
         if (k > n_full || i >= nvec) break;
         float x[EPV];
         unpack<DT>(r[k], x);
+        // klp_bwd's gradient with g_ent = g_lse = 0 (grad_one_logp_only).
 #pragma unroll
-        for (int j = 0; j < EPV; ++j) x[j] = grad_one(kScaled ? x[j] * p.scale : x[j], g);
+        for (int j = 0; j < EPV; ++j)
+            x[j] = grad_one_logp_only(kScaled ? x[j] * p.scale : x[j], g);
         if (i == t_vec) {
 #pragma unroll
             for (int j = 0; j < EPV; ++j)
