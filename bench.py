@@ -55,11 +55,19 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
 # each scaled by the counter's reading for a plain copy of known size
-# (profiles/klp_C2_bf16_hbm_traffic.md).  Keyed by workload, kernel and
+# (profiles/klp_all_configs_hbm_traffic.md).  Keyed by workload, kernel and
 # launch shape (waves, unroll, splits, flags); reported only for that shape.
 MEASURED_TRAFFIC = {
-    ("C2", "fwd", (4, 4, 1, 0)): 311769737,
-    ("C2", "bwd", (16, 2, 8, 1)): 623324882,
+    ("C1", "fwd", (16, 4, 1, 0)): 32960385,
+    ("C1", "bwd", (16, 2, 2, 1)): 65704365,
+    ("C2", "fwd", (4, 4, 1, 0)): 311758388,
+    ("C2", "bwd", (16, 2, 8, 1)): 623290575,
+    ("C3", "fwd", (4, 4, 1, 0)): 2103303576,
+    ("C3", "bwd", (16, 2, 4, 1)): 4205699665,
+    ("C4", "fwd", (4, 4, 1, 0)): 9964861906,
+    ("C4", "bwd", (16, 2, 8, 1)): 19926249858,
+    ("C5", "fwd", (4, 4, 1, 0)): 8592967390,
+    ("C5", "bwd", (16, 2, 8, 1)): 17183269982,
 }
 ROW_BLOCK = 256  # rows per seeded generator block
 

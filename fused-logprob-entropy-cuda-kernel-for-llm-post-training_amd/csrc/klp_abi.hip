@@ -48,8 +48,6 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 // workgroup per row still leaves the chip short of that.  Backward: splitting
 // needs no second pass; see default_bwd_config.
 constexpr int64_t kFwdTargetWaves = 4096;
-constexpr int64_t kBwdTargetBlocks = 8192;
-constexpr int kBwdMinSplits = 8;
 constexpr int kMaxSplits = 64;
 
 // Shared checks of the row-addressed logits operand.
@@ -125,13 +123,14 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     c.splits = 1;
     const int64_t nvec = body_vectors(dtype, vocab);
     const int64_t tile = static_cast<int64_t>(c.waves) * 64 * c.unroll;
-    // Up to 8 pieces per row whatever the batch: resident workgroups then
-    // cover a narrower address window, which measured faster for this mixed
-    // read/write stream (C4: 5.46 vs 5.13 TB/s).  Beyond 8, split only while
-    // the grid is short of kBwdTargetBlocks.
-    while (c.splits < kMaxSplits && nvec / (2 * c.splits) >= tile &&
-           (c.splits < kBwdMinSplits || n_rows * c.splits < kBwdTargetBlocks))
-        c.splits *= 2;
+    // Split a row into as many pieces as keep at least 15/16 of one
+    // iteration (`tile` vectors, 32 KB) per workgroup: short-lived
+    // workgroups of about one iteration each measured fastest for this mixed
+    // read/write stream, and pieces of less than an iteration leave lanes
+    // idle (C3: 8 pieces 665 us vs 4 pieces 729 us; C5: 32 pieces 2925 us vs
+    // 8 pieces 3099 us; C4 / C2 keep 8 pieces of 1.16 iterations).
+    (void)n_rows;
+    while (c.splits < kMaxSplits && nvec / (2 * c.splits) >= tile - tile / 16) c.splits *= 2;
     return c;
 }
 
