@@ -59,15 +59,15 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 # launch shape (waves, unroll, splits, flags); reported only for that shape.
 MEASURED_TRAFFIC = {
     ("C1", "fwd", (16, 4, 1, 0)): 32960385,
-    ("C1", "bwd", (16, 2, 2, 1)): 65704365,
+    ("C1", "bwd", (16, 2, 4, 1)): 65711874,
     ("C2", "fwd", (4, 4, 1, 0)): 311758388,
     ("C2", "bwd", (16, 2, 8, 1)): 623290575,
     ("C3", "fwd", (4, 4, 1, 0)): 2103303576,
-    ("C3", "bwd", (16, 2, 4, 1)): 4205699665,
+    ("C3", "bwd", (16, 2, 8, 1)): 4205676181,
     ("C4", "fwd", (4, 4, 1, 0)): 9964861906,
-    ("C4", "bwd", (16, 2, 8, 1)): 19926249858,
+    ("C4", "bwd", (16, 2, 10, 1)): 19926260879,
     ("C5", "fwd", (4, 4, 1, 0)): 8592967390,
-    ("C5", "bwd", (16, 2, 8, 1)): 17183269982,
+    ("C5", "bwd", (16, 2, 32, 1)): 17183261794,
 }
 ROW_BLOCK = 256  # rows per seeded generator block
 

@@ -48,6 +48,7 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 // workgroup per row still leaves the chip short of that.  Backward: splitting
 // needs no second pass; see default_bwd_config.
 constexpr int64_t kFwdTargetWaves = 4096;
+constexpr int64_t kBwdLargeGrid = 65536;
 constexpr int kMaxSplits = 64;
 
 // Shared checks of the row-addressed logits operand.
@@ -123,14 +124,22 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     c.splits = 1;
     const int64_t nvec = body_vectors(dtype, vocab);
     const int64_t tile = static_cast<int64_t>(c.waves) * 64 * c.unroll;
-    // Split a row into as many pieces as keep at least 15/16 of one
-    // iteration (`tile` vectors, 32 KB) per workgroup: short-lived
-    // workgroups of about one iteration each measured fastest for this mixed
-    // read/write stream, and pieces of less than an iteration leave lanes
-    // idle (C3: 8 pieces 665 us vs 4 pieces 729 us; C5: 32 pieces 2925 us vs
-    // 8 pieces 3099 us; C4 / C2 keep 8 pieces of 1.16 iterations).
-    (void)n_rows;
-    while (c.splits < kMaxSplits && nvec / (2 * c.splits) >= tile - tile / 16) c.splits *= 2;
+    // Pieces of at least 15/16 of one iteration (`tile` vectors, 32 KB),
+    // a power of two of them per row.  Short-lived workgroups of one to two
+    // iterations measured fastest for this mixed read/write stream (C3: 8
+    // pieces 665 us vs 4 pieces 729 us; C5: 32 pieces 2925 us vs 8 3099 us).
+    int64_t s = 1;
+    while (s < kMaxSplits && nvec / (2 * s) >= tile - tile / 16) s *= 2;
+    // Grids of many workgroups: the fewest pieces that keep every piece
+    // within one iteration (C4, 32768 rows: 10 pieces 3183 us vs 8 3356 us
+    // vs 12 3498 us).  On smaller grids that was slower (C2, 1024 rows: 10
+    // pieces 104.8-107.9 us vs 8 103.6-104.5 us).
+    if (n_rows * s >= kBwdLargeGrid) {
+        s = (nvec + tile - 1) / tile;
+        if (s > kMaxSplits) s = kMaxSplits;
+        if (s < 1) s = 1;
+    }
+    c.splits = static_cast<int>(s);
     return c;
 }
 
