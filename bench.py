@@ -385,6 +385,59 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
         u_fwd = timed(lambda: fused_logprob_entropy_forward(h @ w.T, t))
     f_fb = timed(lambda: fb(True))
     u_fb = timed(lambda: fb(False))
+
+    # GRPO on the head: the chunked LM head + fused step (library GEMMs and
+    # klp_grpo_step per chunk of tokens) against the unfused path (bf16
+    # matmul to the full logits, the logprob op, the GRPO loss, backward), at
+    # this token count and at 8x it.
+    from kernel_opt import fused_grpo_loss, fused_linear_grpo_step
+    kw = dict(eps_low=0.2, eps_high=0.28, loss_type="grpo")
+
+    def grpo_head(n_tok, chunks):
+        B, S = 4 * (n_tok // N), N // 4
+        hh = torch.randn(B, S, D, device=dev, generator=g).to(torch.bfloat16)
+        hh.requires_grad_(True)
+        tt = torch.randint(0, V, (B, S), device=dev, generator=g)
+        old = -torch.rand(B, S, device=dev, generator=g) * 8 - 4
+        adv = torch.randn(B, device=dev, generator=g)
+        mask = (torch.rand(B, S, device=dev, generator=g) < 0.9).float()
+
+        def run(chunk):
+            hh.grad = None
+            w.grad = None
+            if chunk:
+                loss, _, _ = fused_linear_grpo_step(hh, w, tt, old, adv, mask,
+                                                    chunk_tokens=chunk, **kw)
+            else:
+                lp, _, _ = fused_logprob_entropy(torch.matmul(hh, w.T), tt)
+                loss, _ = fused_grpo_loss(lp, old, adv, mask, **kw)
+            loss.backward()
+
+        def peak_extra(chunk):
+            """Peak memory above inputs and weights during one loss +
+            backward, the new gradients included."""
+            run(chunk)
+            hh.grad = None
+            w.grad = None
+            torch.cuda.synchronize()
+            base = torch.cuda.memory_allocated()
+            torch.cuda.reset_peak_memory_stats()
+            run(chunk)
+            torch.cuda.synchronize()
+            return round((torch.cuda.max_memory_allocated() - base) / 2 ** 20, 1)
+
+        out = {"tokens": n_tok}
+        for chunk in [0] + chunks:
+            name = f"chunked_{chunk}" if chunk else "unfused"
+            out[name + "_fwd_bwd_ms"] = round(timed(lambda: run(chunk)), 4)
+            out[name + "_peak_extra_mib"] = peak_extra(chunk)
+        hh.grad = None
+        w.grad = None
+        return out
+
+    grpo_heads = [grpo_head(N, [N, N // 4]), grpo_head(8 * N, [2 * N])]
+    torch.cuda.empty_cache()
+
     flops = 2 * N * V * D
     out = {"shape": {"tokens": N, "vocab": V, "hidden": D}, "dtype": "bf16 in, fp32 accumulate",
            "fused_fwd_ms": round(f_fwd, 4), "unfused_fwd_ms": round(u_fwd, 4),
@@ -394,7 +447,14 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
                             "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                             "frac": round(flops / (f_fwd * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
                                           4)},
-           "note": "unfused = bf16 library matmul to [N, V] logits, then klp_fwd / klp_bwd"}
+           "note": "unfused = bf16 library matmul to [N, V] logits, then klp_fwd / klp_bwd",
+           "grpo_step": {
+               "runs": grpo_heads,
+               "note": "fused_linear_grpo_step (chunks of the given token count: library "
+                       "GEMMs + klp_grpo_step, d_hidden / d_weight computed in the forward) "
+                       "against matmul + fused_logprob_entropy + fused_grpo_loss + backward; "
+                       "loss + backward per iteration; peak memory above inputs and weights "
+                       "during one iteration, the new gradients included"}}
     del h, w
     torch.cuda.empty_cache()
     return out

@@ -12,6 +12,7 @@ from .ops import (  # noqa: F401
 )
 from .grpo import fused_grpo_loss  # noqa: F401
 from .grpo_step import fused_grpo_step  # noqa: F401
+from .linear_grpo import fused_linear_grpo_step  # noqa: F401
 from .lmhead import (  # noqa: F401
     fused_linear_logprob_entropy,
     fused_linear_logprob_entropy_forward,
