@@ -342,6 +342,72 @@ def grpo_step_timing(dev, K, logits, targets):
                     "twice); both kernel time through the C ABI, outputs preallocated"}
 
 
+def shard_timing(dev, K, N=32768, V=151936, P=8):
+    """One rank's share of C4 under an 8-way vocab-parallel LM head: the
+    shard forward (klp_fwd_shard, [N, V/P] bf16 -> 16-byte row states), the
+    merge of P states (klp_fwd_shard_merge) and the shard backward (klp_bwd
+    with shard-relative targets), through the C ABI with preallocated
+    outputs.  The all-gather of the states between them is not part of this
+    single-GPU build (16 bytes per row: 512 KB per rank at C4)."""
+    import ctypes
+    from kernel_opt import _C
+    from kernel_opt._library import DTYPE_CODES, check_status, lib
+    sv = -(-V // P)
+    rank = 3
+    g = torch.Generator(device=dev).manual_seed(4)
+    x = (torch.randn(N, sv, generator=g, device=dev) * 2.5).to(torch.bfloat16)
+    t = torch.randint(0, V, (N,), generator=g, device=dev)
+    state = torch.empty(N, 4, dtype=torch.float32, device=dev)
+    states = torch.empty(P, N, 4, dtype=torch.float32, device=dev)
+    lp, ent, lse = (torch.empty(N, dtype=torch.float32, device=dev) for _ in range(3))
+    gl = torch.full((N,), -1.0 / N, device=dev)
+    d = torch.empty_like(x)
+    t_local = (t - rank * sv).contiguous()
+    rows = _C.row_layout(x)
+    P_ = lambda z: ctypes.c_void_p(z.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def fwd():
+        check_status(lib.klp_fwd_shard(P_(x), DTYPE_CODES[x.dtype], N, sv, *rows, P_(t),
+                                       rank * sv, 1.0, P_(state), st))
+
+    def merge():
+        check_status(lib.klp_fwd_shard_merge(P_(states), P, N, P_(t), sv, V, P_(lp), P_(ent),
+                                             P_(lse), st))
+
+    def bwd():
+        _C.bwd_launch(x, t_local, lse, ent, gl, None, None, d)
+
+    fwd()
+    for k in range(P):
+        states[k].copy_(state)
+    res = {}
+    for name, fn in (("fwd", fwd), ("merge", merge), ("bwd", bwd)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(K):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        res[name] = a.elapsed_time(b) / K * 1e3
+    fb = N * sv * 2 + 8 * N + 16 * N
+    bb = 2 * N * sv * 2 + 8 * N + 12 * N
+    out = {"shape": {"rows": N, "vocab": V, "shards": P, "shard_columns": sv, "dtype": "bf16"},
+           "shard_fwd_us": round(res["fwd"], 2), "merge_us": round(res["merge"], 2),
+           "shard_bwd_us": round(res["bwd"], 2),
+           "shard_fwd_tbps": round(fb / (res["fwd"] * 1e-6) / 1e12, 4),
+           "shard_bwd_tbps": round(bb / (res["bwd"] * 1e-6) / 1e12, 4),
+           "note": "per-rank kernels of an 8-way vocab-parallel C4; the exchange of the "
+                   "16-byte row states is outside this single-GPU build"}
+    del x, d
+    torch.cuda.empty_cache()
+    return out
+
+
 def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
     """The fused LM head (hidden @ weight^T folded into the logprob/entropy
     reduction, klp_lmh_*) against the unfused path (a bf16 library matmul,
@@ -478,6 +544,9 @@ def main(argv=None):
     ap.add_argument("--bwd-config", default=None, help="waves,unroll,splits,flags")
     ap.add_argument("--no-lmhead", action="store_true",
                     help="skip the fused LM-head timing (klp_lmh_* against matmul + logprob)")
+    ap.add_argument("--no-shard", action="store_true",
+                    help="skip the vocab-shard timing (one rank's share of C4 under 8-way "
+                         "vocab parallelism)")
     ap.add_argument("--no-grpo", action="store_true",
                     help="skip the GRPO timings (the loss kernels against the eager chain, "
                          "the fused step against the unfused kernels)")
@@ -604,6 +673,7 @@ def main(argv=None):
     grpo = None if args.no_grpo else grpo_timing(dev, K)
     step = None if args.no_grpo else grpo_step_timing(dev, K, logits, targets)
     lmhead = None if args.no_lmhead else lmhead_timing(dev)
+    shard = None if args.no_shard else shard_timing(dev, K)
 
     B, S, _ = cfg["shape"]
     fwd_used = fcfg or _C.default_config("fwd", logits.dtype, N, V)
@@ -654,6 +724,7 @@ def main(argv=None):
         "grpo_loss": grpo,
         "grpo_step": step,
         "lm_head": lmhead,
+        "vocab_shard": shard,
     }
     print(json.dumps(out))
     return 0

@@ -99,13 +99,22 @@ klp::FwdConfig default_fwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     c.unroll = 4;
     c.flags = 0;
     c.splits = 1;
-    if (n_rows * 4 >= kFwdTargetWaves) {
-        c.waves = 4;
+    const int64_t nvec = body_vectors(dtype, vocab);
+    // Up to 4 waves per row, fewer for short rows so that each thread keeps
+    // at least 8 vectors, and unroll 2 below 32 vectors per thread (bf16,
+    // measured: a vocab-parallel shard of C4, [32768, 18992]: 4 waves unroll
+    // 2 195 us vs unroll 4 206 us; [65536, 9496]: 2 waves 206 us vs 4 waves
+    // 272 us; [8192, 4096]: 1 wave 13.4 us vs 4 waves 24.4 us).  Rows that
+    // short take few threads whatever the batch.
+    int w = 4;
+    while (w > 1 && int64_t{w} * 64 * 8 > nvec) w /= 2;
+    if (n_rows * w >= kFwdTargetWaves || w < 4) {
+        c.waves = w;
+        if (nvec / (int64_t{w} * 64) < 32) c.unroll = 2;
     } else if (n_rows * 8 >= kFwdTargetWaves) {
         c.waves = 8;
     } else {
         c.waves = 16;
-        const int64_t nvec = body_vectors(dtype, vocab);
         const int64_t tile = static_cast<int64_t>(c.waves) * 64 * c.unroll;
         // Split while short of the wave target and every piece still keeps
         // each thread busy for at least two full iterations.
@@ -207,6 +216,8 @@ int fwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     p.splits = cfg.splits;
     p.partials = (cfg.splits > 1) ? static_cast<float*>(workspace) : nullptr;
     p.scale = scale;
+    p.target_offset = 0;
+    p.state = nullptr;
     if (injected_failure("forward")) return KLP_ELAUNCH;
     return after_launch(klp::launch_fwd(dtype, p, cfg, static_cast<hipStream_t>(stream)),
                         "forward");
@@ -501,6 +512,83 @@ int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp
     if (injected_failure("grpo backward")) return KLP_ELAUNCH;
     return after_launch(klp::launch_grpo_bwd(p, static_cast<hipStream_t>(stream)),
                         "grpo backward");
+}
+
+int klp_fwd_shard(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                  int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                  const int64_t* targets, int64_t vocab_offset, float temperature, float* state,
+                  void* stream) {
+    int rc = check_rows(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
+                        targets);
+    if (rc != KLP_OK) return rc;
+    float scale;
+    if (!scale_from_temperature(temperature, &scale)) return KLP_EINVAL;
+    if (vocab_offset < 0) return fail(KLP_EINVAL, "vocab_offset must be >= 0");
+    if (n_rows == 0) return ok();
+    if (state == nullptr || !aligned(state, 16))
+        return fail(KLP_EINVAL, "state must be non-null and 16-byte aligned");
+    // One workgroup per row (the states are per row, not per piece).
+    klp::FwdConfig cfg = default_fwd_config(dtype, n_rows, vocab);
+    if (cfg.splits > 1) {
+        cfg.waves = 16;
+        cfg.splits = 1;
+    }
+    if ((rc = check_grid(n_rows, 1, cfg.waves * 64)) != KLP_OK) return rc;
+    klp::FwdParams p;
+    p.logits = logits;
+    p.rm = klp::RowMap{rows_inner, stride_outer, stride_inner};
+    p.n_rows = n_rows;
+    p.vocab = vocab;
+    p.targets = targets;
+    p.logprob = nullptr;
+    p.entropy = nullptr;
+    p.lse = nullptr;
+    p.splits = 1;
+    p.partials = nullptr;
+    p.scale = scale;
+    p.target_offset = vocab_offset;
+    p.state = state;
+    if (injected_failure("shard forward")) return KLP_ELAUNCH;
+    return after_launch(klp::launch_fwd(dtype, p, cfg, static_cast<hipStream_t>(stream)),
+                        "shard forward");
+}
+
+int klp_fwd_shard_merge(const float* states, int64_t n_shards, int64_t n_rows,
+                        const int64_t* targets, int64_t shard_vocab, int64_t vocab,
+                        float* logprob, float* entropy, float* lse, void* stream) {
+    if (n_rows < 0) return fail(KLP_EINVAL, "n_rows must be >= 0");
+    if (n_shards < 1) return fail(KLP_EINVAL, "n_shards must be >= 1");
+    if (shard_vocab < 1 || vocab < 1 || vocab > n_shards * shard_vocab ||
+        vocab <= (n_shards - 1) * shard_vocab)
+        return fail(KLP_EINVAL,
+                    "vocab (%lld) must lie in ((n_shards - 1) * shard_vocab, n_shards * "
+                    "shard_vocab] (n_shards %lld, shard_vocab %lld)",
+                    static_cast<long long>(vocab), static_cast<long long>(n_shards),
+                    static_cast<long long>(shard_vocab));
+    if (n_rows == 0) return ok();
+    if (n_rows > (int64_t{1} << 31) - 1)
+        return fail(KLP_EINVAL, "n_rows above 2^31-1 is not supported");
+    if (states == nullptr || !aligned(states, 16))
+        return fail(KLP_EINVAL, "states must be non-null and 16-byte aligned");
+    if (targets == nullptr || !aligned(targets, 8))
+        return fail(KLP_EINVAL, "targets must be non-null and 8-byte aligned");
+    int rc;
+    if ((rc = check_f32(logprob, "logprob")) != KLP_OK) return rc;
+    if ((rc = check_f32(entropy, "entropy")) != KLP_OK) return rc;
+    if ((rc = check_f32(lse, "lse")) != KLP_OK) return rc;
+    klp::ShardMergeParams p;
+    p.states = states;
+    p.n_shards = n_shards;
+    p.n_rows = n_rows;
+    p.targets = targets;
+    p.shard_vocab = shard_vocab;
+    p.vocab = vocab;
+    p.logprob = logprob;
+    p.entropy = entropy;
+    p.lse = lse;
+    if (injected_failure("shard merge")) return KLP_ELAUNCH;
+    return after_launch(klp::launch_shard_merge(p, static_cast<hipStream_t>(stream)),
+                        "shard merge");
 }
 
 int64_t klp_grpo_step_max_vocab(int dtype) {

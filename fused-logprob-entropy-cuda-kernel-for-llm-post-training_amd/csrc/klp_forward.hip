@@ -102,7 +102,7 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     // split mode the combine kernel reads it instead.
     float x_target = 0.0f;
     if (!kSplit && tid == 0) {
-        const int64_t tgt = p.targets[row];
+        const int64_t tgt = p.targets[row] - p.target_offset;
         if (tgt >= 0 && tgt < vocab) x_target = to_f32<DT>(rp[tgt]) * p.scale;
     }
 
@@ -152,7 +152,34 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
         *slot = make_float4(r.m, r.z, r.t, 0.0f);
         return;
     }
+    if (p.state) {
+        // One vocabulary shard: the row's state, merged across shards by
+        // klp_fwd_shard_merge_kernel.
+        reinterpret_cast<float4*>(p.state)[row] = make_float4(r.m, r.z, r.t, x_target);
+        return;
+    }
     const RowOut o = finalize(r, x_target);
+    p.logprob[row] = o.logp;
+    p.entropy[row] = o.ent;
+    p.lse[row] = o.lse;
+}
+
+// Merge of the row states of `n_shards` vocabulary shards, one thread per row,
+// in shard order (the split-row combine across shards): the target logit comes
+// from the shard that holds the target.
+__global__ __launch_bounds__(256) void klp_fwd_shard_merge_kernel(ShardMergeParams p) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (row >= p.n_rows) return;
+    const float4* st = reinterpret_cast<const float4*>(p.states);
+    Stat acc = stat_empty();
+    for (int64_t k = 0; k < p.n_shards; ++k) {
+        const float4 q = st[k * p.n_rows + row];
+        acc = combine(acc, Stat{q.x, q.y, q.z});
+    }
+    const int64_t tgt = p.targets[row];
+    float x_target = 0.0f;
+    if (tgt >= 0 && tgt < p.vocab) x_target = st[(tgt / p.shard_vocab) * p.n_rows + row].w;
+    const RowOut o = finalize(acc, x_target);
     p.logprob[row] = o.logp;
     p.entropy[row] = o.ent;
     p.lse[row] = o.lse;
@@ -238,6 +265,10 @@ static hipError_t launch_fwd_dt(const FwdParams& p, const FwdConfig& c, hipStrea
     if (c.waves == W && c.unroll == U)                                         \
         return scaled ? launch_fwd_t<DT, W, U, true>(p, stream)                \
                       : launch_fwd_t<DT, W, U, false>(p, stream);
+    KLP_FWD_CASE(1, 2)
+    KLP_FWD_CASE(1, 4)
+    KLP_FWD_CASE(2, 2)
+    KLP_FWD_CASE(2, 4)
     KLP_FWD_CASE(4, 2)
     KLP_FWD_CASE(4, 4)
     KLP_FWD_CASE(8, 2)
@@ -246,6 +277,11 @@ static hipError_t launch_fwd_dt(const FwdParams& p, const FwdConfig& c, hipStrea
     KLP_FWD_CASE(16, 4)
 #undef KLP_FWD_CASE
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_shard_merge(const ShardMergeParams& p, hipStream_t stream) {
+    return launch_kernel(klp_fwd_shard_merge_kernel,
+                         dim3(static_cast<unsigned>((p.n_rows + 255) / 256)), dim3(256), stream, p);
 }
 
 hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream) {
@@ -258,7 +294,8 @@ hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStre
 }
 
 bool fwd_config_supported(const FwdConfig& c) {
-    const bool w = (c.waves == 4 || c.waves == 8 || c.waves == 16);
+    const bool w = (c.waves == 1 || c.waves == 2 || c.waves == 4 || c.waves == 8 ||
+                    c.waves == 16);
     const bool u = (c.unroll == 2 || c.unroll == 4);
     return w && u;
 }

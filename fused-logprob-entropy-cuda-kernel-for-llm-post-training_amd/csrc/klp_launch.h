@@ -22,6 +22,25 @@ struct FwdParams {
     float* partials;  // [n_rows * splits] float4 (m, z, t, unused) when splits > 1
     int splits;
     float scale;      // 1 / temperature; logits are multiplied by it on load
+    // Vocabulary shards (splits == 1 only): the row holds columns
+    // [target_offset, target_offset + vocab) of the full vocabulary, and with
+    // `state` non-null each row's float4 (m, z, t, target logit or 0) is
+    // written there instead of the outputs.
+    int64_t target_offset;
+    float* state;
+};
+
+// Merge of per-shard row states (klp_fwd_shard_merge).
+struct ShardMergeParams {
+    const float* states;     // [n_shards][n_rows] float4
+    int64_t n_shards;
+    int64_t n_rows;
+    const int64_t* targets;  // [n_rows], indices into the full vocabulary
+    int64_t shard_vocab;     // columns per shard (the last may hold fewer)
+    int64_t vocab;           // full vocabulary
+    float* logprob;
+    float* entropy;
+    float* lse;
 };
 
 struct NaiveParams {
@@ -160,6 +179,7 @@ hipError_t launch_lmh_fwd(const LmhParams& p, hipStream_t stream);
 hipError_t launch_lmh_dlogits(const LmhParams& p, hipStream_t stream);
 
 hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream);
+hipError_t launch_shard_merge(const ShardMergeParams& p, hipStream_t stream);
 hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream);
 hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, hipStream_t stream);
 hipError_t launch_grpo_fwd(const GrpoParams& p, hipStream_t stream);

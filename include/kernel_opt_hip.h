@@ -155,6 +155,36 @@ int klp_bwd_temp(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                  void* stream);
 
 /*
+ * Vocabulary shards (a vocab-parallel LM head: each rank holds columns
+ * [vocab_offset, vocab_offset + vocab) of the logits).  No counterpart in the
+ * reference, which has no multi-GPU path; these are the per-rank pieces of
+ * the sharded forward:
+ *   klp_fwd_shard writes, per row, the 16-byte online state of the row's
+ *     shard, float4 (max, sum-exp, sum-x-exp in the kernels' base-2 units,
+ *     target logit or 0), into `state` ([n_rows][4] float32, 16-byte
+ *     aligned).  `targets` index the full vocabulary; the target logit is
+ *     recorded by the shard that holds it.  Logits and temperature as
+ *     klp_fwd_temp.
+ *   klp_fwd_shard_merge merges the states of n_shards shards
+ *     (`states` = [n_shards][n_rows][4], shard k holding columns
+ *     [k * shard_vocab, min((k + 1) * shard_vocab, vocab))) in shard order
+ *     and writes logprob, entropy, lse as klp_fwd.
+ * Between the two, ranks exchange the 16-byte states (an all-gather); every
+ * rank then merges in the same order and holds identical outputs.  The
+ * backward needs no exchange: klp_bwd_temp on the shard, with the merged lse /
+ * entropy and targets shifted by -vocab_offset (a target outside the shard
+ * gets no one-hot term), writes the shard's d_logits.
+ */
+int klp_fwd_shard(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                  int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                  const int64_t* targets, int64_t vocab_offset, float temperature,
+                  float* state, void* stream);
+
+int klp_fwd_shard_merge(const float* states, int64_t n_shards, int64_t n_rows,
+                        const int64_t* targets, int64_t shard_vocab, int64_t vocab,
+                        float* logprob, float* entropy, float* lse, void* stream);
+
+/*
  * GRPO policy loss over per-token log-probabilities.  The reference plans it
  * as kernel "K2 fused_grpo_loss" (notes/PLAN.md:59) but ships it only as
  * eager PyTorch (examples/compare_one_step.py:232-236, the clipped surrogate

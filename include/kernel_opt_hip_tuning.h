@@ -9,8 +9,9 @@
  * not depend on the launch shape beyond fp32 rounding of the reduction order.
  *
  * Conventions are those of kernel_opt_hip.h.  Supported shapes:
- * waves in {4, 8, 16} (wave64s per workgroup), unroll in {2, 4} (16-byte
- * loads per thread per iteration), splits in [1, 1024] (workgroups per row).
+ * waves (wave64s per workgroup) in {1, 2, 4, 8, 16} for the forward and
+ * {4, 8, 16} for the backward, unroll in {2, 4} (16-byte loads per thread per
+ * iteration), splits in [1, 1024] (workgroups per row).
  * `flags` selects kernel variants: forward: must be 0; backward: bit 0 =
  * non-temporal gradient stores.
  */

@@ -284,3 +284,45 @@ def test_grpo_step_validation_errors():
         assert step() == KLP_ELAUNCH and "grpo step" in _err()
     finally:
         lib.klp_debug_fail_next_launches(0)
+
+
+def test_shard_validation_errors():
+    """klp_fwd_shard / klp_fwd_shard_merge reject bad arguments before any
+    launch; injected launch failures are reported."""
+    from kernel_opt._library import KLP_EDTYPE, KLP_EINVAL, KLP_ELAUNCH, lib
+    A = ctypes.c_void_p(0x100000)
+
+    def shard(**kw):
+        a = dict(x=A, dtype=0, n=8, v=1000, ri=8, so=0, si=1000, t=A, off=0, temp=1.0, st=A)
+        a.update(kw)
+        return lib.klp_fwd_shard(a["x"], a["dtype"], a["n"], a["v"], a["ri"], a["so"], a["si"],
+                                 a["t"], a["off"], a["temp"], a["st"], None)
+    assert shard(n=0) == 0
+    assert shard(dtype=7) == KLP_EDTYPE
+    assert shard(temp=-1.0) == KLP_EINVAL and "temperature" in _err()
+    assert shard(off=-1) == KLP_EINVAL and "vocab_offset" in _err()
+    assert shard(st=None) == KLP_EINVAL and "state" in _err()
+    assert shard(st=ctypes.c_void_p(0x100004)) == KLP_EINVAL and "state" in _err()
+    lib.klp_debug_fail_next_launches(1)
+    try:
+        assert shard() == KLP_ELAUNCH and "shard forward" in _err()
+    finally:
+        lib.klp_debug_fail_next_launches(0)
+
+    def merge(**kw):
+        a = dict(s=A, p=4, n=8, t=A, sv=250, v=1000, lp=A, ent=A, lse=A)
+        a.update(kw)
+        return lib.klp_fwd_shard_merge(a["s"], a["p"], a["n"], a["t"], a["sv"], a["v"], a["lp"],
+                                       a["ent"], a["lse"], None)
+    assert merge(n=0) == 0
+    assert merge(p=0) == KLP_EINVAL and "n_shards" in _err()
+    assert merge(v=1001) == KLP_EINVAL and "vocab" in _err()
+    assert merge(v=750) == KLP_EINVAL and "vocab" in _err()
+    assert merge(s=ctypes.c_void_p(0x100008)) == KLP_EINVAL and "states" in _err()
+    assert merge(t=None) == KLP_EINVAL and "targets" in _err()
+    assert merge(lse=None) == KLP_EINVAL and "lse" in _err()
+    lib.klp_debug_fail_next_launches(1)
+    try:
+        assert merge() == KLP_ELAUNCH and "shard merge" in _err()
+    finally:
+        lib.klp_debug_fail_next_launches(0)
