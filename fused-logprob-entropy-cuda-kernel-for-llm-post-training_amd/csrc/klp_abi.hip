@@ -132,6 +132,10 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     c.flags = klp::kFlagNtStore;
     c.splits = 1;
     const int64_t nvec = body_vectors(dtype, vocab);
+    // Rows shorter than one iteration of 16 waves take fewer waves (down to
+    // 4) rather than idle lanes (bf16 [65536, 9496]: 8 waves 403 us vs 16
+    // waves 485 us; [8192, 4096]: 4 waves 22.6 us vs 48.7 us).
+    while (c.waves > 4 && int64_t{c.waves} * 64 * c.unroll > nvec) c.waves /= 2;
     const int64_t tile = static_cast<int64_t>(c.waves) * 64 * c.unroll;
     // Pieces of at least 15/16 of one iteration (`tile` vectors, 32 KB),
     // a power of two of them per row.  Short-lived workgroups of one to two
@@ -140,13 +144,14 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     int64_t s = 1;
     while (s < kMaxSplits && nvec / (2 * s) >= tile - tile / 16) s *= 2;
     // Grids of many workgroups: the fewest pieces that keep every piece
-    // within one iteration (C4, 32768 rows: 10 pieces 3183 us vs 8 3356 us
-    // vs 12 3498 us).  On smaller grids that was slower (C2, 1024 rows: 10
-    // pieces 104.8-107.9 us vs 8 103.6-104.5 us).
+    // within one iteration, if each still fills 7/8 of it (C4, 32768 rows:
+    // 10 pieces of 0.93 iterations 3183 us vs 8 3356 us vs 12 3498 us).  On
+    // smaller grids that was slower (C2, 1024 rows: 10 pieces 104.8-107.9 us
+    // vs 8 103.6-104.5 us), and so were pieces far below one iteration.
     if (n_rows * s >= kBwdLargeGrid) {
-        s = (nvec + tile - 1) / tile;
-        if (s > kMaxSplits) s = kMaxSplits;
-        if (s < 1) s = 1;
+        int64_t e = (nvec + tile - 1) / tile;
+        if (e > kMaxSplits) e = kMaxSplits;
+        if (e >= 1 && nvec / e >= tile - tile / 8) s = e;
     }
     c.splits = static_cast<int>(s);
     return c;
