@@ -237,17 +237,24 @@ __device__ __forceinline__ Stat stat_shfl_xor(const Stat& s, int off) {
     return Stat{__shfl_xor(s.m, off, 64), __shfl_xor(s.z, off, 64), __shfl_xor(s.t, off, 64)};
 }
 
-// Merge the states of all 64 lanes; every lane returns the total.  combine()
-// is commutative bit for bit, so both lanes of a pair compute the same merge
-// and the result depends on nothing but the fixed pairing order: within a
-// row, lanes are paired by DPP quad_perm [1,0,3,2], quad_perm [2,3,0,1],
-// row_half_mirror and row_mirror (the partner always holds the other half of
-// the group merged so far); across rows by xor-16 and xor-32 shuffles.
-__device__ __forceinline__ Stat wave_reduce(Stat s) {
+// Merge the states of the 16 lanes of each DPP row; every lane of the row
+// returns the row's total.  combine() is commutative bit for bit, so both
+// lanes of a pair compute the same merge and the result depends on nothing
+// but the fixed pairing order: lanes are paired by DPP quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror and row_mirror (the partner always
+// holds the other half of the group merged so far).
+__device__ __forceinline__ Stat row_reduce(Stat s) {
     s = combine(s, stat_dpp<0xB1>(s));   // quad_perm [1, 0, 3, 2]
     s = combine(s, stat_dpp<0x4E>(s));   // quad_perm [2, 3, 0, 1]
     s = combine(s, stat_dpp<0x141>(s));  // row_half_mirror
     s = combine(s, stat_dpp<0x140>(s));  // row_mirror
+    return s;
+}
+
+// Merge the states of all 64 lanes; every lane returns the total: the four
+// rows by row_reduce, then across rows by xor-16 and xor-32 shuffles.
+__device__ __forceinline__ Stat wave_reduce(Stat s) {
+    s = row_reduce(s);
     s = combine(s, stat_shfl_xor(s, 16));
     s = combine(s, stat_shfl_xor(s, 32));
     return s;

@@ -16,13 +16,16 @@
 // bf16 row of V <= 155648 or an fp32 row of V <= 77824.
 //
 // Per workgroup (one row):
-//  1. load the row into registers (16-byte loads, non-temporal);
+//  1. load the row into registers (16-byte buffer loads, non-temporal);
 //  2. per-thread online (m, z, t) state (absorb(), as klp_fwd), the wave
-//     reduction and the 16 waves in order through LDS;
+//     reduction, and the 16 wave states through LDS, merged by wave 0 with
+//     one DPP row reduction;
 //  3. logprob, entropy, lse of the row; the GRPO terms of the token
-//     (grpo_token_loss, shared with klp_grpo.hip); loss_tok = w_t * loss_t;
+//     (grpo_token_loss, shared with klp_grpo.hip; its inputs read at the
+//     start); loss_tok = w_t * loss_t;
 //  4. d_logits from the registers (klp_bwd's gradient, which with g_ent = 0
-//     is p * (-g_logp) plus the one-hot term), non-temporal 16-byte stores.
+//     is p * (-g_logp) plus the one-hot term), non-temporal 16-byte buffer
+//     stores.
 // Rows too long for the registers, or whose start or length is not a whole
 // number of 16-byte vectors, are rejected by the caller (KLP_EINVAL), which
 // then runs the unfused kernels.
@@ -35,6 +38,15 @@ namespace {
 
 constexpr int kStepThreads = kGrpoStepThreads;
 constexpr int kStepWaves = kStepThreads / 64;
+constexpr int kCachePolicyNt = 2;  // the "nt" (non-temporal) cache-policy bit
+
+// Raw buffer resource over one row of `bytes` bytes: lanes past the end read
+// 0 without touching memory, and their stores are dropped.  Word 3
+// (0x00020000) is the gfx9-family descriptor default for dword data.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                             static_cast<int>(bytes), 0x00020000);
+}
 
 }  // namespace
 
@@ -47,29 +59,38 @@ __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_kernel(GrpoStepPar
     const int wave = tid >> 6;
     const int64_t row = blockIdx.x;
     const elem* rp = static_cast<const elem*>(p.logits) + row_offset(p.rm, row);
-    // Vector k of this thread is the row's vector tid + k * kStepThreads.
-    // Addresses are the workgroup-uniform row start plus a 32-bit byte
-    // offset, so the compiler keeps one 64-bit base in scalar registers
-    // instead of a 64-bit address per vector in vector registers.
-    const char* rbase = reinterpret_cast<const char*>(rp);
     const uint32_t nvec = static_cast<uint32_t>(p.vocab / EPV);
+    const uint32_t row_bytes = nvec * 16u;
     // Vectors k < n_full exist for every thread; vector n_full only for some.
     const int n_full = static_cast<int>(nvec / kStepThreads);
+    const bool has_tail = static_cast<uint32_t>(tid) < nvec - n_full * kStepThreads;
+    const uint32_t pad = Traits<DT>::kNegInfWord;
 
+    // Vector k of this thread is the row's vector tid + k * kStepThreads.
+    // Every load is issued, unconditionally: a load skipped on some path
+    // leaves the number of loads in flight unknown, and the compiler then
+    // waits for all of them before the first use (no overlap of the scan
+    // with the row's arrival).  Past the row's end the buffer descriptor
+    // returns zeros without a memory access.
+    const __amdgpu_buffer_rsrc_t rs = row_rsrc(rp, row_bytes);
+    // The loads are issued in the order the scan uses them (the scheduling
+    // fences keep them so).
     u32x4 r[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const uint32_t i = tid + k * kStepThreads;
-        const uint32_t w = Traits<DT>::kNegInfWord;
-        r[k] = (i < nvec) ? load16<true>(reinterpret_cast<const u32x4*>(rbase + i * 16u))
-                          : u32x4{w, w, w, w};
+        r[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, (tid + k * kStepThreads) * 16, 0,
+                                                     kCachePolicyNt);
+        __builtin_amdgcn_sched_barrier(0);
     }
     const int64_t tgt = p.targets[row];
     const bool has_t = tgt >= 0 && tgt < p.vocab;
-    // The target logit is read directly, as in klp_fwd; issued early so that
-    // its latency hides behind the scan.
-    float x_target = 0.0f;
-    if (tid == 0 && has_t) x_target = to_f32<DT>(rp[tgt]) * p.scale;
+    // The token's GRPO inputs, read now: their latency hides behind the
+    // row's loads instead of stalling the workgroup after the reduction.
+    const float wt = p.tok_weight[row];
+    const float old_lp = p.old_logp[row];
+    const float adv = p.adv[p.adv_per_token ? row : row / p.seq_len];
+    const bool has_ref = p.ref_logp != nullptr && p.beta != 0.0f;
+    const float ref_lp = has_ref ? p.ref_logp[row] : 0.0f;
 
     // Pass 1 over the registers.  A lane whose own values include -inf
     // redoes its scan with -inf excluded (the reference's sentinel rule,
@@ -80,8 +101,13 @@ __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_kernel(GrpoStepPar
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             if (k > n_full) break;
+            // Vector k's work stays after vector k-1's: hoisting any of it
+            // (the select below, say) makes the first wait one for the
+            // whole row.
+            __builtin_amdgcn_sched_barrier(0);
             float x[EPV];
-            unpack<DT>(r[k], x);
+            // Lanes past the row's end in vector n_full read zeros: -inf.
+            unpack<DT>((k < n_full || has_tail) ? r[k] : u32x4{pad, pad, pad, pad}, x);
             if (kScaled) {
 #pragma unroll
                 for (int j = 0; j < EPV; ++j) x[j] *= p.scale;
@@ -94,45 +120,71 @@ __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_kernel(GrpoStepPar
     Stat s = scan(std::false_type{});
     if (needs_clamped_rescan(s)) s = scan(std::true_type{});
 
+    // The target logit comes from the registers: the thread holding it
+    // publishes it (a global load issued after the row's loads would make
+    // every wave wait for the whole row before its scan).
     __shared__ Stat wave_stat[kStepWaves];
+    __shared__ float target_logit;
     __shared__ float row_vals[3];  // lse, entropy, g_logp
+    if (has_t) {
+        const int64_t tv = tgt / EPV;
+        if (static_cast<int>(tv % kStepThreads) == tid) {
+            const int kt = static_cast<int>(tv / kStepThreads);
+            const int jt = static_cast<int>(tgt - tv * EPV);
+            float xt = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                if (k == kt) {
+                    float x[EPV];
+                    unpack<DT>(r[k], x);
+#pragma unroll
+                    for (int j = 0; j < EPV; ++j)
+                        if (j == jt) xt = x[j];
+                }
+            }
+            target_logit = kScaled ? xt * p.scale : xt;
+        }
+    }
     s = wave_reduce(s);
     if (lane == 0) wave_stat[wave] = s;
     __syncthreads();
-    if (tid == 0) {
-        Stat acc = wave_stat[0];
-#pragma unroll
-        for (int w = 1; w < kStepWaves; ++w) acc = combine(acc, wave_stat[w]);
-        const RowOut o = finalize(acc, x_target);
+    // Wave 0 merges the 16 wave states (each of its 16-lane DPP rows reads
+    // all of them and reduces them, every lane ending with the same bits),
+    // computes the row's results and the token's GRPO terms, and hands the
+    // backward's constants to the other waves through LDS.
+    static_assert(kStepWaves == 16, "one wave state per lane of a DPP row");
+    if (wave == 0) {
+        const RowOut o =
+            finalize(row_reduce(wave_stat[lane & 15]), has_t ? target_logit : 0.0f);
         // GRPO terms of this token (token-level importance weight).
-        const float wt = p.tok_weight[row];
-        const int64_t b = row / p.seq_len;
-        const float adv = p.adv_per_token ? p.adv[row] : p.adv[b];
-        const bool has_ref = p.ref_logp != nullptr && p.beta != 0.0f;
-        const TokenLoss tl = grpo_token_loss(p.eps_low, p.eps_high, p.beta,
-                                             o.logp - p.old_logp[row], adv, o.logp,
-                                             has_ref ? p.ref_logp[row] : 0.0f, has_ref);
+        const TokenLoss tl =
+            grpo_token_loss(p.eps_low, p.eps_high, p.beta, o.logp - old_lp, adv, o.logp,
+                            ref_lp, has_ref);
         const float g_logp = wt * (tl.dw + tl.dlp);
-        p.logprob[row] = o.logp;
-        p.entropy[row] = o.ent;
-        if (p.lse) p.lse[row] = o.lse;
-        p.loss_tok[row] = wt * tl.loss;
-        row_vals[0] = o.lse;
-        row_vals[1] = o.ent;
-        row_vals[2] = g_logp;
+        if (lane == 0) {
+            p.logprob[row] = o.logp;
+            p.entropy[row] = o.ent;
+            if (p.lse) p.lse[row] = o.lse;
+            p.loss_tok[row] = wt * tl.loss;
+            row_vals[0] = o.lse;
+            row_vals[1] = o.ent;
+            row_vals[2] = g_logp;
+        }
     }
     __syncthreads();
 
     // Pass 2: d_logits from the registers.
     const RowGrad g = row_grad(row_vals[0], row_vals[1], row_vals[2], 0.0f, 0.0f);
-    char* dbase = reinterpret_cast<char*>(static_cast<elem*>(p.d_logits) + row * p.vocab);
+    // Stores past the row's end are dropped by the descriptor.
+    const __amdgpu_buffer_rsrc_t ds =
+        row_rsrc(static_cast<elem*>(p.d_logits) + row * p.vocab, row_bytes);
     // Vector index holding the target's one-hot term (or none).
     const uint32_t t_vec = has_t ? static_cast<uint32_t>(tgt / EPV) : 0xFFFFFFFFu;
     const int t_elem = has_t ? static_cast<int>(tgt % EPV) : 0;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const uint32_t i = tid + k * kStepThreads;
-        if (k > n_full || i >= nvec) break;
+        if (k > n_full) break;
         float x[EPV];
         unpack<DT>(r[k], x);
         // klp_bwd's gradient with g_ent = g_lse = 0 (grad_one_logp_only).
@@ -148,7 +200,7 @@ __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_kernel(GrpoStepPar
 #pragma unroll
             for (int j = 0; j < EPV; ++j) x[j] *= p.scale;
         }
-        __builtin_nontemporal_store(pack<DT>(x), reinterpret_cast<u32x4*>(dbase + i * 16u));
+        __builtin_amdgcn_raw_buffer_store_b128(pack<DT>(x), ds, i * 16u, 0, kCachePolicyNt);
     }
 }
 
