@@ -472,8 +472,9 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
             hh.grad = None
             w.grad = None
             if chunk:
-                loss, _, _ = fused_linear_grpo_step(hh, w, tt, old, adv, mask,
-                                                    chunk_tokens=chunk, **kw)
+                loss, _, _ = fused_linear_grpo_step(
+                    hh, w, tt, old, adv, mask,
+                    chunk_tokens=None if chunk == "default" else chunk, **kw)
             else:
                 lp, _, _ = fused_logprob_entropy(torch.matmul(hh, w.T), tt)
                 loss, _ = fused_grpo_loss(lp, old, adv, mask, **kw)
@@ -501,7 +502,9 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
         w.grad = None
         return out
 
-    grpo_heads = [grpo_head(N, [N, N // 4]), grpo_head(8 * N, [2 * N])]
+    # "default": fused_linear_grpo_step's own chunking (one chunk at 8 * N
+    # for this head).
+    grpo_heads = [grpo_head(N, [N, N // 4]), grpo_head(8 * N, ["default", 2 * N])]
     torch.cuda.empty_cache()
 
     flops = 2 * N * V * D
@@ -516,7 +519,8 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
            "note": "unfused = bf16 library matmul to [N, V] logits, then klp_fwd / klp_bwd",
            "grpo_step": {
                "runs": grpo_heads,
-               "note": "fused_linear_grpo_step (chunks of the given token count: library "
+               "note": "fused_linear_grpo_step (chunks of the given token count, 'default' "
+                       "its own chunking: library "
                        "GEMMs + klp_grpo_step, d_hidden / d_weight computed in the forward) "
                        "against matmul + fused_logprob_entropy + fused_grpo_loss + backward; "
                        "loss + backward per iteration; peak memory above inputs and weights "

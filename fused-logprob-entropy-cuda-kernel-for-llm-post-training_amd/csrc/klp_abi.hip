@@ -596,6 +596,28 @@ int klp_fwd_shard_merge(const float* states, int64_t n_shards, int64_t n_rows,
                         "shard merge");
 }
 
+int klp_scale_inplace(void* data, int dtype, int64_t n, const float* scale, void* stream) {
+    if (dtype != KLP_BF16 && dtype != KLP_FP16 && dtype != KLP_FP32)
+        return fail(KLP_EDTYPE, "dtype must be bf16, fp16, or fp32");
+    if (n < 0) return fail(KLP_EINVAL, "n must be >= 0");
+    if (n == 0) return ok();
+    const int esz = elem_bytes(dtype);
+    if (data == nullptr || !aligned(data, esz))
+        return fail(KLP_EINVAL, "data must be non-null and aligned to its element size");
+    if (scale == nullptr || !aligned(scale, 4))
+        return fail(KLP_EINVAL, "scale must be non-null and 4-byte aligned");
+    klp::ScaleParams p;
+    p.data = data;
+    p.n = n;
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(data);
+    p.head = static_cast<int64_t>(((16u - (addr & 15u)) & 15u) / esz);
+    if (p.head > n) p.head = n;
+    p.nvec = (n - p.head) / (16 / esz);
+    p.scale = scale;
+    if (injected_failure("scale")) return KLP_ELAUNCH;
+    return after_launch(klp::launch_scale(dtype, p, static_cast<hipStream_t>(stream)), "scale");
+}
+
 int64_t klp_grpo_step_max_vocab(int dtype) {
     if (dtype != KLP_BF16 && dtype != KLP_FP16 && dtype != KLP_FP32) return 0;
     return int64_t{klp::kGrpoStepMaxVec} * klp::kGrpoStepThreads * (16 / elem_bytes(dtype));

@@ -72,6 +72,10 @@ template <> __device__ __forceinline__ uint16_t from_f32<kBF16>(float x) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
 }
 template <> __device__ __forceinline__ uint16_t from_f32<kFP16>(float x) {
+    // The empty asm hides x's origin from instruction selection: a product
+    // rounded straight to fp16 would otherwise become v_fma_mixlo_f16 a, b, +0,
+    // which turns a -0 product into +0.
+    asm("" : "+v"(x));
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
 template <> __device__ __forceinline__ uint32_t from_f32<kFP32>(float x) {

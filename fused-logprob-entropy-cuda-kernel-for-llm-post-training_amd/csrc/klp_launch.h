@@ -145,6 +145,19 @@ constexpr int kGrpoStepMaxVec = 19;
 constexpr int kGrpoStepThreads = 1024;
 hipError_t launch_grpo_step(int dtype, const GrpoStepParams& p, hipStream_t stream);
 
+// In-place scaling by a device scalar (klp_scale_inplace): elements
+// [0, head) and [head + nvec * per-vector, n) one by one, the nvec 16-byte
+// vectors from element `head` (16-byte aligned) in between.
+struct ScaleParams {
+    void* data;
+    int64_t n;
+    int64_t head;
+    int64_t nvec;
+    const float* scale;
+};
+
+hipError_t launch_scale(int dtype, const ScaleParams& p, hipStream_t stream);
+
 // Fused LM head forward (klp_lmhead.hip).
 struct LmhParams {
     const uint16_t* hidden;  // bf16 [n_tokens, ld_hidden], first `dim` columns used

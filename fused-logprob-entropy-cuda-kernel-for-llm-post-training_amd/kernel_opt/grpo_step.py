@@ -113,6 +113,22 @@ def grpo_step_launch(logits, targets, old, ref, adv, weight, params):
     return logp, ent, lse, loss_tok, d_logits
 
 
+def scale_by_upstream(t: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """``t *= g`` in place (``t`` contiguous, ``g`` a one-element tensor on
+    ``t``'s device) without reading ``g`` on the host: klp_scale_inplace reads
+    it on the device, multiplies in float32 and rounds once to ``t``'s dtype
+    (as ``t * float(g)`` would), and writes nothing when ``g == 1``."""
+    if not t.is_contiguous():
+        raise RuntimeError("scale_by_upstream needs a contiguous tensor")
+    g32 = g.detach().to(device=t.device, dtype=torch.float32).reshape(1).contiguous()
+    with torch.cuda.device(t.device):
+        stream = torch.cuda.current_stream(t.device).cuda_stream
+        rc = lib.klp_scale_inplace(_ptr(t), DTYPE_CODES[t.dtype], t.numel(), _ptr(g32),
+                                   ctypes.c_void_p(stream))
+    check_status(rc)
+    return t
+
+
 class _FusedGrpoStep(torch.autograd.Function):
 
     @staticmethod
@@ -132,13 +148,9 @@ class _FusedGrpoStep(torch.autograd.Function):
         ctx.d_logits = None
         if g_loss is None or not ctx.needs_input_grad[0]:
             return None, None, None, None, None, None, None
-        g = float(g_loss)
-        if g != 1.0:
-            # A Python scalar: torch multiplies in float32 with fp32(g) and
-            # rounds once to d's dtype (a 0-dim device tensor would first be
-            # cast to d's dtype).
-            d = d * g
-        return d, None, None, None, None, None, None
+        # The upstream gradient stays on the device (no host synchronisation);
+        # exactly 1 leaves d as it is.
+        return scale_by_upstream(d, g_loss), None, None, None, None, None, None
 
 
 def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch.Tensor,

@@ -31,12 +31,26 @@ import torch
 
 from ._library import DTYPE_CODES, lib
 from .grpo import fused_grpo_loss
-from .grpo_step import grpo_step_launch, grpo_token_weights
+from .grpo_step import grpo_step_launch, grpo_token_weights, scale_by_upstream
 from .ops import fused_logprob_entropy
 
 __all__ = ["fused_linear_grpo_step"]
 
-DEFAULT_CHUNK_TOKENS = 4096
+# Default chunking: each [chunk, V] buffer (a chunk's logits, then its
+# d_logits) is held to about this many bytes, and the tokens are split into
+# the fewest chunks that respect it, of equal size.  Fewer, larger chunks keep
+# the library GEMMs efficient and skip the float32 d_weight accumulator
+# entirely when one chunk suffices; 4 GiB per buffer is small beside 288 GB of
+# HBM.
+DEFAULT_CHUNK_BYTES = 4 << 30
+
+
+def default_chunk_tokens(n_tokens: int, vocab: int, elem_bytes: int) -> int:
+    """Tokens per chunk for the default: the fewest equal chunks whose
+    [chunk, vocab] buffers stay within DEFAULT_CHUNK_BYTES."""
+    max_tok = max(1, DEFAULT_CHUNK_BYTES // max(1, vocab * elem_bytes))
+    n_chunks = max(1, -(-n_tokens // max_tok))
+    return max(1, -(-n_tokens // n_chunks))
 
 
 def _accumulate_f32(acc, a, b):
@@ -114,13 +128,12 @@ class _FusedLinearGrpoStep(torch.autograd.Function):
         d_hidden, d_weight = grads
         if g_loss is None:
             return (None,) * 9
-        g = float(g_loss)
-        if g != 1.0:
-            # Python scalar: multiplied in float32, one rounding to the dtype.
-            d_hidden = None if d_hidden is None else d_hidden * g
-            d_weight = None if d_weight is None else d_weight * g
+        # The upstream gradient stays on the device (no host synchronisation):
+        # multiplied in float32, one rounding to the dtype; 1 writes nothing.
         if d_hidden is not None:
-            d_hidden = d_hidden.view(ctx.hidden_shape)
+            d_hidden = scale_by_upstream(d_hidden, g_loss).view(ctx.hidden_shape)
+        if d_weight is not None:
+            scale_by_upstream(d_weight, g_loss)
         return d_hidden, d_weight, None, None, None, None, None, None, None
 
 
@@ -150,10 +163,12 @@ def fused_linear_grpo_step(hidden: torch.Tensor, weight: torch.Tensor, targets: 
         old_logp, advantages, mask, ref_logp and the loss keywords: as
             :func:`kernel_opt.fused_grpo_loss`; ``temperature`` divides the
             logits.
-        chunk_tokens: tokens per chunk (default 4096); peak extra memory is
-            about ``2 * chunk_tokens * V`` elements, plus a float32 ``[V, D]``
+        chunk_tokens: tokens per chunk.  Peak extra memory is about
+            ``2 * chunk_tokens * V`` elements, plus a float32 ``[V, D]``
             accumulator for ``d_weight`` when there is more than one chunk.
-            Smaller chunks cost GEMM efficiency.
+            Smaller chunks cost GEMM efficiency.  Default: the fewest equal
+            chunks whose ``[chunk, V]`` buffers stay within 4 GiB
+            (:data:`DEFAULT_CHUNK_BYTES`).
 
     Returns ``(loss, logp, entropy)`` (``+ stats`` with ``return_stats``);
     ``logp`` and ``entropy`` are float32 ``[B, S]`` constants.
@@ -174,10 +189,11 @@ def fused_linear_grpo_step(hidden: torch.Tensor, weight: torch.Tensor, targets: 
     T = 1.0 if temperature is None else float(temperature)
     if not (T > 0.0 and T != float("inf")):
         raise RuntimeError(f"temperature must be finite and > 0, got {T}")
-    chunk = DEFAULT_CHUNK_TOKENS if chunk_tokens is None else int(chunk_tokens)
+    V = weight.size(0)
+    chunk = (default_chunk_tokens(B * S, V, hidden.element_size()) if chunk_tokens is None
+             else int(chunk_tokens))
     if chunk < 1:
         raise ValueError("chunk_tokens must be >= 1")
-    V = weight.size(0)
     loss_kw = dict(eps_low=eps_low, eps_high=eps_high, beta=beta, loss_type=loss_type,
                    importance_level=importance_level,
                    max_completion_length=max_completion_length, normalizer=normalizer)

@@ -287,6 +287,18 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                   void* d_logits, void* stream);
 
 /*
+ * data[i] *= *scale for i in [0, n), in place, on the stream: each element is
+ * multiplied in fp32 and rounded once to `dtype` (RNE), as torch's
+ * `tensor * float` computes it.  `scale` is a device pointer read by the
+ * kernel; when *scale == 1 nothing is written.  No counterpart in the
+ * reference.  It is for gradients computed in the forward (klp_grpo_step's
+ * d_logits; the chunked LM head's d_hidden and d_weight), whose backward only
+ * applies the loss's upstream gradient: kept on the device, that scalar needs
+ * no host synchronisation.  data aligned to its element size, n >= 0.
+ */
+int klp_scale_inplace(void* data, int dtype, int64_t n, const float* scale, void* stream);
+
+/*
  * Fused LM head + per-token logprob / entropy, forward.  No counterpart in the
  * reference, which names it as its follow-up (a Liger-style fused linear +
  * loss, docs/FINAL_REPORT.md:439-450): instead of logits = hidden @ weight^T

@@ -326,3 +326,29 @@ def test_shard_validation_errors():
         assert merge() == KLP_ELAUNCH and "shard merge" in _err()
     finally:
         lib.klp_debug_fail_next_launches(0)
+
+
+def test_scale_inplace_validation_errors():
+    """klp_scale_inplace rejects bad arguments before any launch; n = 0 is a
+    no-op; an injected launch failure is reported."""
+    from kernel_opt._library import KLP_EDTYPE, KLP_EINVAL, KLP_ELAUNCH, lib
+    A = ctypes.c_void_p(0x100000)
+
+    def scale(**kw):
+        a = dict(d=A, dtype=0, n=100, s=A)
+        a.update(kw)
+        return lib.klp_scale_inplace(a["d"], a["dtype"], a["n"], a["s"], None)
+    assert scale(n=0) == 0
+    assert scale(n=0, d=None, s=None) == 0
+    assert scale(dtype=3) == KLP_EDTYPE
+    assert scale(n=-1) == KLP_EINVAL and "n must" in _err()
+    assert scale(d=None) == KLP_EINVAL and "data" in _err()
+    assert scale(d=ctypes.c_void_p(0x100001)) == KLP_EINVAL and "data" in _err()
+    assert scale(dtype=2, d=ctypes.c_void_p(0x100002)) == KLP_EINVAL and "data" in _err()
+    assert scale(s=None) == KLP_EINVAL and "scale" in _err()
+    assert scale(s=ctypes.c_void_p(0x100002)) == KLP_EINVAL and "scale" in _err()
+    lib.klp_debug_fail_next_launches(1)
+    try:
+        assert scale() == KLP_ELAUNCH and "scale" in _err()
+    finally:
+        lib.klp_debug_fail_next_launches(0)

@@ -126,3 +126,24 @@ def test_token_weights_match_oracle(loss_type):
     e = token_weights(mask, B, S, kind, norm)
     np.testing.assert_allclose(w, e, rtol=2 ** -23, atol=0)
     assert np.all(w[1] == 0.0)
+
+
+def test_default_chunk_tokens():
+    """fused_linear_grpo_step's default chunking: the fewest chunks whose
+    [chunk, V] buffers fit DEFAULT_CHUNK_BYTES, of equal size (the last one
+    at most n_chunks - 1 tokens shorter), covering every token."""
+    from kernel_opt.linear_grpo import DEFAULT_CHUNK_BYTES, default_chunk_tokens
+    assert default_chunk_tokens(8192, 152064, 2) == 8192           # one chunk
+    assert default_chunk_tokens(32768, 152064, 2) == 10923         # 3 chunks (14122 max)
+    assert default_chunk_tokens(1, 152064, 4) == 1
+    rng = np.random.default_rng(0)
+    for _ in range(2000):
+        n = int(rng.integers(1, 1 << 20))
+        v = int(rng.integers(1, 1 << 19))
+        esz = int(rng.choice([2, 4]))
+        c = default_chunk_tokens(n, v, esz)
+        k = -(-n // c)  # chunks used
+        max_tok = max(1, DEFAULT_CHUNK_BYTES // (v * esz))
+        assert 1 <= c <= max(1, min(n, max_tok))
+        assert k == -(-n // max_tok)                   # fewest chunks that fit
+        assert n - (k - 1) * c >= c - (k - 1)          # balanced: short last chunk by < k

@@ -214,6 +214,31 @@ def test_autograd_op():
     assert torch.equal(xg2.grad, (d.float() * torch.tensor(0.3, device=DEV)).to(d.dtype))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_scale_by_upstream(dtype):
+    """klp_scale_inplace (through scale_by_upstream), which applies the loss's
+    upstream gradient without reading it on the host: t * g multiplied in
+    float32 and rounded once, bit for bit as torch's t.float() * g; g == 1
+    leaves the bits untouched; every alignment of start and length (the
+    kernel's scalar head and tail), and nothing outside the view is written."""
+    from kernel_opt.grpo_step import scale_by_upstream
+    gen = torch.Generator().manual_seed(21)
+    base = (torch.randn(1 << 20, generator=gen) * 3).to(dtype).to(DEV)
+    bits = {torch.float32: torch.int32}.get(dtype, torch.int16)
+    for off, n in ((0, 0), (0, 1), (1, 7), (3, 8), (0, 4097), (5, (1 << 20) - 9),
+                   (0, 1 << 20)):
+        for sc in (0.3, -2.5, 0.0, 1.0):
+            print(f"scale: dtype={dtype} off={off} n={n} g={sc}", flush=True)
+            buf = base.clone()
+            view = buf[off:off + n]
+            scale_by_upstream(view, torch.tensor(sc, device=DEV))
+            src = base[off:off + n]
+            exp = src if sc == 1.0 else (src.float() * sc).to(dtype)
+            assert torch.equal(view.view(bits), exp.view(bits))
+            assert torch.equal(buf[:off], base[:off])
+            assert torch.equal(buf[off + n:], base[off + n:])
+
+
 def test_fallbacks_match_composition():
     """Inputs the fused path does not take (vocab not a whole number of
     16-byte vectors, above the row capacity, sequence-level weights) run the

@@ -199,3 +199,21 @@ def test_qwen_head_shape_chunks():
     del full, chunked
     for a, b in zip(out_a[1:], out_b[1:]):
         assert torch.all((a - b).abs() <= 2 * dx + 2e-5)
+
+
+def test_default_chunking_is_one_chunk_when_it_fits():
+    """Without chunk_tokens, tokens that fit the default budget run as one
+    chunk: the same results as chunk_tokens = all tokens."""
+    ko = _ko()
+    h, w, t, mask, adv, old, ref = make(2, 48, 128, 2048, seed=7)
+    B, S, D = h.shape
+    outs = []
+    for chunk in (None, B * S):
+        hh = h.clone().requires_grad_(True)
+        ww = w.clone().requires_grad_(True)
+        loss, lp, ent = ko.fused_linear_grpo_step(hh, ww, t, old, adv, mask, ref,
+                                                  chunk_tokens=chunk, **KW)
+        loss.backward()
+        outs.append((loss, lp, ent, hh.grad, ww.grad))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)

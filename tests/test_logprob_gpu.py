@@ -370,6 +370,46 @@ def test_negative_infinity_logits(dtype, config, oracle):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+def test_one_element_path_matches_vector_path(dtype):
+    """The backward writes the same bits for a row whether it takes the
+    16-byte vector path or the one-element path (rows whose logits and
+    d_logits sit at different offsets within 16 bytes), with and without a
+    temperature, signed zeros included: a -inf logit's gradient is
+    0 * c0 (times 1/T), -0 for c0 = -g_logp < 0.  (For fp16 the compiler
+    would otherwise fold a product rounded to fp16 into an fma with a +0
+    addend in the one-element path, which turns -0 into +0.)"""
+    from kernel_opt import _C
+    N, V = 4, 9001
+    g = torch.Generator().manual_seed(61)
+    base = seeded_logits((N, V + 1), dtype, seed=61)
+    mask = torch.rand(N, V + 1, generator=g) < 0.2
+    base = base.masked_fill(mask, float("-inf"))
+    t_cpu = seeded_targets((N,), V, seed=61)
+    for r in range(N):  # targets with finite logits
+        while not torch.isfinite(base[r, t_cpu[r]]):
+            t_cpu[r] = (t_cpu[r] + 1) % V
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    x = base[:, :V].contiguous().to(DEV)  # 16-byte aligned rows: the vector path
+    shifted = torch.empty((N, V + 1), dtype=dtype, device=DEV)
+    shifted[:, 1:] = x
+    x_mis = shifted[:, 1:]  # the same values one element off: the one-element path
+    t = t_cpu.to(DEV)
+    gl = torch.full((N,), 0.5, device=DEV)
+    inf = ~torch.isfinite(x.float())
+    for temperature in (None, 0.7):
+        print(f"one-element vs vector path: dtype={dtype} T={temperature}", flush=True)
+        outs = [torch.empty(N, device=DEV) for _ in range(3)]
+        _C.fwd_launch(x, t, *outs, temperature=temperature)
+        d_vec, d_one = (torch.empty((N, V), dtype=dtype, device=DEV) for _ in range(2))
+        _C.bwd_launch(x, t, outs[2], outs[1], gl, None, None, d_vec, temperature=temperature)
+        _C.bwd_launch(x_mis, t, outs[2], outs[1], gl, None, None, d_one,
+                      temperature=temperature)
+        assert torch.equal(d_one.view(bits), d_vec.view(bits)), "paths differ"
+        assert (d_vec.float()[inf] == 0).all()
+        assert torch.signbit(d_vec.float()[inf]).all()  # -0: 0 * (c0 < 0)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_special_rows(dtype):
     """Whole row -inf, a NaN, a +inf: same outcome classes as the reference
     v1 kernel (lse -inf / entropy NaN; NaN rows; NaN for +inf)."""
