@@ -260,6 +260,49 @@ def test_fallbacks_match_composition():
         assert torch.equal(xa.grad, xb.grad)
 
 
+@pytest.mark.parametrize("B,S,V,dtype", [(8, 1024, 128256, torch.float16),    # C3
+                                          (16, 2048, 151936, torch.bfloat16)])  # C4
+def test_full_size_matches_unfused_composition(B, S, V, dtype):
+    """C3 and C4 at full size (C4: 4.98e9 elements, 64-bit row offsets): the
+    fused step against the unfused composition on the same inputs, loss within
+    1e-5 relative, logp / entropy within 4e-5, every d_logits element within
+    1 ulp (compared in row blocks to bound memory)."""
+    ko = _ko()
+    print(f"grpo step full size: {(B, S, V)} {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(15)
+    x = (torch.randn(B, S, V, generator=g, device=DEV) * 2.0).to(dtype)
+    t = torch.randint(0, V, (B, S), generator=g, device=DEV)
+    mask = (torch.rand(B, S, generator=g, device=DEV) < 0.9).float()
+    adv = torch.randn(B, generator=g, device=DEV)
+    with torch.no_grad():
+        lp0, _, _ = ko.fused_logprob_entropy_forward(x, t)
+    old = lp0 + 0.2 * torch.randn(B, S, generator=g, device=DEV)
+    kw = dict(eps_low=0.2, eps_high=0.28, beta=0.0, loss_type="bnpo")
+    xa = x.requires_grad_(True)
+    la, lpa, enta = ko.fused_grpo_step(xa, t, old, adv, mask, **kw)
+    la.backward()
+    da = xa.grad
+    xa.grad = None
+    lpb, entb, _ = ko.fused_logprob_entropy(xa, t)
+    lb, _ = ko.fused_grpo_loss(lpb, old, adv, mask, **kw)
+    lb.backward()
+    db = xa.grad
+    assert abs(la.item() - lb.item()) <= 1e-5 * max(1.0, abs(lb.item()))
+    assert (lpa - lpb).abs().max().item() <= 4e-5
+    assert (enta - entb).abs().max().item() <= 4e-5
+
+    def ordered(v):
+        v = v.view(torch.int16).to(torch.int32)
+        mag = v & 0x7FFF
+        return torch.where(v < 0, -mag, mag)
+    a2, b2 = da.view(-1, V), db.view(-1, V)
+    worst = 0
+    for r0 in range(0, a2.size(0), 2048):
+        worst = max(worst, (ordered(a2[r0:r0 + 2048]) - ordered(b2[r0:r0 + 2048]))
+                    .abs().max().item())
+    assert worst <= 1, f"d_logits up to {worst} ulp from the unfused composition"
+
+
 def test_c2_matches_unfused_composition():
     """C2 ([4, 256, 152064] bf16): the fused step against the unfused
     composition on the same inputs."""
