@@ -35,6 +35,7 @@ from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import torch
 
 from . import _C
@@ -47,6 +48,13 @@ __all__ = ["fused_grpo_step", "grpo_token_weights", "grpo_step_launch"]
 
 def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _f32_reciprocal(v) -> float:
+    """fp32(1) / fp32(v), rounded once in float32 (what dividing a float32
+    tensor gives), as a Python float: multiplying a float32 tensor by it needs
+    no device copy of a host scalar (no synchronisation, capturable)."""
+    return float(np.float32(1.0) / np.float32(v))
 
 
 def grpo_token_weights(mask: torch.Tensor, loss_type: str = "bnpo",
@@ -65,11 +73,11 @@ def grpo_token_weights(mask: torch.Tensor, loss_type: str = "bnpo",
         return m * (1.0 / m.sum().clamp(min=1.0))
     if loss_type == "dr_grpo":
         L = S if max_completion_length is None else max_completion_length
-        return m * (1.0 / torch.tensor(float(B * L), dtype=torch.float32, device=m.device))
+        return m * _f32_reciprocal(B * L)
     if loss_type == "dapo":
         if normalizer is None:
             raise ValueError("loss_type='dapo' needs `normalizer`")
-        return m * (1.0 / torch.tensor(float(normalizer), dtype=torch.float32, device=m.device))
+        return m * _f32_reciprocal(normalizer)
     raise ValueError(f"unknown loss_type {loss_type!r}")
 
 

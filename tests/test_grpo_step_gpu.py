@@ -239,6 +239,58 @@ def test_scale_by_upstream(dtype):
             assert torch.equal(buf[off + n:], base[off + n:])
 
 
+@pytest.mark.parametrize("loss_type", ["grpo", "dr_grpo"])
+def test_hip_graph_capture_of_loss_and_backward(loss_type):
+    """fused_grpo_step's forward and (0.5 * loss).backward() captured in one
+    HIP graph: nothing on the way reads a device value on the host (the
+    upstream gradient is applied by klp_scale_inplace, the token weights'
+    normalisers are host floats).  Every replay, with new logits, eager work
+    and synchronisations between replays, equals the eager step on the same
+    logits bit for bit."""
+    ko = _ko()
+    B, S, V = 2, 40, 8192
+    gen = torch.Generator(device=DEV).manual_seed(17)
+
+    def logits():
+        return (torch.randn(B, S, V, generator=gen, device=DEV) * 2).to(torch.bfloat16)
+    x = logits().requires_grad_(True)
+    t = torch.randint(0, V, (B, S), generator=gen, device=DEV)
+    mask = (torch.rand(B, S, generator=gen, device=DEV) < 0.9).float()
+    adv = torch.randn(B, generator=gen, device=DEV)
+    old = torch.full((B, S), -9.0, device=DEV)
+    kw = dict(eps_low=0.2, eps_high=0.28, loss_type=loss_type)
+
+    def step(inp):
+        loss, lp, ent = ko.fused_grpo_step(inp, t, old, adv, mask, **kw)
+        (loss * 0.5).backward()
+        return loss, lp, ent
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):  # warm-up on the capture stream
+            step(x)
+            x.grad = None
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = step(x)
+    for rep in range(3):
+        print(f"graph replay {rep} ({loss_type})", flush=True)
+        with torch.no_grad():
+            x.copy_(logits())
+        junk = torch.randn(1000, device=DEV).sum()  # unrelated eager work
+        g.replay()
+        torch.cuda.synchronize()
+        assert junk.isfinite()
+        got = [z.detach().clone() for z in out] + [x.grad.clone()]
+        xe = x.detach().clone().requires_grad_(True)
+        exp = list(step(xe)) + [xe.grad]
+        for a, b in zip(got, exp):
+            assert torch.equal(a, b.detach()), f"replay {rep} differs from eager"
+
+
 def test_fallbacks_match_composition():
     """Inputs the fused path does not take (vocab not a whole number of
     16-byte vectors, above the row capacity, sequence-level weights) run the
