@@ -27,7 +27,7 @@ import threading
 
 import torch
 
-from ._library import DTYPE_CODES, check_status, lib
+from ._library import DTYPE_CODES, check_status, device_guard, lib, ptr, stream_handle
 
 __all__ = [
     "fused_logprob_entropy_naive",
@@ -51,6 +51,13 @@ def row_layout(t: torch.Tensor):
     be reached with unit-stride rows and at most two leading strides."""
     if t.dim() == 0:
         return None
+    if t.is_contiguous():
+        # Fast path, same result as the general walk below for two or more
+        # rows: one run of rows V elements apart.
+        V = t.size(-1)
+        n = t.numel() // V if V else 0
+        if n >= 2:
+            return (n, 0, V)
     if t.size(-1) > 1 and t.stride(-1) != 1:
         return None
     dims = [(s, st) for s, st in zip(t.shape[:-1], t.stride()[:-1]) if s != 1]
@@ -78,21 +85,25 @@ _ws_lock = threading.Lock()
 _workspaces: dict = {}
 
 
-def _workspace(device: torch.device, stream: torch.cuda.Stream, nbytes: int):
+def _workspace(device_index: int, stream: int, nbytes: int):
+    """The workspace of (device, raw stream handle) holding at least
+    ``nbytes``; the device must be current and ``stream`` its current
+    stream."""
     if nbytes == 0:
         return None
-    key = (device.index, stream.cuda_stream)
+    key = (device_index, stream)
     with _ws_lock:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() < nbytes:
-            with torch.cuda.stream(stream):
-                buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            # Allocated on the stream that uses it (the caching allocator then
+            # reuses it only in that stream's order).
+            with torch.cuda.stream(torch.cuda.current_stream(device_index)):
+                buf = torch.empty(nbytes, dtype=torch.uint8, device=device_index)
             _workspaces[key] = buf
         return buf
 
 
-def _ptr(t):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+_ptr = ptr
 
 
 def _common_forward_checks(logits, targets, logprob, entropy, lse_out, per_output: bool):
@@ -118,8 +129,10 @@ def _common_forward_checks(logits, targets, logprob, entropy, lse_out, per_outpu
     _require(targets.is_contiguous(), "targets must be contiguous")
     _require(logprob.is_contiguous() and entropy.is_contiguous() and lse_out.is_contiguous(),
              "outputs must be contiguous")
-    for t in (targets, logprob, entropy, lse_out):
-        _require(t.device == logits.device, "all tensors must be on the device of logits")
+    d = logits.get_device()
+    _require(targets.get_device() == d and logprob.get_device() == d
+             and entropy.get_device() == d and lse_out.get_device() == d,
+             "all tensors must be on the device of logits")
     return rows, N, V
 
 
@@ -142,9 +155,9 @@ def fwd_launch(logits, targets, logprob, entropy, lse_out, config=None, temperat
     if N == 0:
         return
     code = DTYPE_CODES[logits.dtype]
-    dev = logits.device
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev)
+    dev = logits.get_device()
+    with device_guard(dev):
+        stream = stream_handle(dev)
         if config is None:
             nbytes = lib.klp_fwd_workspace_bytes(code, N, V)
         else:
@@ -154,12 +167,12 @@ def fwd_launch(logits, targets, logprob, entropy, lse_out, config=None, temperat
                 _ptr(logprob), _ptr(entropy), _ptr(lse_out), _ptr(ws),
                 0 if ws is None else ws.numel()]
         if temp is not None:
-            rc = lib.klp_fwd_temp(*args[:8], temp, *args[8:], ctypes.c_void_p(stream.cuda_stream))
+            rc = lib.klp_fwd_temp(*args[:8], temp, *args[8:], stream)
         elif config is None:
-            rc = lib.klp_fwd(*args, ctypes.c_void_p(stream.cuda_stream))
+            rc = lib.klp_fwd(*args, stream)
         else:
             w, u, sp, fl = (int(c) for c in config)
-            rc = lib.klp_fwd_ex(*args, w, u, sp, fl, ctypes.c_void_p(stream.cuda_stream))
+            rc = lib.klp_fwd_ex(*args, w, u, sp, fl, stream)
     check_status(rc)
 
 
@@ -173,12 +186,11 @@ def fused_logprob_entropy_naive(logits, targets, logprob, entropy, lse_out) -> N
     rows, N, V = _common_forward_checks(logits, targets, logprob, entropy, lse_out, True)
     if N == 0:
         return
-    dev = logits.device
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev)
+    dev = logits.get_device()
+    with device_guard(dev):
         rc = lib.klp_fwd_naive(_ptr(logits), DTYPE_CODES[logits.dtype], N, V, rows[0], rows[1],
                                rows[2], _ptr(targets), _ptr(logprob), _ptr(entropy),
-                               _ptr(lse_out), ctypes.c_void_p(stream.cuda_stream))
+                               _ptr(lse_out), stream_handle(dev))
     check_status(rc)
 
 
@@ -203,8 +215,9 @@ def _backward_checks(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logi
              and all(g.numel() == N for g in grads), "leading-dim count mismatch")
     _require(targets.is_contiguous() and lse.is_contiguous() and entropy.is_contiguous(),
              "targets / saved lse / entropy must be contiguous")
-    for t in [targets, lse, entropy, d_logits] + grads:
-        _require(t.device == logits.device, "all tensors must be on the device of logits")
+    d = logits.get_device()
+    _require(all(t.get_device() == d for t in [targets, lse, entropy, d_logits] + grads),
+             "all tensors must be on the device of logits")
     return rows, N, V
 
 
@@ -217,19 +230,19 @@ def bwd_launch(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits,
     temp = _temperature(temperature, config)
     if N == 0:
         return
-    dev = logits.device
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev)
+    dev = logits.get_device()
+    with device_guard(dev):
+        stream = stream_handle(dev)
         args = [_ptr(logits), DTYPE_CODES[logits.dtype], N, V, rows[0], rows[1], rows[2],
                 _ptr(targets), _ptr(lse), _ptr(entropy), _ptr(g_logp), _ptr(g_ent),
                 _ptr(g_lse), _ptr(d_logits)]
         if temp is not None:
-            rc = lib.klp_bwd_temp(*args[:8], temp, *args[8:], ctypes.c_void_p(stream.cuda_stream))
+            rc = lib.klp_bwd_temp(*args[:8], temp, *args[8:], stream)
         elif config is None:
-            rc = lib.klp_bwd(*args, ctypes.c_void_p(stream.cuda_stream))
+            rc = lib.klp_bwd(*args, stream)
         else:
             w, u, sp, fl = (int(c) for c in config)
-            rc = lib.klp_bwd_ex(*args, w, u, sp, fl, ctypes.c_void_p(stream.cuda_stream))
+            rc = lib.klp_bwd_ex(*args, w, u, sp, fl, stream)
     check_status(rc)
 
 

@@ -10,6 +10,7 @@ process then holds a single HIP runtime.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 
@@ -97,6 +98,34 @@ def last_error() -> str:
     buf = ctypes.create_string_buffer(n + 1)
     lib.klp_last_error(buf, n + 1)
     return buf.value.decode("utf-8", "replace")
+
+
+# Per-call host helpers of the launch wrappers.  A launch goes onto torch's
+# current stream of the tensors' device, with that device current; these
+# avoid building a torch.cuda.Stream object and entering a device context
+# on every call (together about 3 us of a ~12 us call).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_no_switch = contextlib.nullcontext()
+
+
+def stream_handle(device_index: int) -> int:
+    """The raw hipStream_t of ``device_index``'s current stream."""
+    if _raw_stream is not None:
+        return _raw_stream(device_index)
+    return torch.cuda.current_stream(device_index).cuda_stream
+
+
+def device_guard(device_index: int):
+    """Context manager making ``device_index`` current: a no-op when it
+    already is."""
+    if torch.cuda.current_device() == device_index:
+        return _no_switch
+    return torch.cuda.device(device_index)
+
+
+def ptr(t):
+    """Data pointer of ``t`` for a ``void*`` argument (``None`` -> NULL)."""
+    return None if t is None else t.data_ptr()
 
 
 def check_status(rc: int) -> None:

@@ -26,20 +26,18 @@ With no tokens (B = 0 or S = 0) the loss is 0.
 """
 from __future__ import annotations
 
-import ctypes
-
 import torch
 
 from ._library import (KLP_GRPO_LOSS_BNPO, KLP_GRPO_LOSS_FIXED, KLP_GRPO_LOSS_GRPO,
-                       KLP_GRPO_SEQUENCE, KLP_GRPO_TOKEN, check_status, lib)
+                       KLP_GRPO_SEQUENCE, KLP_GRPO_TOKEN, check_status, device_guard, lib, ptr,
+                       stream_handle)
 
 __all__ = ["fused_grpo_loss"]
 
 _LEVELS = {"token": KLP_GRPO_TOKEN, "sequence": KLP_GRPO_SEQUENCE}
 
 
-def _ptr(t):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+_ptr = ptr
 
 
 def _f32(t, name, shape, device):
@@ -86,11 +84,11 @@ class _FusedGrpoLoss(torch.autograd.Function):
         ws = torch.empty(lib.klp_grpo_workspace_bytes(B), dtype=torch.uint8, device=dev)
         loss = torch.empty(1, dtype=torch.float32, device=dev)
         stats = torch.empty(4, dtype=torch.float32, device=dev)
-        with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
+        with device_guard(dev.index):
+            stream = stream_handle(dev.index)
             rc = lib.klp_grpo_fwd(_ptr(lp), _ptr(old_logp), _ptr(ref_logp), _ptr(advantages),
                                   _ptr(mask), B, S, *params, _ptr(loss), _ptr(stats), _ptr(ws),
-                                  ws.numel(), ctypes.c_void_p(stream))
+                                  ws.numel(), stream)
         check_status(rc)
         ctx.save_for_backward(lp, old_logp, ref_logp, advantages, mask, ws)
         ctx.params = params
@@ -106,11 +104,11 @@ class _FusedGrpoLoss(torch.autograd.Function):
         g = g_loss.detach().to(torch.float32).reshape(1).contiguous()
         d = torch.empty_like(lp)
         dev = lp.device
-        with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
+        with device_guard(dev.index):
+            stream = stream_handle(dev.index)
             rc = lib.klp_grpo_bwd(_ptr(lp), _ptr(old_logp), _ptr(ref_logp), _ptr(advantages),
                                   _ptr(mask), B, S, *ctx.params, _ptr(g), _ptr(d), _ptr(ws),
-                                  ws.numel(), ctypes.c_void_p(stream))
+                                  ws.numel(), stream)
         check_status(rc)
         return d, None, None, None, None, None
 

@@ -33,21 +33,18 @@ Restrictions of the fused path, by construction:
 """
 from __future__ import annotations
 
-import ctypes
-
 import numpy as np
 import torch
 
 from . import _C
-from ._library import DTYPE_CODES, check_status, lib
+from ._library import DTYPE_CODES, check_status, device_guard, lib, ptr, stream_handle
 from .grpo import fused_grpo_loss
 from .ops import fused_logprob_entropy
 
 __all__ = ["fused_grpo_step", "grpo_token_weights", "grpo_step_launch"]
 
 
-def _ptr(t):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+_ptr = ptr
 
 
 def _f32_reciprocal(v) -> float:
@@ -110,13 +107,13 @@ def grpo_step_launch(logits, targets, old, ref, adv, weight, params):
     logp, ent, lse, loss_tok = (torch.empty((B, S), dtype=torch.float32, device=dev)
                                 for _ in range(4))
     d_logits = torch.empty((B, S, V), dtype=logits.dtype, device=dev)
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
+    with device_guard(dev.index):
+        stream = stream_handle(dev.index)
         rc = lib.klp_grpo_step(_ptr(logits), DTYPE_CODES[logits.dtype], B * S, V, *rows,
                                _ptr(targets), float(temperature), _ptr(old), _ptr(ref),
                                _ptr(adv), _ptr(weight), S, eps_low, eps_high, beta, per_token,
                                _ptr(logp), _ptr(ent), _ptr(lse), _ptr(loss_tok), _ptr(d_logits),
-                               ctypes.c_void_p(stream))
+                               stream)
     check_status(rc)
     return logp, ent, lse, loss_tok, d_logits
 
@@ -129,10 +126,10 @@ def scale_by_upstream(t: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
     if not t.is_contiguous():
         raise RuntimeError("scale_by_upstream needs a contiguous tensor")
     g32 = g.detach().to(device=t.device, dtype=torch.float32).reshape(1).contiguous()
-    with torch.cuda.device(t.device):
-        stream = torch.cuda.current_stream(t.device).cuda_stream
+    with device_guard(t.device.index):
+        stream = stream_handle(t.device.index)
         rc = lib.klp_scale_inplace(_ptr(t), DTYPE_CODES[t.dtype], t.numel(), _ptr(g32),
-                                   ctypes.c_void_p(stream))
+                                   stream)
     check_status(rc)
     return t
 

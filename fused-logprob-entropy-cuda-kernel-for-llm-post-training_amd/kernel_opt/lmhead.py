@@ -21,27 +21,26 @@ old-policy and reference log-probabilities).
 """
 from __future__ import annotations
 
-import ctypes
-
 import torch
 
-from ._library import check_status, lib
+from ._library import check_status, device_guard, lib, ptr, stream_handle
 
 __all__ = ["fused_linear_logprob_entropy", "fused_linear_logprob_entropy_forward"]
 
 
-def _ptr(t):
-    return ctypes.c_void_p(t.data_ptr())
+_ptr = ptr
 
 
 _ws = {}
 
 
 def _workspace(dev, stream, nbytes):
-    key = (dev.index, stream.cuda_stream)
+    """The workspace of (device, raw handle of its current stream), allocated
+    on that stream."""
+    key = (dev.index, stream)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
-        with torch.cuda.stream(stream):
+        with torch.cuda.stream(torch.cuda.current_stream(dev)):
             buf = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
         _ws[key] = buf
     return buf
@@ -100,13 +99,13 @@ class _FusedLinearLogprobEntropy(torch.autograd.Function):
         ld_d = (V + 3) // 4 * 4
         d = torch.empty(N, ld_d, dtype=torch.bfloat16, device=hidden.device)
         T = 1.0 if ctx.temperature is None else float(ctx.temperature)
-        with torch.cuda.device(hidden.device):
-            stream = torch.cuda.current_stream(hidden.device)
+        with device_guard(hidden.device.index):
+            stream = stream_handle(hidden.device.index)
             rc = lib.klp_lmh_bwd_logits(
                 _ptr(h2), _ld(h2), _ptr(weight), _ld(weight), N, V, D, _ptr(t), T,
                 _ptr(lse), _ptr(ent), None if gl is None else _ptr(gl),
                 None if ge is None else _ptr(ge), None if gs is None else _ptr(gs),
-                _ptr(d), ld_d, ctypes.c_void_p(stream.cuda_stream))
+                _ptr(d), ld_d, stream)
         check_status(rc)
         dl = d[:, :V]
         dh = torch.mm(dl, weight).reshape(hidden.shape) if need_h else None
@@ -144,11 +143,11 @@ def fused_linear_logprob_entropy_forward(hidden: torch.Tensor, weight: torch.Ten
         return tuple(out)
     T = 1.0 if temperature is None else float(temperature)
     dev = hidden.device
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev)
+    with device_guard(dev.index):
+        stream = stream_handle(dev.index)
         ws = _workspace(dev, stream, lib.klp_lmh_workspace_bytes(N, V, D))
         rc = lib.klp_lmh_fwd(_ptr(h2), _ld(h2), _ptr(weight), _ld(weight),
                              N, V, D, _ptr(t), T, _ptr(out[0]), _ptr(out[1]), _ptr(out[2]),
-                             _ptr(ws), ws.numel(), ctypes.c_void_p(stream.cuda_stream))
+                             _ptr(ws), ws.numel(), stream)
     check_status(rc)
     return tuple(out)

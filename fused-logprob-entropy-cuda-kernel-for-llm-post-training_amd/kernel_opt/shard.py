@@ -16,18 +16,15 @@ caller's collective.  The reference has no multi-GPU path.
 """
 from __future__ import annotations
 
-import ctypes
-
 import torch
 
 from . import _C
-from ._library import DTYPE_CODES, check_status, lib
+from ._library import DTYPE_CODES, check_status, device_guard, lib, ptr, stream_handle
 
 __all__ = ["shard_state", "merge_shard_states", "shard_backward"]
 
 
-def _ptr(t):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+_ptr = ptr
 
 
 def shard_state(logits_shard: torch.Tensor, targets: torch.Tensor, vocab_offset: int,
@@ -47,11 +44,11 @@ def shard_state(logits_shard: torch.Tensor, targets: torch.Tensor, vocab_offset:
     t = targets.contiguous()
     state = torch.empty(*targets.shape, 4, dtype=torch.float32, device=logits_shard.device)
     T = 1.0 if temperature is None else float(temperature)
-    with torch.cuda.device(logits_shard.device):
-        stream = torch.cuda.current_stream(logits_shard.device).cuda_stream
+    with device_guard(logits_shard.device.index):
+        stream = stream_handle(logits_shard.device.index)
         rc = lib.klp_fwd_shard(_ptr(logits_shard), DTYPE_CODES[logits_shard.dtype], N, V, *rows,
                                _ptr(t), int(vocab_offset), T, _ptr(state),
-                               ctypes.c_void_p(stream))
+                               stream)
     check_status(rc)
     return state
 
@@ -68,11 +65,11 @@ def merge_shard_states(states: torch.Tensor, targets: torch.Tensor, shard_vocab:
     t = targets.contiguous()
     outs = [torch.empty(targets.shape, dtype=torch.float32, device=states.device)
             for _ in range(3)]
-    with torch.cuda.device(states.device):
-        stream = torch.cuda.current_stream(states.device).cuda_stream
+    with device_guard(states.device.index):
+        stream = stream_handle(states.device.index)
         rc = lib.klp_fwd_shard_merge(_ptr(s), P, t.numel(), _ptr(t), int(shard_vocab),
                                      int(vocab), *[_ptr(o) for o in outs],
-                                     ctypes.c_void_p(stream))
+                                     stream)
     check_status(rc)
     return tuple(outs)
 
