@@ -52,12 +52,18 @@ def row_layout(t: torch.Tensor):
     if t.dim() == 0:
         return None
     if t.is_contiguous():
-        # Fast path, same result as the general walk below for two or more
-        # rows: one run of rows V elements apart.
+        # Fast path, same result as _row_layout_walk for two or more rows:
+        # one run of rows V elements apart.
         V = t.size(-1)
         n = t.numel() // V if V else 0
         if n >= 2:
             return (n, 0, V)
+    return _row_layout_walk(t)
+
+
+def _row_layout_walk(t: torch.Tensor):
+    """row_layout by merging the leading dims' strides (any tensor of rank
+    >= 1)."""
     if t.size(-1) > 1 and t.stride(-1) != 1:
         return None
     dims = [(s, st) for s, st in zip(t.shape[:-1], t.stride()[:-1]) if s != 1]

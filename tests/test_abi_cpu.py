@@ -177,6 +177,18 @@ def test_row_layout():
     assert row_layout(torch.zeros(())) is None
 
 
+def test_row_layout_fast_path_matches_general_walk():
+    """row_layout's contiguous fast path returns what the general stride walk
+    returns, for contiguous tensors of every rank up to 4 and every size
+    pattern over {0, 1, 2, 3, 7} (size-1 and size-0 dims included)."""
+    import itertools
+    from kernel_opt._C import _row_layout_walk, row_layout
+    for rank in (1, 2, 3, 4):
+        for shape in itertools.product((0, 1, 2, 3, 7), repeat=rank):
+            t = torch.empty(shape)
+            assert row_layout(t) == _row_layout_walk(t), shape
+
+
 def test_package_surface_matches_reference():
     """reference python/kernel_opt/__init__.py:1-15."""
     import kernel_opt
