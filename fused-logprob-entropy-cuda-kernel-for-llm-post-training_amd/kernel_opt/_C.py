@@ -22,6 +22,7 @@ messages (``csrc/fused_logprob.cu:294-311,362-374,412-424``).  Differences:
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 import threading
 
@@ -87,8 +88,12 @@ def _row_layout_walk(t: torch.Tensor):
 
 # Split-row workspaces (partial states), one per (device, stream) so that
 # launches sharing one are ordered by their stream.  No initialisation needed.
+# At most _WS_KEEP are kept, least recently used dropped first: each was
+# allocated on its own stream, so the caching allocator hands a dropped one
+# out again only in that stream's order, after the launches that used it.
 _ws_lock = threading.Lock()
-_workspaces: dict = {}
+_workspaces: collections.OrderedDict = collections.OrderedDict()
+_WS_KEEP = 16
 
 
 def _workspace(device_index: int, stream: int, nbytes: int):
@@ -106,6 +111,9 @@ def _workspace(device_index: int, stream: int, nbytes: int):
             with torch.cuda.stream(torch.cuda.current_stream(device_index)):
                 buf = torch.empty(nbytes, dtype=torch.uint8, device=device_index)
             _workspaces[key] = buf
+        _workspaces.move_to_end(key)
+        while len(_workspaces) > _WS_KEEP:
+            _workspaces.popitem(last=False)
         return buf
 
 

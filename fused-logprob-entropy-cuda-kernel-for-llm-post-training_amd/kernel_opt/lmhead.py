@@ -21,6 +21,9 @@ old-policy and reference log-probabilities).
 """
 from __future__ import annotations
 
+import collections
+import threading
+
 import torch
 
 from ._library import check_status, device_guard, lib, ptr, stream_handle
@@ -31,19 +34,27 @@ __all__ = ["fused_linear_logprob_entropy", "fused_linear_logprob_entropy_forward
 _ptr = ptr
 
 
-_ws = {}
+# Forward workspaces, one per (device, stream), the 16 most recently used
+# kept (as kernel_opt._C keeps its split-row workspaces).
+_ws_lock = threading.Lock()
+_ws: collections.OrderedDict = collections.OrderedDict()
+_WS_KEEP = 16
 
 
 def _workspace(dev, stream, nbytes):
     """The workspace of (device, raw handle of its current stream), allocated
     on that stream."""
     key = (dev.index, stream)
-    buf = _ws.get(key)
-    if buf is None or buf.numel() < nbytes:
-        with torch.cuda.stream(torch.cuda.current_stream(dev)):
-            buf = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
-        _ws[key] = buf
-    return buf
+    with _ws_lock:
+        buf = _ws.get(key)
+        if buf is None or buf.numel() < nbytes:
+            with torch.cuda.stream(torch.cuda.current_stream(dev)):
+                buf = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+            _ws[key] = buf
+        _ws.move_to_end(key)
+        while len(_ws) > _WS_KEEP:
+            _ws.popitem(last=False)
+        return buf
 
 
 def _check(hidden, weight, targets):

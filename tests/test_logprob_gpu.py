@@ -505,6 +505,31 @@ def test_multiple_streams(oracle):
         _check_fwd(oracle, xs[i], ts[i], outs[i], 2e-5, label=f"stream {i}")
 
 
+def test_workspace_cache_is_bounded():
+    """Split-row forwards on 20 new streams in turn: the shim keeps at most 16
+    workspaces (least recently used dropped), and every stream's results equal
+    the default stream's."""
+    from kernel_opt import _C
+    V = 30011
+    x = seeded_logits((48, V), torch.bfloat16, seed=151).to(DEV)
+    t = seeded_targets((48,), V, seed=151).to(DEV)
+    cfg = (8, 2, 8, 0)  # 8 pieces per row: a workspace is needed
+    ref = [torch.empty(48, device=DEV) for _ in range(3)]
+    _C.fwd_launch(x, t, *ref, config=cfg)
+    torch.cuda.synchronize()
+    for i in range(20):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        out = [torch.empty(48, device=DEV) for _ in range(3)]
+        with torch.cuda.stream(s):
+            _C.fwd_launch(x, t, *out, config=cfg)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        assert len(_C._workspaces) <= _C._WS_KEEP
+        for a, b in zip(out, ref):
+            assert torch.equal(a, b), f"stream {i}"
+
+
 # ---------------------------------------------------------------------------
 # Committed known-answer fixtures (tests/golden/klp_golden.npz)
 # ---------------------------------------------------------------------------
