@@ -19,12 +19,16 @@
 //    reduction until the end of the chunk;
 //  - K advances in steps of 32 through a ring of 5 LDS stages (32 KB each,
 //    all 160 KB of LDS), filled by direct global -> LDS copies
-//    (global_load_lds_dwordx4, no register staging) issued 4 stages ahead of
-//    the multiply; the ring runs across tile boundaries;
+//    (global_load_lds_dwordx4, no register staging) 3-4 stages ahead of the
+//    multiply; a slot is refilled once every wave is past the MFMAs of the
+//    stage it held; the ring runs across tile boundaries;
 //  - LDS rows are 64 bytes; the 16-byte chunk index is XOR-swizzled with
 //    row bits 0..3 (swz_f) so that the MFMA operand reads are free of bank
 //    conflicts;
-//  - a stage's operand fragments are all read before its MFMAs run;
+//  - a stage's operands are read in two 16-column halves, ping-ponged: the
+//    MFMAs of one half run while the other half is read from LDS (the next
+//    stage's first half under the current stage's second), one barrier per
+//    stage between the halves;
 //  - after each tile the block's logits are folded into per-lane
 //    (m, z, t) states (absorb() of klp_device.h) and the target logit is
 //    captured if it lies in the tile.
@@ -168,32 +172,83 @@ __global__ __launch_bounds__(kThreads) void klp_lmh_kernel(LmhParams p) {
         }
     }
 
-    // Issue the copies of global stage g (tile tile_first + g / n_ksteps,
-    // K step g % n_ksteps) into ring slot g % kRing.
-    auto issue = [&](int g) {
-        const int64_t vt = tile_first + g / n_ksteps;
-        const int64_t koff = static_cast<int64_t>(g % n_ksteps) * kBK;
-        unsigned char* dst = lds + (g % kRing) * kStageBytes;
+    // Copies.  Stages run across the chunk's tiles: global stage g is tile
+    // tile_first + g / n_ksteps, K step g % n_ksteps, in ring slot g % kRing.
+    // `issued` stages have been issued; the W sources of the tile being issued
+    // are set once per tile and advanced by kBK columns per stage.
+    int64_t iss_vt = tile_first;
+    int iss_k = 0;
+    int issued = 0;
+    const uint16_t* wsrc[kWCopies];
+    auto point_w = [&]() {
 #pragma unroll
         for (int j = 0; j < kWCopies; ++j) {
-            const int q = wave + 4 * j;
-            int64_t v = vt * kBV + q * kRowsPerCopy + lrow;
+            int64_t v = iss_vt * kBV + (wave + 4 * j) * kRowsPerCopy + lrow;
             if (v > p.vocab - 1) v = p.vocab - 1;
-            __builtin_amdgcn_global_load_lds(p.weight + v * p.ld_weight + gchunk * 8 + koff,
-                                             dst + q * 1024, 16, 0, 0);
+            wsrc[j] = p.weight + v * p.ld_weight + gchunk * 8;
         }
+    };
+    point_w();
+    // Issue stages up to (not including) `limit`.  A slot may be refilled
+    // once every wave is past the MFMAs of the stage it held: the callers
+    // pass limit = h + 1 + kRing right after a barrier that follows stage h's
+    // MFMAs (the operands of stage h + 1 may still be in flight from LDS, so
+    // its slot stays untouched).
+    auto issue_upto = [&](int limit) {
+        if (limit > n_stages) limit = n_stages;
+        while (issued < limit) {
+            unsigned char* dst = lds + (issued % kRing) * kStageBytes;
+            const int64_t koff = static_cast<int64_t>(iss_k) * kBK;
 #pragma unroll
-        for (int j = 0; j < kHCopies; ++j) {
-            const int q = wave + 4 * j;
-            __builtin_amdgcn_global_load_lds(hsrc[j] + koff, dst + kWBytes + q * 1024, 16, 0, 0);
+            for (int j = 0; j < kWCopies; ++j)
+                __builtin_amdgcn_global_load_lds(wsrc[j] + koff, dst + (wave + 4 * j) * 1024, 16,
+                                                 0, 0);
+#pragma unroll
+            for (int j = 0; j < kHCopies; ++j)
+                __builtin_amdgcn_global_load_lds(hsrc[j] + koff,
+                                                 dst + kWBytes + (wave + 4 * j) * 1024, 16, 0, 0);
+            ++issued;
+            if (++iss_k == n_ksteps) {
+                iss_k = 0;
+                ++iss_vt;
+                point_w();
+            }
         }
     };
 
+    // Operands in two halves of the stage's K (16 columns each, one MFMA K
+    // step), ping-ponged: the MFMAs of one half run while the other half's
+    // operands are read from LDS.  Half 0 of the next stage is read under
+    // half 1's MFMAs, so a stage's first MFMAs find their operands in
+    // registers.  Two halves take the registers one whole stage did.
+    static_assert(kBK == 32, "two 16-column halves per stage");
+    bf16x8 ah[2][kVB], bh[2][kTB];
+    auto read_half = [&](auto half_tag, int stage) {
+        constexpr int H = decltype(half_tag)::value;
+        const unsigned char* wl = lds + (stage % kRing) * kStageBytes;
+        const unsigned char* hl = wl + kWBytes;
+        const int c = H * 2 + (lane >> 5);
 #pragma unroll
-    for (int g = 0; g < kRing - 1; ++g)
-        if (g < n_stages) issue(g);
+        for (int a = 0; a < kVB; ++a)
+            ah[H][a] = *reinterpret_cast<const bf16x8*>(
+                wl + swz(wv * (kVB * 32) + a * 32 + (lane & 31), c));
+#pragma unroll
+        for (int b = 0; b < kTB; ++b)
+            bh[H][b] = *reinterpret_cast<const bf16x8*>(
+                hl + swz(wt * (kTB * 32) + b * 32 + (lane & 31), c));
+    };
+    // Wait until stage `stage` has landed for this wave (at most the stages
+    // issued after it outstanding, up to kRing - 2 of them), then the barrier
+    // makes every wave's copies of it visible.
+    auto sync_stage = [&](int stage) {
+        wait_stages<kRing - 2>(issued - 1 - stage);
+        __builtin_amdgcn_s_barrier();
+    };
+    constexpr int kReadsPerHalf = kVB + kTB;
+    constexpr int kMfmaPerHalf = kVB * kTB;
 
-    int g = 0;  // global stage index, runs across tiles
+    issue_upto(kRing);  // prologue: every slot is free
+    int g = 0;          // global stage index, runs across tiles
     for (int64_t vt = tile_first; vt < tile_end; ++vt) {
         f32x16 acc[kVB][kTB];
 #pragma unroll
@@ -203,46 +258,54 @@ __global__ __launch_bounds__(kThreads) void klp_lmh_kernel(LmhParams p) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
-        for (int ks_stage = 0; ks_stage < n_ksteps; ++ks_stage, ++g) {
-            // Stage g has landed once at most the copies of the stages issued
-            // after it (up to kRing - 2 of them) are outstanding; then the
-            // barrier makes every wave's copies visible and frees slot
-            // (g - 1) % kRing for the copies of stage g + kRing - 1.
-            wait_stages<kRing - 2>(n_stages - 1 - g);
-            __builtin_amdgcn_s_barrier();
-            if (g + kRing - 1 < n_stages) issue(g + kRing - 1);
-
-            const unsigned char* wl = lds + (g % kRing) * kStageBytes;
-            const unsigned char* hl = wl + kWBytes;
-            // All operand fragments of the stage are read first, then the
-            // MFMAs run; the scheduling groups below keep that order (left
-            // alone, the scheduler reuses one register quad for the A
-            // fragments and waits for each read in turn).
-            constexpr int kKS = kBK / 16;
-            bf16x8 af[kKS][kVB], bfr[kKS][kTB];
+        auto mfma_half = [&](auto half_tag) {
+            constexpr int H = decltype(half_tag)::value;
 #pragma unroll
-            for (int ks = 0; ks < kKS; ++ks) {
-                const int c = ks * 2 + (lane >> 5);
-#pragma unroll
-                for (int a = 0; a < kVB; ++a)
-                    af[ks][a] = *reinterpret_cast<const bf16x8*>(
-                        wl + swz(wv * (kVB * 32) + a * 32 + (lane & 31), c));
+            for (int a = 0; a < kVB; ++a)
 #pragma unroll
                 for (int b = 0; b < kTB; ++b)
-                    bfr[ks][b] = *reinterpret_cast<const bf16x8*>(
-                        hl + swz(wt * (kTB * 32) + b * 32 + (lane & 31), c));
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[H][a], bh[H][b],
+                                                                        acc[a][b], 0, 0, 0);
+        };
+        // One read per MFMA for the first kReadsPerHalf MFMAs, then the rest.
+        auto interleave = [&]() {
+#pragma unroll
+            for (int i = 0; i < kReadsPerHalf; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
             }
-#pragma unroll
-            for (int ks = 0; ks < kKS; ++ks)
-#pragma unroll
-                for (int a = 0; a < kVB; ++a)
-#pragma unroll
-                    for (int b = 0; b < kTB; ++b)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            af[ks][a], bfr[ks][b], acc[a][b], 0, 0, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, kKS * (kVB + kTB), 0);  // DS reads
-            __builtin_amdgcn_sched_group_barrier(0x008, kKS * kVB * kTB, 0);    // MFMAs
-        }
+            __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerHalf - kReadsPerHalf, 0);
+        };
+        using Half0 = std::integral_constant<int, 0>;
+        using Half1 = std::integral_constant<int, 1>;
+        // Stage g: half 0's MFMAs under half 1's reads; then, when stage g + 1
+        // belongs to this tile, sync on it, top up the ring and read its half
+        // 0 under half 1's MFMAs.
+        auto step = [&](auto prefetch_tag) {
+            constexpr bool kPrefetch = decltype(prefetch_tag)::value;
+            read_half(Half1{}, g);
+            mfma_half(Half0{});
+            interleave();
+            if constexpr (kPrefetch) {
+                sync_stage(g + 1);
+                // Stage g - 1's operand reads all completed before its MFMAs,
+                // which are behind this barrier; stage g's may still be in flight.
+                issue_upto(g + kRing);
+                read_half(Half0{}, g + 1);
+            }
+            mfma_half(Half1{});
+            if constexpr (kPrefetch) interleave();
+            ++g;
+        };
+
+        // The tile's first stage: its half 0.
+        sync_stage(g);
+        issue_upto(g + kRing);  // stage g - 1's MFMAs are behind the barrier
+        read_half(Half0{}, g);
+        for (int kk = 0; kk + 1 < n_ksteps; ++kk) step(std::true_type{});
+        // The tile's last stage reads nothing ahead: the pipeline drains at
+        // the tile's end, so no operands are live across the epilogue.
+        step(std::false_type{});
 
         const int64_t v0 = vt * kBV;
         if constexpr (kGrad) {
