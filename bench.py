@@ -275,8 +275,9 @@ def grpo_step_timing(dev, K, logits, targets):
     both through the C ABI with preallocated outputs (kernel time only)."""
     import ctypes
     from kernel_opt import _C
-    from kernel_opt._library import (DTYPE_CODES, KLP_GRPO_LOSS_GRPO, KLP_GRPO_TOKEN,
-                                     check_status, lib)
+    from kernel_opt._library import (DTYPE_CODES, KLP_GRPO_LOSS_GRPO,
+                                     KLP_GRPO_STEP_SCHED_BYTES, KLP_GRPO_TOKEN, check_status,
+                                     lib)
     from kernel_opt.grpo_step import grpo_token_weights
     B, S, V = logits.shape
     N = B * S
@@ -293,6 +294,7 @@ def grpo_step_timing(dev, K, logits, targets):
     mask = (torch.rand(B, S, generator=g) < 0.9).float().to(dev)
     w = grpo_token_weights(mask, "grpo").contiguous()
     d = torch.empty(logits.shape, dtype=logits.dtype, device=dev)
+    sched = torch.zeros(KLP_GRPO_STEP_SCHED_BYTES, dtype=torch.uint8, device=dev)
     ws = torch.empty(lib.klp_grpo_workspace_bytes(B), dtype=torch.uint8, device=dev)
     loss = f32(1)
     rows = _C.row_layout(logits)
@@ -305,7 +307,7 @@ def grpo_step_timing(dev, K, logits, targets):
         check_status(lib.klp_grpo_step(P(logits), DTYPE_CODES[logits.dtype], N, V, *rows,
                                        P(targets), 1.0, P(old), P(ref), P(adv), P(w), S,
                                        eps_low, eps_high, beta, 0, P(lp), P(ent), P(lse),
-                                       P(loss_tok), P(d), st))
+                                       P(loss_tok), P(d), P(sched), st))
 
     def unfused():
         _C.fwd_launch(logits, targets, lp, ent, lse)

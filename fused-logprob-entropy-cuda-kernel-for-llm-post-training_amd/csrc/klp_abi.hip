@@ -629,7 +629,7 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                   const float* ref_logp, const float* advantages, const float* tok_weight,
                   int64_t seq_len, float eps_low, float eps_high, float beta, int adv_per_token,
                   float* logprob, float* entropy, float* lse, float* loss_tok, void* d_logits,
-                  void* stream) {
+                  void* sched, void* stream) {
     int rc = check_rows(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
                         targets);
     if (rc != KLP_OK) return rc;
@@ -663,6 +663,8 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
         return fail(KLP_EINVAL, "eps_low and eps_high must be finite and >= 0");
     if (!(beta == beta) || beta == INFINITY || beta == -INFINITY)
         return fail(KLP_EINVAL, "beta must be finite");
+    if (sched != nullptr && !aligned(sched, 8))
+        return fail(KLP_EINVAL, "sched must be 8-byte aligned");
     if ((rc = check_grid(n_rows, 1, klp::kGrpoStepThreads)) != KLP_OK) return rc;
 
     klp::GrpoStepParams p;
@@ -686,9 +688,14 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
     p.lse = lse;
     p.loss_tok = loss_tok;
     p.d_logits = d_logits;
+    p.sched = static_cast<klp::StepSched*>(sched);
     if (injected_failure("grpo step")) return KLP_ELAUNCH;
     return after_launch(klp::launch_grpo_step(dtype, p, static_cast<hipStream_t>(stream)),
                         "grpo step");
+}
+
+int64_t klp_grpo_step_persistent_min_rows(int dtype, int64_t vocab, int scaled) {
+    return klp::grpo_step_persistent_min_rows(dtype, vocab, scaled != 0);
 }
 
 size_t klp_lmh_workspace_bytes(int64_t n_tokens, int64_t vocab, int64_t dim) {

@@ -116,8 +116,16 @@ struct GrpoParams {
 // Workspace words per row of the GRPO loss (5 used, padded).
 constexpr int kGrpoRowWords = 8;
 
-// Fused GRPO step (klp_grpo_step.hip): one workgroup per row, the row held
-// in registers.  Rows are token rows of a [B, S] batch (n_rows = B * S).
+// Row counter of the persistent GRPO step kernel (klp_grpo_step's `sched`):
+// zero before a launch, and left zero by it.
+struct StepSched {
+    unsigned long long next;  // rows handed out after the first gridDim.x
+    unsigned int done;        // workgroups past the last row
+    unsigned int unused;
+};
+
+// Fused GRPO step (klp_grpo_step.hip): the row held in the registers of one
+// workgroup.  Rows are token rows of a [B, S] batch (n_rows = B * S).
 struct GrpoStepParams {
     const void* logits;
     RowMap rm;
@@ -139,11 +147,15 @@ struct GrpoStepParams {
     float* lse;               // [n_rows], nullable
     float* loss_tok;          // [n_rows]: tok_weight * token loss
     void* d_logits;           // dense [n_rows, vocab], logits dtype
+    StepSched* sched;         // nullable: one workgroup per row
 };
 // Most 16-byte vectors one thread of the step kernel holds (1024 threads).
 constexpr int kGrpoStepMaxVec = 19;
 constexpr int kGrpoStepThreads = 1024;
 hipError_t launch_grpo_step(int dtype, const GrpoStepParams& p, hipStream_t stream);
+// Rows from which launch_grpo_step runs the persistent kernel (given a
+// counter) on the current device; -1 if unknown, 0 for unsupported rows.
+int64_t grpo_step_persistent_min_rows(int dtype, int64_t vocab, bool scaled);
 
 // In-place scaling by a device scalar (klp_scale_inplace): elements
 // [0, head) and [head + nvec * per-vector, n) one by one, the nvec 16-byte

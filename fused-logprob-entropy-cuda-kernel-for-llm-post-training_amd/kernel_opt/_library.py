@@ -30,6 +30,8 @@ KLP_OK, KLP_EINVAL, KLP_EDTYPE, KLP_ELAUNCH, KLP_EWORKSPACE = 0, 1, 2, 3, 4
 # klp_grpo_loss_type / klp_grpo_level values
 KLP_GRPO_LOSS_GRPO, KLP_GRPO_LOSS_BNPO, KLP_GRPO_LOSS_FIXED = 0, 1, 2
 KLP_GRPO_TOKEN, KLP_GRPO_SEQUENCE = 0, 1
+# klp_grpo_step's row counter (KLP_GRPO_STEP_SCHED_BYTES).
+KLP_GRPO_STEP_SCHED_BYTES = 16
 
 # Every symbol the public headers declare, with its ctypes signature.
 _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
@@ -60,8 +62,9 @@ SIGNATURES = {
     "klp_grpo_step_max_vocab": (_i64, [_i32]),
     "klp_scale_inplace": (_i32, [_vp, _i32, _i64, _vp, _vp]),
     "klp_grpo_step": (_i32, _ROWS + [_vp, ctypes.c_float] + [_vp] * 4 + [_i64]
-                      + [ctypes.c_float] * 3 + [_i32] + [_vp] * 6),
+                      + [ctypes.c_float] * 3 + [_i32] + [_vp] * 7),
     # include/kernel_opt_hip_tuning.h
+    "klp_grpo_step_persistent_min_rows": (_i64, [_i32, _i64, _i32]),
     "klp_fwd_workspace_bytes_ex": (_sz, [_i64, _i32]),
     "klp_fwd_ex": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _sz, _i32, _i32, _i32, _i32, _vp]),
     "klp_bwd_ex": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,

@@ -33,11 +33,15 @@ Restrictions of the fused path, by construction:
 """
 from __future__ import annotations
 
+import collections
+import threading
+
 import numpy as np
 import torch
 
 from . import _C
-from ._library import DTYPE_CODES, check_status, device_guard, lib, ptr, stream_handle
+from ._library import (DTYPE_CODES, KLP_GRPO_STEP_SCHED_BYTES, check_status, device_guard, lib,
+                       ptr, stream_handle)
 from .grpo import fused_grpo_loss
 from .ops import fused_logprob_entropy
 
@@ -92,6 +96,32 @@ def _fused_supported(logits: torch.Tensor, rows) -> bool:
             and (s_inner * esz) % 16 == 0 and (s_outer * esz) % 16 == 0)
 
 
+# klp_grpo_step's row counters, one per (device, raw stream handle): each is
+# zeroed once, when allocated on its stream, and every launch leaves it zero,
+# so launches on one stream can share it.  At most _SCHED_KEEP are kept,
+# least recently used dropped first (the caching allocator reuses a dropped
+# one only in its stream's order).
+_sched_lock = threading.Lock()
+_scheds: collections.OrderedDict = collections.OrderedDict()
+_SCHED_KEEP = 16
+
+
+def _sched(device_index: int, stream: int) -> torch.Tensor:
+    """The row counter of (device, stream); the device must be current and
+    ``stream`` its current stream."""
+    key = (device_index, stream)
+    with _sched_lock:
+        buf = _scheds.get(key)
+        if buf is None:
+            buf = torch.zeros(KLP_GRPO_STEP_SCHED_BYTES // 8, dtype=torch.int64,
+                              device=torch.device("cuda", device_index))
+            _scheds[key] = buf
+        _scheds.move_to_end(key)
+        while len(_scheds) > _SCHED_KEEP:
+            _scheds.popitem(last=False)
+        return buf
+
+
 def grpo_step_launch(logits, targets, old, ref, adv, weight, params):
     """One klp_grpo_step call, no autograd: returns float32 ``logp``,
     ``entropy``, ``lse``, ``loss_tok`` ``[B, S]`` and ``d_logits`` (dense,
@@ -113,7 +143,7 @@ def grpo_step_launch(logits, targets, old, ref, adv, weight, params):
                                _ptr(targets), float(temperature), _ptr(old), _ptr(ref),
                                _ptr(adv), _ptr(weight), S, eps_low, eps_high, beta, per_token,
                                _ptr(logp), _ptr(ent), _ptr(lse), _ptr(loss_tok), _ptr(d_logits),
-                               stream)
+                               _ptr(_sched(dev.index, stream)), stream)
     check_status(rc)
     return logp, ent, lse, loss_tok, d_logits
 

@@ -273,8 +273,17 @@ int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp
  * and length are whole 16-byte vectors are supported (row starts 16-byte
  * aligned, vocab * element size a multiple of 16); anything else returns
  * KLP_EINVAL, and the caller runs klp_fwd / klp_grpo_fwd / klp_grpo_bwd /
- * klp_bwd instead.  No workspace.
+ * klp_bwd instead.
+ * sched (nullable): KLP_GRPO_STEP_SCHED_BYTES of device memory, 8-byte
+ * aligned, zero before the first call that gets it; every call leaves it
+ * zero.  With it, batches of many rows (8 or more per resident workgroup)
+ * run on persistent workgroups that take rows from a counter held there;
+ * without it, or for fewer rows, each row has a workgroup of its own.
+ * Results are the same bits either way.  Calls that share one must be
+ * ordered (one stream): concurrent calls on one counter skip rows.
  */
+#define KLP_GRPO_STEP_SCHED_BYTES 16
+
 int64_t klp_grpo_step_max_vocab(int dtype);
 
 int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
@@ -284,7 +293,7 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                   const float* tok_weight, int64_t seq_len,
                   float eps_low, float eps_high, float beta, int adv_per_token,
                   float* logprob, float* entropy, float* lse, float* loss_tok,
-                  void* d_logits, void* stream);
+                  void* d_logits, void* sched, void* stream);
 
 /*
  * data[i] *= *scale for i in [0, n), in place, on the stream: each element is

@@ -51,6 +51,14 @@ int klp_bwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
 void klp_default_config(int which, int dtype, int64_t n_rows, int64_t vocab,
                         int* waves, int* unroll, int* splits, int* flags);
 
+/*
+ * Fewest rows from which klp_grpo_step, given a `sched` counter, runs its
+ * persistent kernel on the current device for rows of `vocab` elements of
+ * `dtype` (temperature 1 or not: the two variants are separate kernels);
+ * -1 if the device cannot be queried, 0 for an unsupported dtype or vocab.
+ */
+int64_t klp_grpo_step_persistent_min_rows(int dtype, int64_t vocab, int scaled);
+
 #ifdef __cplusplus
 }
 #endif

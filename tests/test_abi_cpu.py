@@ -267,12 +267,12 @@ def test_grpo_step_validation_errors():
     def step(**kw):
         a = dict(logits=A, dtype=0, n=8, v=4096, ri=8, so=0, si=4096, tg=A, temp=1.0, old=A,
                  ref=None, adv=A, w=A, S=4, el=0.2, eh=0.28, beta=0.0, pt=0, lp=A, ent=A,
-                 lse=None, lt=A, d=A)
+                 lse=None, lt=A, d=A, sched=None)
         a.update(kw)
         return lib.klp_grpo_step(a["logits"], a["dtype"], a["n"], a["v"], a["ri"], a["so"],
                                  a["si"], a["tg"], a["temp"], a["old"], a["ref"], a["adv"],
                                  a["w"], a["S"], a["el"], a["eh"], a["beta"], a["pt"], a["lp"],
-                                 a["ent"], a["lse"], a["lt"], a["d"], None)
+                                 a["ent"], a["lse"], a["lt"], a["d"], a["sched"], None)
     assert step(n=0) == 0
     assert step(dtype=9) == KLP_EDTYPE
     assert step(temp=0.0) == KLP_EINVAL and "temperature" in _err()
@@ -291,6 +291,7 @@ def test_grpo_step_validation_errors():
     assert step(d=ctypes.c_void_p(0x100004)) == KLP_EINVAL and "d_logits" in _err()
     assert step(el=-1.0) == KLP_EINVAL and "eps_low" in _err()
     assert step(beta=float("inf")) == KLP_EINVAL and "beta" in _err()
+    assert step(sched=ctypes.c_void_p(0x100004)) == KLP_EINVAL and "sched" in _err()
     lib.klp_debug_fail_next_launches(1)
     try:
         assert step() == KLP_ELAUNCH and "grpo step" in _err()

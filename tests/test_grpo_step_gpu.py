@@ -389,3 +389,86 @@ def test_c2_matches_unfused_composition():
         return torch.where(v < 0, -mag, mag)
     ulps = (ordered(da) - ordered(db)).abs().max().item()
     assert ulps <= 1, f"d_logits up to {ulps} bf16 ulp from the unfused composition"
+
+
+def _step_abi(x, t, old, ref, adv, w, temperature, per_token, sched):
+    """klp_grpo_step through the C ABI with an explicit `sched` (None: one
+    workgroup per row); returns (logp, ent, lse, loss_tok, d_logits)."""
+    from kernel_opt import _C
+    from kernel_opt._library import DTYPE_CODES, check_status, lib
+    N, V = t.numel(), x.size(-1)
+    S = t.size(-1)
+    outs = [torch.full(t.shape, float("nan"), device=DEV) for _ in range(4)]
+    d = torch.full(x.shape, float("nan"), dtype=x.dtype, device=DEV)
+    P = lambda z: None if z is None else z.data_ptr()
+    st = torch.cuda.current_stream().cuda_stream
+    check_status(lib.klp_grpo_step(P(x), DTYPE_CODES[x.dtype], N, V, *_C.row_layout(x), P(t),
+                                   temperature, P(old), P(ref), P(adv), P(w), S, 0.2, 0.28,
+                                   0.04 if ref is not None else 0.0, per_token, *map(P, outs),
+                                   P(d), P(sched), st))
+    return (*outs, d)
+
+
+@pytest.mark.parametrize("dtype,B,S,V,temperature,per_token,with_ref,sliced", [
+    (torch.bfloat16, 5, 1024, 152064, 1.0, 0, True, False),    # the C2 vocabulary
+    (torch.bfloat16, 5, 1100, 100000, 0.7, 1, True, False),    # 16 vectors, a partial one;
+                                                               # temperature, per-token adv
+    (torch.bfloat16, 5, 1030, 155648, 1.3, 0, False, True),    # the row capacity, strided
+])
+def test_persistent_rows_match_one_row_per_workgroup(dtype, B, S, V, temperature, per_token,
+                                                     with_ref, sliced):
+    """With a `sched` counter and at least klp_grpo_step_persistent_min_rows
+    rows, klp_grpo_step runs persistent workgroups that claim rows from the
+    counter.  Every output equals, bit for bit, the one-workgroup-per-row
+    kernel's (sched = NULL) on the same inputs, including rows with -inf
+    logits and ignored targets (outputs start as NaN, so a row either kernel
+    skipped would show); the counter is left zero, and a second call on it
+    (fewer rows) again matches."""
+    from kernel_opt._library import KLP_GRPO_STEP_SCHED_BYTES, DTYPE_CODES, lib
+    print(f"persistent step: {dtype} {(B, S, V)} T={temperature}", flush=True)
+    min_rows = lib.klp_grpo_step_persistent_min_rows(DTYPE_CODES[dtype], V,
+                                                     int(temperature != 1.0))
+    assert min_rows > 0
+    assert B * S >= min_rows, (B * S, min_rows)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    full = (torch.randn(B, S + int(sliced), V, generator=g, device=DEV) * 2.0).to(dtype)
+    x = full[:, :S] if sliced else full
+    x[0, 3, ::5] = float("-inf")
+    x[1, 7, : V // 3] = float("-inf")
+    t = torch.randint(0, V, (B, S), generator=g, device=DEV)
+    t[0, 1] = IGNORE
+    t[1, 2] = V + 5
+    lp0 = torch.randn(B, S, generator=g, device=DEV) - 10.0
+    old = lp0 + 0.2 * torch.randn(B, S, generator=g, device=DEV)
+    ref = (lp0 + 0.2 * torch.randn(B, S, generator=g, device=DEV)) if with_ref else None
+    adv = torch.randn((B, S) if per_token else (B,), generator=g, device=DEV)
+    w = (torch.rand(B, S, generator=g, device=DEV) < 0.8).float() / (B * S)
+    sched = torch.zeros(KLP_GRPO_STEP_SCHED_BYTES, dtype=torch.uint8, device=DEV)
+    for rows in (B, B - 1):  # the second call: fewer rows, still above the threshold
+        assert rows * S >= min_rows
+        xs, ts = x[:rows], t[:rows]
+        olds, refs = old[:rows].contiguous(), None if ref is None else ref[:rows].contiguous()
+        advs, ws = adv[:rows].contiguous(), w[:rows].contiguous()
+        a = _step_abi(xs, ts, olds, refs, advs, ws, temperature, per_token, None)
+        b = _step_abi(xs, ts, olds, refs, advs, ws, temperature, per_token, sched)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(sched).item() == 0, "the counter was not left zero"
+        for name, u, v in zip(("logp", "entropy", "lse", "loss_tok", "d_logits"), a, b):
+            as_int = torch.int32 if u.dtype == torch.float32 else torch.int16
+            assert torch.equal(u.view(as_int), v.view(as_int)), name
+
+
+def test_persistent_rows_only_where_they_pay():
+    """The persistent kernel is used for bf16 rows of 16 or more 16-byte
+    vectors per thread (V > 98304), from 16 rows per resident workgroup on;
+    elsewhere the one-row kernel measured as fast or faster, and the query
+    reports 0."""
+    from kernel_opt._library import KLP_BF16, KLP_FP16, KLP_FP32, lib
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    for scaled in (0, 1):
+        for V in (100000, 152064, 155648):
+            assert lib.klp_grpo_step_persistent_min_rows(KLP_BF16, V, scaled) == 16 * n_cu
+        for dtype, V in ((KLP_BF16, 32000), (KLP_BF16, 98304), (KLP_FP16, 128256),
+                         (KLP_FP32, 77824)):
+            assert lib.klp_grpo_step_persistent_min_rows(dtype, V, scaled) == 0
+        assert lib.klp_grpo_step_persistent_min_rows(KLP_BF16, 155656, scaled) == 0
