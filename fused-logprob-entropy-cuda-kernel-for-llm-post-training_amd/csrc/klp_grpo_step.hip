@@ -29,6 +29,12 @@
 // Rows too long for the registers, or whose start or length is not a whole
 // number of 16-byte vectors, are rejected by the caller (KLP_EINVAL), which
 // then runs the unfused kernels.
+//
+// Two kernels run these steps: klp_grpo_step_kernel, one workgroup per row;
+// and, for large bf16 batches of long rows when the caller passes a row
+// counter, klp_grpo_step_rows_kernel, persistent workgroups that claim rows
+// from the counter and load the next row under the current row's pass 2.
+// Their outputs are the same bits.
 #include "klp_grpo_terms.h"
 #include "klp_launch.h"
 
