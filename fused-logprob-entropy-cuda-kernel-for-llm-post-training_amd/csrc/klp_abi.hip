@@ -94,6 +94,14 @@ bool injected_failure(const char* what) {
 
 int64_t body_vectors(int dtype, int64_t vocab) { return vocab / (16 / elem_bytes(dtype)); }
 
+// Bytes of the largest vector piece of a backward row in `splits` pieces (the
+// kernel rounds pieces up to 8 vectors); its buffer offsets are 32-bit, so
+// this must stay under 2 GiB.
+int64_t bwd_piece_bytes(int dtype, int64_t vocab, int64_t splits) {
+    const int64_t per = (body_vectors(dtype, vocab) + splits - 1) / splits;
+    return ((per + 7) & ~int64_t{7}) * 16;
+}
+
 klp::FwdConfig default_fwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     klp::FwdConfig c;
     c.unroll = 4;
@@ -153,6 +161,9 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
         if (e > kMaxSplits) e = kMaxSplits;
         if (e >= 1 && nvec / e >= tile - tile / 8) s = e;
     }
+    // Rows of more than 2 GiB per 64 pieces (never a real vocabulary) take
+    // more pieces.
+    while (s < 1024 && bwd_piece_bytes(dtype, vocab, s) > int64_t{INT32_MAX}) s *= 2;
     c.splits = static_cast<int>(s);
     return c;
 }
@@ -248,6 +259,11 @@ int bwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
         return fail(KLP_EINVAL,
                     "unsupported backward launch shape (waves=%d unroll=%d splits=%d flags=%d)",
                     cfg.waves, cfg.unroll, cfg.splits, cfg.flags);
+    if (bwd_piece_bytes(dtype, vocab, cfg.splits) > int64_t{INT32_MAX})
+        return fail(KLP_EINVAL,
+                    "backward row pieces must be under 2 GiB (vocab %lld in %d pieces): use "
+                    "more splits",
+                    static_cast<long long>(vocab), cfg.splits);
     if ((rc = check_grid(n_rows, cfg.splits, cfg.waves * 64)) != KLP_OK) return rc;
 
     klp::BwdParams p;

@@ -91,6 +91,15 @@ def test_workspace_and_launch_shape_errors():
     assert rc == KLP_EINVAL and "launch shape" in _err()
     rc = lib.klp_bwd(P, 0, 4, 100, 4, 0, 100, P, P, P, None, None, None, None, None)
     assert rc == KLP_EINVAL and "d_logits" in _err()
+    # The backward's row pieces are read with 32-bit buffer offsets: a bf16
+    # row of 2^30 logits in one piece is refused, not misread.
+    V = 1 << 30
+    rc = lib.klp_bwd_ex(P, 0, 1, V, 1, 0, V, P, P, P, None, None, None, P, 16, 2, 1, 1, None)
+    assert rc == KLP_EINVAL and "2 GiB" in _err()
+    w, u, sp, fl = (ctypes.c_int() for _ in range(4))
+    lib.klp_default_config(1, 0, 1, V, ctypes.byref(w), ctypes.byref(u), ctypes.byref(sp),
+                           ctypes.byref(fl))
+    assert sp.value >= 2  # the default keeps each piece under 2 GiB
 
 
 def test_injected_launch_failure_reports_elaunch():
