@@ -11,7 +11,9 @@
  * Conventions are those of kernel_opt_hip.h.  Supported shapes:
  * waves (wave64s per workgroup) in {1, 2, 4, 8, 16} for the forward and
  * {4, 8, 16} for the backward, unroll in {2, 4} (16-byte loads per thread per
- * iteration), splits in [1, 1024] (workgroups per row).
+ * iteration), splits in [1, 1024] (workgroups per row); the backward's row
+ * pieces (vocab / splits, rounded up to 8 16-byte vectors) must stay under
+ * 2 GiB (KLP_EINVAL otherwise).
  * `flags` selects kernel variants: forward: must be 0; backward: bit 0 =
  * non-temporal gradient stores.
  */
