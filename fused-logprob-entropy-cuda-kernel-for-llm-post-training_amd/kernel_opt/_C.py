@@ -28,7 +28,8 @@ import threading
 
 import torch
 
-from ._library import DTYPE_CODES, check_status, device_guard, lib, ptr, stream_handle
+from ._library import (DTYPE_CODES, capturing, check_status, device_guard, keep_for_capture, lib,
+                       ptr, stream_handle)
 
 __all__ = [
     "fused_logprob_entropy_naive",
@@ -99,9 +100,13 @@ _WS_KEEP = 16
 def _workspace(device_index: int, stream: int, nbytes: int):
     """The workspace of (device, raw stream handle) holding at least
     ``nbytes``; the device must be current and ``stream`` its current
-    stream."""
+    stream.  Under graph capture every call gets a workspace of its own, kept
+    for the life of the process: graphs captured on one stream would
+    otherwise share one and race when replayed concurrently."""
     if nbytes == 0:
         return None
+    if capturing():
+        return keep_for_capture(torch.empty(nbytes, dtype=torch.uint8, device=device_index))
     key = (device_index, stream)
     with _ws_lock:
         buf = _workspaces.get(key)

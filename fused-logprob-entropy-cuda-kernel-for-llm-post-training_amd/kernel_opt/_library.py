@@ -126,6 +126,24 @@ def device_guard(device_index: int):
     return torch.cuda.device(device_index)
 
 
+# Buffers allocated while a stream was being captured into a graph: the
+# graph bakes in their addresses, so they must outlive it.  They are kept for
+# the life of the process (one small buffer per captured call that needed
+# one).
+_capture_keepalive: list = []
+
+
+def capturing() -> bool:
+    """True while the current stream is being captured into a graph."""
+    return torch.cuda.is_current_stream_capturing()
+
+
+def keep_for_capture(buf):
+    """Keep ``buf`` alive for the life of the process and return it."""
+    _capture_keepalive.append(buf)
+    return buf
+
+
 def ptr(t):
     """Data pointer of ``t`` for a ``void*`` argument (``None`` -> NULL)."""
     return None if t is None else t.data_ptr()

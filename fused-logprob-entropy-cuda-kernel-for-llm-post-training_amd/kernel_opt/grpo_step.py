@@ -40,8 +40,8 @@ import numpy as np
 import torch
 
 from . import _C
-from ._library import (DTYPE_CODES, KLP_GRPO_STEP_SCHED_BYTES, check_status, device_guard, lib,
-                       ptr, stream_handle)
+from ._library import (DTYPE_CODES, KLP_GRPO_STEP_SCHED_BYTES, capturing, check_status,
+                       device_guard, keep_for_capture, lib, ptr, stream_handle)
 from .grpo import fused_grpo_loss
 from .ops import fused_logprob_entropy
 
@@ -100,7 +100,9 @@ def _fused_supported(logits: torch.Tensor, rows) -> bool:
 # zeroed once, when allocated on its stream, and every launch leaves it zero,
 # so launches on one stream can share it.  At most _SCHED_KEEP are kept,
 # least recently used dropped first (the caching allocator reuses a dropped
-# one only in its stream's order).
+# one only in its stream's order).  A call under graph capture gets a counter
+# of its own instead (kept for the life of the process): graphs captured on
+# one stream and replayed concurrently would otherwise race on a shared one.
 _sched_lock = threading.Lock()
 _scheds: collections.OrderedDict = collections.OrderedDict()
 _SCHED_KEEP = 16
@@ -109,6 +111,10 @@ _SCHED_KEEP = 16
 def _sched(device_index: int, stream: int) -> torch.Tensor:
     """The row counter of (device, stream); the device must be current and
     ``stream`` its current stream."""
+    if capturing():
+        # torch.zeros fills with a kernel, which a graph replays correctly.
+        return keep_for_capture(torch.zeros(KLP_GRPO_STEP_SCHED_BYTES // 8, dtype=torch.int64,
+                                            device=torch.device("cuda", device_index)))
     key = (device_index, stream)
     with _sched_lock:
         buf = _scheds.get(key)
@@ -214,6 +220,10 @@ def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch
     B, S, V = logits.shape
     if tuple(targets.shape) != (B, S):
         raise RuntimeError(f"targets has shape {tuple(targets.shape)}, expected {(B, S)}")
+    if targets.device != logits.device:
+        # Checked before either path is chosen: the fused kernel would
+        # otherwise read a host pointer as device memory.
+        raise RuntimeError(f"targets must be on {logits.device}, got {targets.device}")
     if importance_level not in ("token", "sequence"):
         raise ValueError(f"importance_level must be 'token' or 'sequence', got {importance_level!r}")
     t = 1.0 if temperature is None else float(temperature)
@@ -224,9 +234,14 @@ def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch
                    max_completion_length=max_completion_length, normalizer=normalizer)
 
     rows = _C.row_layout(logits)
-    if (importance_level != "token" or B * S == 0 or not targets.is_contiguous()
-            or targets.dtype != torch.int64 or not _fused_supported(logits, rows)):
+    wants_grad = torch.is_grad_enabled() and logits.requires_grad
+    if (not wants_grad or importance_level != "token" or B * S == 0
+            or not targets.is_contiguous() or targets.dtype != torch.int64
+            or not _fused_supported(logits, rows)):
         # The unfused composition: same loss, logp / entropy differentiable.
+        # It also serves calls that need no gradient (evaluation, logging,
+        # torch.no_grad()): the fused kernel would allocate and write a
+        # full [B, S, V] d_logits that nothing reads.
         logp, ent, _ = fused_logprob_entropy(logits, targets, temperature)
         loss, stats = fused_grpo_loss(logp, old_logp, advantages, mask, ref_logp, **loss_kw)
         return (loss, logp, ent, stats) if return_stats else (loss, logp, ent)

@@ -214,6 +214,58 @@ def test_autograd_op():
     assert torch.equal(xg2.grad, (d.float() * torch.tensor(0.3, device=DEV)).to(d.dtype))
 
 
+def test_host_targets_raise_before_any_launch(monkeypatch):
+    """targets in host memory raise RuntimeError before either path is chosen
+    (the fused kernel would read the host pointer as device memory).  The
+    kernel's entry point is replaced by a stub that fails, so that no kernel
+    can launch even if the check regressed."""
+    ko = _ko()
+    from kernel_opt import grpo_step as gs
+
+    def no_launch(*args, **kwargs):
+        raise AssertionError("klp_grpo_step was called with host targets")
+    monkeypatch.setattr(gs.lib, "klp_grpo_step", no_launch)
+    B, S, V = 2, 3, 4096
+    x, t, mask, adv = make_case(B, S, V, torch.bfloat16, 31)
+    xg = x.to(DEV).requires_grad_(True)
+    old = torch.full((B, S), -9.0, device=DEV)
+    with pytest.raises(RuntimeError, match="targets must be on"):
+        ko.fused_grpo_step(xg, t, old, adv.to(DEV), mask.to(DEV))
+
+
+@pytest.mark.parametrize("mode", ["no_grad", "leaf_without_grad"])
+def test_call_without_gradient_writes_no_d_logits(mode):
+    """Under torch.no_grad(), or for logits that do not require a gradient,
+    fused_grpo_step runs the forward composition: peak memory stays below one
+    [B, S, V] buffer (the fused kernel would write a full d_logits), and the
+    loss equals the composition's."""
+    ko = _ko()
+    B, S, V = 4, 64, 152064
+    print(f"grpo step without gradient: {mode}", flush=True)
+    x, t, mask, adv = make_case(B, S, V, torch.bfloat16, 32)
+    x, t, mask, adv = x.to(DEV), t.to(DEV), mask.to(DEV), adv.to(DEV)
+    if mode == "no_grad":
+        x.requires_grad_(True)
+    old = torch.full((B, S), -11.0, device=DEV)
+    kw = dict(eps_low=0.2, eps_high=0.28, loss_type="grpo")
+    ko.fused_grpo_step(x.detach(), t, old, adv, mask, **kw)  # warm caches and workspaces
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    if mode == "no_grad":
+        with torch.no_grad():
+            loss, lp, _ = ko.fused_grpo_step(x, t, old, adv, mask, **kw)
+    else:
+        loss, lp, _ = ko.fused_grpo_step(x, t, old, adv, mask, **kw)
+    torch.cuda.synchronize()
+    extra = torch.cuda.max_memory_allocated() - base
+    assert extra < x.numel() * x.element_size() // 4, f"{extra} bytes allocated"
+    with torch.no_grad():
+        lpb, _, _ = ko.fused_logprob_entropy_forward(x, t)
+        lb, _ = ko.fused_grpo_loss(lpb, old, adv, mask, **kw)
+    assert torch.equal(loss, lb) and torch.equal(lp, lpb)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_scale_by_upstream(dtype):
     """klp_scale_inplace (through scale_by_upstream), which applies the loss's
