@@ -6,26 +6,41 @@ the fused kernels over that batch, through the library's C ABI (via
 kernel_opt._C), with inputs resident in HBM.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2]
-                    [--no-cpu-baseline] [--flush]
+                    [--no-cpu-baseline] [--core-only] [--sweep OUT.md]
+    python bench.py --trace-from DIR [--config C2]          # rocprofv3 kernel trace -> markdown
+    python bench.py --traffic-from FETCH_DIR WRITE_DIR      # rocprofv3 counters -> markdown
 
 Prints ONE JSON line.  `value` = achieved algorithmic HBM bandwidth over the
-whole step (fwd bytes + bwd bytes) / (fwd + bwd time), in TB/s.
+step (fwd bytes + bwd bytes) / `ms_per_step`, in TB/s.
 
 Algorithmic bytes per launch (s = bytes per logit, N rows, V vocab):
     forward  = N*V*s + 8N (targets) + 12N (logp, entropy, lse)
     backward = 2*N*V*s + 8N (targets) + 16N (lse, entropy, g_logp, g_ent)
 (g_lse is None in these workloads, so it is not read.)
 
-Timing (HIP events on the stream the kernels run on): `ms_per_step` is one
-event pair around K interleaved forward+backward steps, divided by K; the
-per-kernel `fwd_ms` / `bwd_ms` are one event pair around K back-to-back
-launches of that kernel, divided by K.  With --flush a 1 GiB buffer is read
-(or, with --flush-mode write, overwritten) before every launch and each
-launch is timed on its own.  The
-roofline object reports the dominant kernel, the backward (it moves twice the
-forward's bytes); `traffic` is the HBM bytes per launch that rocprofv3's
-FETCH_SIZE / WRITE_SIZE counters measured for that launch shape, scaled by
-their readings for a plain copy of known size (MEASURED_TRAFFIC below).
+Timing, all with HIP events on the stream the kernels run on:
+  * `ms_per_step`: one event pair around K interleaved forward+backward steps
+    (the backward re-reads logits the forward has just streamed through the
+    256 MB Infinity Cache, so the step can beat the per-kernel rates);
+  * `fwd_ms` / `bwd_ms`: one event pair around K back-to-back launches;
+  * `fwd_ms_flushed` / `bwd_ms_flushed`: each of K launches timed on its own
+    after a 1 GiB buffer was read (which evicts the logits from the cache);
+  * `ceilings`: in the same process, at the same size and launch shape, the
+    library's calibration kernels (klp_ceiling_read: the forward's loads
+    without arithmetic; klp_ceiling_copy: the backward's loads and stores)
+    and torch's device copy, warm and flushed; `fwd_over_read` and
+    `bwd_over_copy` are the kernels' times over them.
+`roofline` reports the dominant kernel, the backward (it moves twice the
+forward's bytes), at the lower of its warm and flushed rates.  `traffic` is
+the HBM bytes per launch from a committed rocprofv3 counter summary under
+profiles/ (made by --traffic-from) whose build id equals this build's (a hash
+of the library sources); null when none matches.
+
+`autograd` times the drop-in path (kernel_opt.fused_logprob_entropy and
+loss.backward(), as the reference's bench/bench_backward.py:45-53 does) and
+reports the bytes each allocates beyond its outputs (the reference's method,
+bench/bench_micro.py:62-78).  `C1` is the BASELINE's CPU-runnable config on
+the GPU and on the CPU eager path.
 
 The cpu_baseline leg times the reference's CPU eager path (TRL
 selective_log_softmax + entropy_from_logits forward, restated in
@@ -36,14 +51,19 @@ second) on this machine's cores.
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
+import hashlib
 import json
 import math
 import os
+import re
 import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.join(ROOT, "fused-logprob-entropy-cuda-kernel-for-llm-post-training_amd")
+PROFILES_DIR = os.path.join(ROOT, "profiles")
 for _p in (PKG_DIR, ROOT):
     if _p not in sys.path:
         sys.path.insert(0, _p)
@@ -52,23 +72,25 @@ import torch  # noqa: E402
 
 HBM_PEAK_TBPS = 8.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+FLUSH_BYTES = 1 << 30
 
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
-# each scaled by the counter's reading for a plain copy of known size
-# (profiles/klp_all_configs_hbm_traffic.md).  Keyed by workload, kernel and
-# launch shape (waves, unroll, splits, flags); reported only for that shape.
-MEASURED_TRAFFIC = {
-    ("C1", "fwd", (16, 4, 1, 0)): 32960385,
-    ("C1", "bwd", (16, 2, 4, 1)): 65711874,
-    ("C2", "fwd", (4, 4, 1, 0)): 311758388,
-    ("C2", "bwd", (16, 2, 8, 1)): 623290575,
-    ("C3", "fwd", (4, 4, 1, 0)): 2103303576,
-    ("C3", "bwd", (16, 2, 8, 1)): 4205676181,
-    ("C4", "fwd", (4, 4, 1, 0)): 9964861906,
-    ("C4", "bwd", (16, 2, 10, 1)): 19926260879,
-    ("C5", "fwd", (4, 4, 1, 0)): 8592967390,
-    ("C5", "bwd", (16, 2, 32, 1)): 17183261794,
-}
+
+def build_id() -> str:
+    """Hash of the library's sources (kernels, headers, Makefile): the same
+    sources build the same kernels, so a profile made from them describes
+    this build."""
+    paths = (glob.glob(os.path.join(PKG_DIR, "csrc", "*")) +
+             glob.glob(os.path.join(ROOT, "include", "*.h")) + [os.path.join(PKG_DIR, "Makefile")])
+    h = hashlib.sha256()
+    for path in sorted(paths):
+        h.update(os.path.relpath(path, ROOT).encode())
+        h.update(b"\0")
+        with open(path, "rb") as f:
+            h.update(f.read())
+        h.update(b"\0")
+    return h.hexdigest()[:16]
+
+
 ROW_BLOCK = 256  # rows per seeded generator block
 
 # BASELINE.json configs.  Seeds are per config; each block of ROW_BLOCK rows
@@ -169,6 +191,222 @@ def algorithmic_bytes(n_rows: int, vocab: int, elem_bytes: int):
     fwd = n_rows * vocab * elem_bytes + 8 * n_rows + 12 * n_rows
     bwd = 2 * n_rows * vocab * elem_bytes + 8 * n_rows + 16 * n_rows
     return fwd, bwd
+
+
+def ceiling_row_bytes(vocab: int, elem_bytes: int) -> int:
+    """Row size of the calibration kernels' buffer: the logits row rounded up
+    to whole 16-byte vectors."""
+    return (vocab * elem_bytes + 15) // 16 * 16
+
+
+# ---------------------------------------------------------------------------
+# rocprofv3 output -> committed summaries (profiles/), and back.
+#
+# A summary is markdown for the reader plus one machine-readable line,
+#   <!-- klp-profile {...json...} -->
+# carrying the build id, the workload and the per-kernel figures.  The
+# default bench run looks up the summaries of its own build id and workload
+# for `roofline.traffic` and for the trace cross-check.
+# ---------------------------------------------------------------------------
+PROFILE_TAG = "klp-profile"
+
+
+def _rocprof_csv(directory: str, suffix: str):
+    hits = sorted(glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True))
+    if not hits:
+        raise FileNotFoundError(f"no *{suffix} under {directory}")
+    rows = []
+    for path in hits:
+        with open(path, newline="") as f:
+            rows.extend(csv.DictReader(f))
+    return rows
+
+
+def short_kernel(name: str) -> str:
+    """'void klp::klp_bwd_kernel<0, 16, 2, true, false>(klp::BwdParams)' ->
+    'klp_bwd_kernel<0, 16, 2, true, false>'; other names unchanged up to
+    the argument list."""
+    m = re.match(r"(?:void )?(?:klp::)?([A-Za-z_0-9]+(?:<[^()]*>)?)", name)
+    return m.group(1) if m else name
+
+
+def _is_klp(name: str) -> bool:
+    return "klp::" in name
+
+
+def _workload_sizes(config: str):
+    cfg = CONFIGS[config]
+    B, S, V = cfg["shape"]
+    esz = torch.empty((), dtype=cfg["dtype"]).element_size()
+    return B * S, V, esz
+
+
+def kernel_bytes(short: str, config: str):
+    """Algorithmic bytes of one launch of a klp kernel of `config`'s
+    workload, or None for kernels without a stated figure."""
+    N, V, esz = _workload_sizes(config)
+    fb, bb = algorithmic_bytes(N, V, esz)
+    rb = ceiling_row_bytes(V, esz) * N
+    if short.startswith("klp_fwd_kernel"):
+        return fb
+    if short.startswith("klp_bwd_kernel"):
+        return bb
+    if short.startswith("klp_ceiling_read"):
+        return rb
+    if short.startswith("klp_ceiling_copy"):
+        return 2 * rb
+    return None
+
+
+def _profile_line(data: dict) -> str:
+    return f"<!-- {PROFILE_TAG} {json.dumps(data, sort_keys=True)} -->"
+
+
+def load_profiles(kind: str, config: str, bid: str):
+    """Machine-readable data of the committed summaries of `kind` ("traffic"
+    or "trace") for `config` made from build `bid`."""
+    out = []
+    for path in sorted(glob.glob(os.path.join(PROFILES_DIR, "*.md"))):
+        with open(path) as f:
+            for line in f:
+                line = line.strip()
+                if line.startswith(f"<!-- {PROFILE_TAG} ") and line.endswith("-->"):
+                    data = json.loads(line[len(PROFILE_TAG) + 5:-3])
+                    if (data.get("kind") == kind and data.get("config") == config
+                            and data.get("build_id") == bid):
+                        data["file"] = os.path.relpath(path, ROOT)
+                        out.append(data)
+    return out
+
+
+def _git_head() -> str | None:
+    try:
+        import subprocess
+        return subprocess.run(["git", "-C", ROOT, "rev-parse", "--short=12", "HEAD"],
+                              capture_output=True, text=True, check=True).stdout.strip()
+    except Exception:
+        return None
+
+
+def summarize_traffic(fetch_dir: str, write_dir: str, config: str, command: str = ""):
+    """Per-dispatch HBM bytes of the klp kernels from two rocprofv3 --pmc
+    runs (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by what the
+    same counter reads for klp_ceiling_copy_kernel, whose reads and writes are
+    known (N rows of the logits' size each way).  Returns (markdown, data)."""
+    N, V, esz = _workload_sizes(config)
+    copy_bytes = ceiling_row_bytes(V, esz) * N
+    per = {}
+    for counter, directory in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        for r in _rocprof_csv(directory, "counter_collection.csv"):
+            if r["Counter_Name"] != counter or not _is_klp(r["Kernel_Name"]):
+                continue
+            d = per.setdefault(short_kernel(r["Kernel_Name"]), {})
+            d.setdefault(counter, []).append(float(r["Counter_Value"]))
+    cal = [k for k in per if k.startswith("klp_ceiling_copy")]
+    if not cal:
+        raise RuntimeError("no klp_ceiling_copy_kernel dispatch: the calibration is missing")
+    cd = per[cal[0]]
+    f_fetch = copy_bytes / (1024 * sum(cd["FETCH_SIZE"]) / len(cd["FETCH_SIZE"]))
+    f_write = copy_bytes / (1024 * sum(cd["WRITE_SIZE"]) / len(cd["WRITE_SIZE"]))
+    kernels = {}
+    rows = []
+    for k in sorted(per):
+        d = per[k]
+        if "FETCH_SIZE" not in d or "WRITE_SIZE" not in d:
+            continue
+        fe = sum(d["FETCH_SIZE"]) / len(d["FETCH_SIZE"])
+        wr = sum(d["WRITE_SIZE"]) / len(d["WRITE_SIZE"])
+        traffic = int(round(1024 * (fe * f_fetch + wr * f_write)))
+        alg = kernel_bytes(k, config)
+        kernels[k] = {"dispatches": len(d["FETCH_SIZE"]), "fetch_kib": round(fe, 1),
+                      "write_kib": round(wr, 1), "traffic_bytes": traffic,
+                      "algorithmic_bytes": alg,
+                      "ratio": None if not alg else round(traffic / alg, 4)}
+        rows.append(f"| `{k}` | {len(d['FETCH_SIZE'])} | {fe:.1f} | {wr:.1f} | {traffic} | "
+                    f"{alg if alg else '-'} | {kernels[k]['ratio'] or '-'} |")
+    bid = build_id()
+    data = {"kind": "traffic", "config": config, "build_id": bid, "git_head": _git_head(),
+            "fetch_factor": round(f_fetch, 5), "write_factor": round(f_write, 5),
+            "kernels": kernels}
+    md = [f"# rocprofv3 HBM counters: klp kernels, workload {config}", "",
+          f"Build id `{bid}` (hash of the library sources, as `bench.py` computes it); "
+          f"summarised at git `{data['git_head']}` by `python bench.py --traffic-from "
+          f"{fetch_dir} {write_dir} --config {config}`.", ""]
+    if command:
+        md += ["Commands (MI355X):", "```", command, "```", ""]
+    md += ["Calibration: `klp_ceiling_copy_kernel` reads and writes exactly "
+           f"{copy_bytes} bytes per launch. Scale factors (known bytes / counter bytes): "
+           f"FETCH_SIZE x{f_fetch:.5f}, WRITE_SIZE x{f_write:.5f}.", "",
+           "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic bytes | "
+           "algorithmic bytes | traffic / algorithmic |", "|---|---:|---:|---:|---:|---:|---:|"]
+    md += rows + ["", _profile_line(data), ""]
+    return "\n".join(md), data
+
+
+def _phase(prev: str | None, name: str) -> str:
+    if prev is None:
+        return "other"
+    if "reduce_kernel" in prev:
+        return "flushed"
+    if prev == name:
+        return "back to back"
+    if _is_klp(prev):
+        return "after another klp kernel"
+    return "other"
+
+
+def summarize_trace(trace_dir: str, config: str, command: str = ""):
+    """Average kernel durations of the klp kernels from a rocprofv3
+    --kernel-trace run, overall and per phase of bench.py (a launch right
+    after the 1 GiB flush read: "flushed"; after a launch of the same kernel:
+    "back to back"; after the other klp kernel: the interleaved step).
+    Returns (markdown, data)."""
+    rows = _rocprof_csv(trace_dir, "kernel_trace.csv")
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    stats = {}
+    prev = None
+    for r in rows:
+        name = r["Kernel_Name"]
+        if _is_klp(name):
+            k = short_kernel(name)
+            dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            ph = _phase(prev, name)
+            stats.setdefault(k, {}).setdefault("all", []).append(dur)
+            stats[k].setdefault(ph, []).append(dur)
+        prev = name
+    kernels = {}
+    lines = []
+    for k in sorted(stats):
+        alg = kernel_bytes(k, config)
+        kernels[k] = {}
+        for ph in ("all", "back to back", "flushed", "after another klp kernel", "other"):
+            ds = stats[k].get(ph)
+            if not ds:
+                continue
+            avg = sum(ds) / len(ds)
+            med = sorted(ds)[len(ds) // 2]
+            tb = None if not alg else alg / (avg * 1e-9) / 1e12
+            kernels[k][ph] = {"n": len(ds), "avg_ns": round(avg, 1), "median_ns": med,
+                              "min_ns": min(ds), "max_ns": max(ds),
+                              "tbps": None if tb is None else round(tb, 4)}
+            lines.append(f"| `{k}` | {ph} | {len(ds)} | {avg / 1e3:.2f} | {med / 1e3:.2f} | "
+                         f"{min(ds) / 1e3:.2f} | {max(ds) / 1e3:.2f} | "
+                         f"{'-' if tb is None else f'{tb:.3f} ({100 * tb / HBM_PEAK_TBPS:.1f}%)'} |")
+    bid = build_id()
+    data = {"kind": "trace", "config": config, "build_id": bid, "git_head": _git_head(),
+            "kernels": kernels}
+    md = [f"# rocprofv3 kernel trace: klp kernels, workload {config}", "",
+          f"Build id `{bid}` (hash of the library sources, as `bench.py` computes it); "
+          f"summarised at git `{data['git_head']}` by `python bench.py --trace-from "
+          f"{trace_dir} --config {config}`.", ""]
+    if command:
+        md += ["Command (MI355X):", "```", command, "```", ""]
+    md += ["TB/s = algorithmic bytes per launch / average duration (forward "
+           "N*V*s + 20N, backward 2*N*V*s + 24N, calibration kernels their buffer bytes).", "",
+           "| kernel | phase | launches | avg us | median us | min us | max us | TB/s (% of 8) |",
+           "|---|---|---:|---:|---:|---:|---:|---:|"]
+    md += lines + ["", _profile_line(data), ""]
+    return "\n".join(md), data
 
 
 # ---------------------------------------------------------------------------
@@ -532,46 +770,66 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
     return out
 
 
-def main(argv=None):
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
-    ap.add_argument("--flush", action="store_true",
-                    help="run through a 1 GiB buffer before every launch (cold Infinity Cache)")
-    ap.add_argument("--flush-mode", choices=("read", "write"), default="read",
-                    help="read: sum the buffer (evicts with clean lines); write: fill it "
-                         "(leaves up to the cache size of dirty lines for the next kernel)")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=1024,
-                    help="rows of the workload the CPU baseline times (whole batch elements)")
-    ap.add_argument("--fwd-config", default=None, help="waves,unroll,splits,flags")
-    ap.add_argument("--bwd-config", default=None, help="waves,unroll,splits,flags")
-    ap.add_argument("--no-lmhead", action="store_true",
-                    help="skip the fused LM-head timing (klp_lmh_* against matmul + logprob)")
-    ap.add_argument("--no-shard", action="store_true",
-                    help="skip the vocab-shard timing (one rank's share of C4 under 8-way "
-                         "vocab parallelism)")
-    ap.add_argument("--no-grpo", action="store_true",
-                    help="skip the GRPO timings (the loss kernels against the eager chain, "
-                         "the fused step against the unfused kernels)")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run torch's copy of a buffer the size of the logits (known "
-                         "traffic, for scaling HBM counters)")
-    args = ap.parse_args(argv)
+# ---------------------------------------------------------------------------
+# The core measurement
+# ---------------------------------------------------------------------------
+class Timer:
+    """HIP-event timing on one stream, with an optional Infinity-Cache flush
+    (reading, or with mode "write" overwriting, a 1 GiB buffer) before each
+    launch."""
 
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(rows are independent, so data-parallel ranks would each run this same "
-              "kernel on their own batch with no exchange)", file=sys.stderr)
-        return 2
+    def __init__(self, dev, K, flush_mode="read"):
+        self.stream = torch.cuda.current_stream(dev)
+        self.K = K
+        self.flush_mode = flush_mode
+        self.buf = torch.ones(FLUSH_BYTES, dtype=torch.uint8, device=dev)
 
+    def b2b(self, body):
+        """Average ms of `body` over K back-to-back calls: one event pair
+        around the whole loop."""
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(self.stream)
+        for _ in range(self.K):
+            body()
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / self.K
+
+    def flush(self, k=0):
+        if self.flush_mode == "read":
+            self.buf.view(torch.int64).sum()
+        else:
+            self.buf.fill_(k & 0xFF)
+
+    def flushed(self, body):
+        """(mean, median) ms of `body` over K calls, each timed on its own
+        right after a flush."""
+        ts = []
+        for k in range(self.K):
+            self.flush(k)
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(self.stream)
+            body()
+            b.record(self.stream)
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return sum(ts) / len(ts), sorted(ts)[len(ts) // 2]
+
+
+def _tbps(nbytes, ms):
+    return nbytes / (ms * 1e-3) / 1e12
+
+
+def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None):
+    """Forward / backward of workload `name` through the C ABI: the timed
+    step loop, back-to-back and flushed per-kernel times, and the same-run
+    read / copy ceilings at the kernels' size and launch shapes."""
     from kernel_opt import _C
+    from kernel_opt._library import check_status, lib
 
-    assert torch.cuda.is_available(), "bench.py needs a GPU"
-    dev = torch.device("cuda:0")
-    name = args.config
     cfg = CONFIGS[name]
     inp = make_inputs(name, dev)
     logits, targets = inp["logits"], inp["targets"]
@@ -583,9 +841,6 @@ def main(argv=None):
     ent = torch.empty_like(logp)
     lse = torch.empty_like(logp)
     d_logits = torch.empty(logits.shape, dtype=logits.dtype, device=dev)
-    fcfg = tuple(int(v) for v in args.fwd_config.split(",")) if args.fwd_config else None
-    bcfg = tuple(int(v) for v in args.bwd_config.split(",")) if args.bwd_config else None
-    flush_buf = torch.ones(1 << 30, dtype=torch.uint8, device=dev) if args.flush else None
 
     def fwd():
         _C.fwd_launch(logits, targets, logp, ent, lse, config=fcfg)
@@ -593,73 +848,340 @@ def main(argv=None):
     def bwd():
         _C.bwd_launch(logits, targets, lse, ent, g_logp, g_ent, None, d_logits, config=bcfg)
 
-    stream = torch.cuda.current_stream(dev)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         fwd()
         bwd()
-    if args.copy_calibration:
-        src = logits if logits.is_contiguous() else logits.contiguous()
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        del dst
     torch.cuda.synchronize()
 
-    K = args.steps
+    t_wall0 = time.perf_counter()
+    # the timed steps: forward then backward, repeated, as a training loop runs them
+    step_ms = timer.b2b(lambda: (fwd(), bwd()))
+    t_wall = time.perf_counter() - t_wall0
+    fwd_ms = timer.b2b(fwd)
+    bwd_ms = timer.b2b(bwd)
+    fwd_fl, fwd_fl_med = timer.flushed(fwd)
+    bwd_fl, bwd_fl_med = timer.flushed(bwd)
 
-    def timed_loop(body):
-        """Average ms of `body` over K back-to-back calls: one event pair on
-        the stream the kernels run on, around the whole loop."""
+    fwd_used = tuple(fcfg) if fcfg else _C.default_config("fwd", logits.dtype, N, V)
+    bwd_used = tuple(bcfg) if bcfg else _C.default_config("bwd", logits.dtype, N, V)
+
+    # Calibration kernels over a buffer of the logits' size (the logits
+    # themselves when their rows are whole contiguous 16-byte vectors), with
+    # the kernels' launch shapes; the copy writes into d_logits.
+    rb = ceiling_row_bytes(V, esz)
+    if logits.is_contiguous() and (V * esz) % 16 == 0:
+        src = logits
+    else:
+        src = torch.empty(N * rb, dtype=torch.uint8, device=dev)
+    dst = d_logits if d_logits.numel() * esz >= N * rb else torch.empty(N * rb, dtype=torch.uint8,
+                                                                        device=dev)
+    sink = torch.zeros(N * max(fwd_used[2], 1), dtype=torch.int32, device=dev)
+    st = timer.stream.cuda_stream
+    fw, fu, fs, _ = fwd_used
+    bw, bu, bs, _ = bwd_used
+
+    def ceil_read():
+        check_status(lib.klp_ceiling_read(src.data_ptr(), N, rb, fw, fu, fs, sink.data_ptr(),
+                                          0x9E3779B9, st))
+
+    def ceil_copy():
+        check_status(lib.klp_ceiling_copy(src.data_ptr(), dst.data_ptr(), N, rb, bw, bu, bs,
+                                          st))
+
+    tsrc = src.view(-1)[:N * rb // src.element_size()] if src is logits else src
+    tdst = dst.view(-1)[:tsrc.numel()] if dst.dtype == tsrc.dtype else None
+
+    def torch_copy():
+        tdst.copy_(tsrc)
+
+    for fn in (ceil_read, ceil_copy):
+        fn()
+    ceil = {"read_ms": timer.b2b(ceil_read), "copy_ms": timer.b2b(ceil_copy)}
+    ceil["read_ms_flushed"], _ = timer.flushed(ceil_read)
+    ceil["copy_ms_flushed"], _ = timer.flushed(ceil_copy)
+    if tdst is not None:
+        torch_copy()
+        ceil["torch_copy_ms"] = timer.b2b(torch_copy)
+        ceil["torch_copy_ms_flushed"], _ = timer.flushed(torch_copy)
+    del sink
+    if dst is not d_logits:
+        del dst
+    fb, bb = algorithmic_bytes(N, V, esz)
+    rbytes = N * rb
+    out_ceil = {
+        "read_kernel": f"klp_ceiling_read, launch {dict(zip(('waves', 'unroll', 'splits'), fwd_used[:3]))}",
+        "copy_kernel": f"klp_ceiling_copy, launch {dict(zip(('waves', 'unroll', 'splits'), bwd_used[:3]))}",
+        "buffer_bytes": rbytes,
+    }
+    for k, v in ceil.items():
+        out_ceil[k] = round(v, 5)
+        nbytes = rbytes if k.startswith("read") else 2 * rbytes
+        out_ceil[k.replace("_ms", "_tbps")] = round(_tbps(nbytes, v), 4)
+    out_ceil["fwd_over_read"] = round(fwd_ms / ceil["read_ms"], 4)
+    out_ceil["bwd_over_copy"] = round(bwd_ms / ceil["copy_ms"], 4)
+    out_ceil["fwd_over_read_flushed"] = round(fwd_fl / ceil["read_ms_flushed"], 4)
+    out_ceil["bwd_over_copy_flushed"] = round(bwd_fl / ceil["copy_ms_flushed"], 4)
+    return dict(inputs=inp, logits=logits, targets=targets, g_logp=g_logp, g_ent=g_ent,
+                N=N, V=V, esz=esz, fb=fb, bb=bb, step_ms=step_ms, wall=t_wall, fwd_ms=fwd_ms,
+                bwd_ms=bwd_ms, fwd_fl=fwd_fl, fwd_fl_med=fwd_fl_med, bwd_fl=bwd_fl,
+                bwd_fl_med=bwd_fl_med, fwd_used=fwd_used, bwd_used=bwd_used, ceilings=out_ceil,
+                d_logits=d_logits)
+
+
+def autograd_timing(dev, K, logits, targets, g_logp, g_ent):
+    """The drop-in path: kernel_opt.fused_logprob_entropy forward and
+    loss.backward() through its autograd op, timed and with their
+    allocations measured as the reference does (bench/bench_micro.py:62-78:
+    peak allocated during the calls minus allocated before;
+    bench/bench_backward.py:39-56: events around loss.backward()).
+    `*_transient_bytes` is the part of the peak not held after the call
+    (intermediates); the backward's held bytes are the gradient itself."""
+    from kernel_opt import fused_logprob_entropy
+    x = logits.detach().requires_grad_(True)
+    gl, ge = g_logp.view(targets.shape), g_ent.view(targets.shape)
+
+    def loss_of(lp, ent):
+        return (lp * gl + ent * ge).sum()
+
+    for _ in range(3):
+        x.grad = None
+        lp, ent, _ = fused_logprob_entropy(x, targets)
+        loss_of(lp, ent).backward()
+    x.grad = None
+    del lp, ent
+    torch.cuda.synchronize()
+
+    # forward: allocation of one call, then timing over K calls
+    pre = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    outs = fused_logprob_entropy(x, targets)
+    torch.cuda.synchronize()
+    fwd_peak = torch.cuda.max_memory_allocated() - pre
+    fwd_held = torch.cuda.memory_allocated() - pre
+    out_bytes = sum(o.numel() * o.element_size() for o in outs)
+    del outs
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    for i in range(K):
+        starts[i].record()
+        o = fused_logprob_entropy(x, targets)
+        ends[i].record()
+        del o
+    torch.cuda.synchronize()
+    fwd_t = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
+
+    # backward: allocation of one call, then timing over K calls
+    lp, ent, _ = fused_logprob_entropy(x, targets)
+    loss = loss_of(lp, ent)
+    torch.cuda.synchronize()
+    pre = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    loss.backward()
+    torch.cuda.synchronize()
+    bwd_peak = torch.cuda.max_memory_allocated() - pre
+    bwd_held = torch.cuda.memory_allocated() - pre
+    grad_bytes = x.grad.numel() * x.grad.element_size()
+    x.grad = None
+    bts = []
+    for i in range(K):
+        lp, ent, _ = fused_logprob_entropy(x, targets)
+        loss = loss_of(lp, ent)
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        loss.backward()
+        b.record()
+        x.grad = None
         torch.cuda.synchronize()
-        a.record(stream)
-        for _ in range(K):
-            body()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / K
+        bts.append(a.elapsed_time(b))
+    bts.sort()
+    return {
+        "fwd_ms_median": round(fwd_t[len(fwd_t) // 2], 5),
+        "bwd_ms_median": round(bts[len(bts) // 2], 5),
+        "fwd_peak_bytes": fwd_peak, "fwd_output_bytes": out_bytes,
+        "fwd_transient_bytes": fwd_peak - fwd_held,
+        "bwd_peak_bytes": bwd_peak, "bwd_grad_bytes": grad_bytes,
+        "bwd_transient_bytes": bwd_peak - bwd_held,
+        "bwd_peak_beyond_grad_bytes": bwd_peak - grad_bytes,
+        "note": "kernel_opt.fused_logprob_entropy and loss.backward() from Python, events per "
+                "call (median of K); loss = sum(logp*g_logp + entropy*g_ent); peak = max "
+                "allocated during one call minus allocated before it",
+    }
 
-    def flush(k):
-        if args.flush_mode == "read":
-            flush_buf.view(torch.int64).sum()
-        else:
-            flush_buf.fill_(k & 0xFF)
 
-    def timed_each(fn):
-        """Per-launch ms with the Infinity Cache flushed before each launch."""
-        ts = []
-        for k in range(K):
-            flush(k)
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            fn()
-            b.record(stream)
-            torch.cuda.synchronize()
-            ts.append(a.elapsed_time(b))
-        return sum(ts) / K
+def c1_leg(dev, K, timer, with_cpu):
+    """BASELINE config C1 (fp32 [2, 128, 32000]): GPU forward / backward
+    (back to back through the C ABI) and the CPU eager path on the whole
+    batch."""
+    from kernel_opt import _C
+    inp = make_inputs("C1", dev)
+    x, t = inp["logits"], inp["targets"]
+    gl, ge = inp["g_logp"].contiguous(), inp["g_ent"].contiguous()
+    lp, ent, lse = (torch.empty(t.shape, dtype=torch.float32, device=dev) for _ in range(3))
+    d = torch.empty_like(x)
+    V = x.size(-1)
+    N = x.numel() // V
+    fb, bb = algorithmic_bytes(N, V, 4)
 
-    t_wall0 = time.perf_counter()
-    if flush_buf is None:
-        # the step as a training loop runs it: forward then backward, repeated
-        step_ms = timed_loop(lambda: (fwd(), bwd()))
-        # each kernel on its own, launched back to back
-        fwd_avg = timed_loop(fwd)
-        bwd_avg = timed_loop(bwd)
-    else:
-        fwd_avg = timed_each(fwd)
-        bwd_avg = timed_each(bwd)
-        step_ms = fwd_avg + bwd_avg
-    t_wall = time.perf_counter() - t_wall0
-    fb, bb = algorithmic_bytes(N, V, esz)
-    fwd_tbps = fb / (fwd_avg * 1e-3) / 1e12
-    bwd_tbps = bb / (bwd_avg * 1e-3) / 1e12
-    step_tbps = (fb + bb) / (step_ms * 1e-3) / 1e12
+    def fwd():
+        _C.fwd_launch(x, t, lp, ent, lse)
+
+    def bwd():
+        _C.bwd_launch(x, t, lse, ent, gl, ge, None, d)
+
+    for _ in range(5):
+        fwd()
+        bwd()
+    f_ms, b_ms = timer.b2b(fwd), timer.b2b(bwd)
+    out = {"workload": "C1: logits [2,128,32000] float32", "fwd_us": round(f_ms * 1e3, 3),
+           "bwd_us": round(b_ms * 1e3, 3), "fwd_tbps": round(_tbps(fb, f_ms), 4),
+           "bwd_tbps": round(_tbps(bb, b_ms), 4),
+           "fwd_launch": dict(zip(("waves", "unroll", "splits", "flags"),
+                                  _C.default_config("fwd", x.dtype, N, V))),
+           "bwd_launch": dict(zip(("waves", "unroll", "splits", "flags"),
+                                  _C.default_config("bwd", x.dtype, N, V)))}
+    if with_cpu:
+        c = cpu_baseline("C1", N, x, t, gl, ge)
+        out.update({"cpu_fwd_ms": round(c["fwd_ms"], 3), "cpu_fwd_bwd_ms": round(c["fwd_bwd_ms"], 3),
+                    "cpu_threads": c["threads"],
+                    "cpu_note": "the reference's CPU eager path (TRL-eager forward restated; "
+                                "eager forward + autograd backward), whole batch, median of 3"})
+    return out
+
+
+def sweep(name, dev, K, timer, out_md):
+    """Launch-shape sweep of the forward and backward at workload `name`,
+    back to back and flushed, written as a markdown table."""
+    from kernel_opt import _C
+    inp = make_inputs(name, dev)
+    x, t = inp["logits"], inp["targets"]
+    gl, ge = inp["g_logp"].contiguous(), inp["g_ent"].contiguous()
+    lp, ent, lse = (torch.empty(t.shape, dtype=torch.float32, device=dev) for _ in range(3))
+    d = torch.empty(x.shape, dtype=x.dtype, device=dev)
+    V = x.size(-1)
+    N = x.numel() // V
+    fb, bb = algorithmic_bytes(N, V, x.element_size())
+    fdef = _C.default_config("fwd", x.dtype, N, V)
+    bdef = _C.default_config("bwd", x.dtype, N, V)
+    lines = [f"# Launch-shape sweep, workload {name} (build `{build_id()}`)", "",
+             f"`python bench.py --config {name} --sweep OUT.md --steps {K}`: each shape timed "
+             f"over {K} back-to-back launches (one event pair) and {K} launches each after a "
+             "1 GiB read (per-launch event pairs, mean). Defaults marked *.", "",
+             "| kernel | waves | unroll | splits | b2b us | b2b % of 8 TB/s | flushed us | "
+             "flushed % |", "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    _C.fwd_launch(x, t, lp, ent, lse)
+    for w in (4, 8, 16):
+        for u in (2, 4):
+            for sp in (1, 2):
+                c = (w, u, sp, 0)
+                fn = (lambda c=c: _C.fwd_launch(x, t, lp, ent, lse, config=c))
+                fn()
+                a = timer.b2b(fn)
+                f, _ = timer.flushed(fn)
+                mark = "*" if c == tuple(fdef) else ""
+                lines.append(f"| fwd{mark} | {w} | {u} | {sp} | {a * 1e3:.2f} | "
+                             f"{100 * _tbps(fb, a) / HBM_PEAK_TBPS:.1f} | {f * 1e3:.2f} | "
+                             f"{100 * _tbps(fb, f) / HBM_PEAK_TBPS:.1f} |")
+                print(lines[-1], file=sys.stderr, flush=True)
+    for w in (4, 8, 16):
+        for u in (2, 4):
+            for sp in (4, 8, 16):
+                c = (w, u, sp, 1)
+                fn = (lambda c=c: _C.bwd_launch(x, t, lse, ent, gl, ge, None, d, config=c))
+                fn()
+                a = timer.b2b(fn)
+                f, _ = timer.flushed(fn)
+                mark = "*" if c == tuple(bdef) else ""
+                lines.append(f"| bwd{mark} | {w} | {u} | {sp} | {a * 1e3:.2f} | "
+                             f"{100 * _tbps(bb, a) / HBM_PEAK_TBPS:.1f} | {f * 1e3:.2f} | "
+                             f"{100 * _tbps(bb, f) / HBM_PEAK_TBPS:.1f} |")
+                print(lines[-1], file=sys.stderr, flush=True)
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="C2", choices=sorted(CONFIGS))
+    ap.add_argument("--flush-mode", choices=("read", "write"), default="read",
+                    help="read: sum a 1 GiB buffer before each flushed launch (evicts with "
+                         "clean lines); write: fill it (leaves up to the cache size of dirty "
+                         "lines for the next kernel)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=1024,
+                    help="rows of the workload the CPU baseline times (whole batch elements)")
+    ap.add_argument("--fwd-config", default=None, help="waves,unroll,splits,flags")
+    ap.add_argument("--bwd-config", default=None, help="waves,unroll,splits,flags")
+    ap.add_argument("--core-only", action="store_true",
+                    help="only the workload's forward / backward timings and ceilings (for "
+                         "profiler runs)")
+    ap.add_argument("--no-lmhead", action="store_true",
+                    help="skip the fused LM-head timing (klp_lmh_* against matmul + logprob)")
+    ap.add_argument("--no-shard", action="store_true",
+                    help="skip the vocab-shard timing (one rank's share of C4 under 8-way "
+                         "vocab parallelism)")
+    ap.add_argument("--no-grpo", action="store_true",
+                    help="skip the GRPO timings (the loss kernels against the eager chain, "
+                         "the fused step against the unfused kernels)")
+    ap.add_argument("--sweep", metavar="OUT_MD", default=None,
+                    help="time a grid of launch shapes of the forward and backward and write "
+                         "the table to OUT_MD (nothing else runs)")
+    ap.add_argument("--trace-from", metavar="DIR", default=None,
+                    help="summarise a rocprofv3 --kernel-trace output directory (markdown to "
+                         "stdout; no GPU needed)")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"), default=None,
+                    help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) into HBM "
+                         "bytes per launch (markdown to stdout; no GPU needed)")
+    ap.add_argument("--command", default="",
+                    help="the profiling command, quoted in the --trace-from / --traffic-from "
+                         "summary")
+    args = ap.parse_args(argv)
+
+    if args.trace_from:
+        md, _ = summarize_trace(args.trace_from, args.config, args.command)
+        print(md)
+        return 0
+    if args.traffic_from:
+        md, _ = summarize_traffic(*args.traffic_from, args.config, args.command)
+        print(md)
+        return 0
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(rows are independent, so data-parallel ranks would each run this same "
+              "kernel on their own batch with no exchange)", file=sys.stderr)
+        return 2
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    name = args.config
+    cfg = CONFIGS[name]
+    K = args.steps
+    timer = Timer(dev, K, args.flush_mode)
+    if args.sweep:
+        sweep(name, dev, K, timer, args.sweep)
+        return 0
+
+    fcfg = tuple(int(v) for v in args.fwd_config.split(",")) if args.fwd_config else None
+    bcfg = tuple(int(v) for v in args.bwd_config.split(",")) if args.bwd_config else None
+    core = core_timing(name, dev, K, args.warmup, timer, fcfg, bcfg)
+    N, V, fb, bb = core["N"], core["V"], core["fb"], core["bb"]
+    step_ms, fwd_ms, bwd_ms = core["step_ms"], core["fwd_ms"], core["bwd_ms"]
+    fwd_fl, bwd_fl = core["fwd_fl"], core["bwd_fl"]
+    logits, targets = core["logits"], core["targets"]
+    del core["d_logits"]
+
+    extra = not args.core_only
+    autograd = (autograd_timing(dev, K, logits, targets, core["g_logp"], core["g_ent"])
+                if extra else None)
+    c1 = c1_leg(dev, K, timer, not args.no_cpu_baseline) if extra and name != "C1" else None
 
     cpu = None
-    if not args.no_cpu_baseline:
-        c = cpu_baseline(name, args.cpu_rows, logits, targets, g_logp, g_ent)
+    if extra and not args.no_cpu_baseline:
+        c = cpu_baseline(name, args.cpu_rows, logits, targets, core["g_logp"], core["g_ent"])
         sample = (f"{c['rows']} of {N} rows of {name} (the whole batch)" if not c["scaled"] else
                   f"{c['rows']} of {N} rows of {name}, scaled by {N}/{c['rows']}")
         cpu = {
@@ -675,15 +1197,42 @@ def main(argv=None):
             "fwd_ms": round(c["fwd_ms"], 3),
             "fwd_bwd_ms": round(c["fwd_bwd_ms"], 3),
         }
+        if c1 is not None and "cpu_fwd_bwd_ms" in c1:
+            cpu["C1"] = {"fwd_ms": c1["cpu_fwd_ms"], "fwd_bwd_ms": c1["cpu_fwd_bwd_ms"],
+                         "cores": c1["cpu_threads"]}
 
-    grpo = None if args.no_grpo else grpo_timing(dev, K)
-    step = None if args.no_grpo else grpo_step_timing(dev, K, logits, targets)
-    lmhead = None if args.no_lmhead else lmhead_timing(dev)
-    shard = None if args.no_shard else shard_timing(dev, K)
+    grpo = step = lmhead = shard = None
+    if extra:
+        grpo = None if args.no_grpo else grpo_timing(dev, K)
+        step = None if args.no_grpo else grpo_step_timing(dev, K, logits, targets)
+        lmhead = None if args.no_lmhead else lmhead_timing(dev)
+        shard = None if args.no_shard else shard_timing(dev, K)
 
     B, S, _ = cfg["shape"]
-    fwd_used = fcfg or _C.default_config("fwd", logits.dtype, N, V)
-    bwd_used = bcfg or _C.default_config("bwd", logits.dtype, N, V)
+    fwd_tbps, bwd_tbps = _tbps(fb, fwd_ms), _tbps(bb, bwd_ms)
+    fwd_fl_tbps, bwd_fl_tbps = _tbps(fb, fwd_fl), _tbps(bb, bwd_fl)
+    step_tbps = _tbps(fb + bb, step_ms)
+    bid = build_id()
+    # The dominant kernel at the lower of its warm and flushed rates.
+    warm_is_lower = bwd_tbps <= bwd_fl_tbps
+    bwd_rate = bwd_tbps if warm_is_lower else bwd_fl_tbps
+    bwd_short = None
+    traffic = fwd_traffic = None
+    traffic_src = None
+    for prof in load_profiles("traffic", name, bid):
+        for k, v in prof["kernels"].items():
+            if k.startswith("klp_bwd_kernel"):
+                traffic, bwd_short = v["traffic_bytes"], k
+            elif k.startswith("klp_fwd_kernel"):
+                fwd_traffic = v["traffic_bytes"]
+        traffic_src = prof["file"]
+    trace_check = None
+    for prof in load_profiles("trace", name, bid):
+        for k, v in prof["kernels"].items():
+            if k.startswith("klp_bwd_kernel") or k.startswith("klp_fwd_kernel"):
+                trace_check = trace_check or {"file": prof["file"]}
+                trace_check[k] = {ph: round(d["avg_ns"] / 1e3, 3) for ph, d in v.items()}
+    dt = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[logits.dtype]
     out = {
         "metric": "fwd/bwd ms + HBM TB/s (% of peak) at B*S=1024, V=152064 bf16",
         "value": round(step_tbps, 4),
@@ -695,37 +1244,51 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[
-            logits.dtype],
+        "dtype": dt,
         "data": "synthetic",
         "config": {"workload": f"{name}: logits [{B},{S},{V}] "
                                f"{str(logits.dtype).replace('torch.', '')}, one forward + one "
                                f"backward launch per step",
                    "global_batch": B, "seq_len": S, "vocab": V, "n_rows": N,
                    "parallelism": "single-gpu",
-                   "infinity_cache": (f"flushed ({args.flush_mode} 1 GiB before each launch)"
-                                      if args.flush else "warm")},
-        "fwd_ms": round(fwd_avg, 5),
-        "bwd_ms": round(bwd_avg, 5),
+                   "infinity_cache": "warm for ms_per_step / value / fwd_ms / bwd_ms; "
+                                     "*_flushed after a 1 GiB read before each launch"},
+        "build_id": bid,
+        "fwd_ms": round(fwd_ms, 5),
+        "bwd_ms": round(bwd_ms, 5),
+        "fwd_ms_flushed": round(fwd_fl, 5),
+        "bwd_ms_flushed": round(bwd_fl, 5),
+        "fwd_ms_flushed_median": round(core["fwd_fl_med"], 5),
+        "bwd_ms_flushed_median": round(core["bwd_fl_med"], 5),
         "fwd_tbps": round(fwd_tbps, 4),
         "bwd_tbps": round(bwd_tbps, 4),
         "fwd_pct_peak": round(100 * fwd_tbps / HBM_PEAK_TBPS, 2),
         "bwd_pct_peak": round(100 * bwd_tbps / HBM_PEAK_TBPS, 2),
-        "fwd_launch": dict(zip(("waves", "unroll", "splits", "flags"), fwd_used)),
-        "bwd_launch": dict(zip(("waves", "unroll", "splits", "flags"), bwd_used)),
-        "wall_s_timed": round(t_wall, 4),
+        "fwd_pct_peak_flushed": round(100 * fwd_fl_tbps / HBM_PEAK_TBPS, 2),
+        "bwd_pct_peak_flushed": round(100 * bwd_fl_tbps / HBM_PEAK_TBPS, 2),
+        "step_tbps_flushed": round(_tbps(fb + bb, fwd_fl + bwd_fl), 4),
+        "fwd_launch": dict(zip(("waves", "unroll", "splits", "flags"), core["fwd_used"])),
+        "bwd_launch": dict(zip(("waves", "unroll", "splits", "flags"), core["bwd_used"])),
+        "ceilings": core["ceilings"],
+        "wall_s_timed": round(core["wall"], 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "klp_bwd_kernel",
-            "achieved": round(bb / (bwd_avg * 1e-3) / 1e9, 1),
+            "kernel": bwd_short or "klp_bwd_kernel",
+            "achieved": round(bwd_rate * 1000, 1),
             "peak": HBM_PEAK_TBPS * 1000,
             "unit": "GB/s",
-            "frac": round(bwd_tbps / HBM_PEAK_TBPS, 4),
-            "traffic": MEASURED_TRAFFIC.get((name, "bwd", tuple(bwd_used))),
+            "frac": round(bwd_rate / HBM_PEAK_TBPS, 4),
+            "timing": ("back to back, warm (lower than flushed)" if warm_is_lower
+                       else "flushed per launch (lower than back to back, warm)"),
+            "traffic": traffic,
             "algorithmic_bytes": bb,
-            "fwd_traffic": MEASURED_TRAFFIC.get((name, "fwd", tuple(fwd_used))),
+            "fwd_traffic": fwd_traffic,
             "fwd_algorithmic_bytes": fb,
+            "traffic_source": traffic_src or f"no counter summary of build {bid} under profiles/",
+            "trace_check": trace_check,
         },
+        "autograd": autograd,
+        "C1": c1,
         "cpu_baseline": cpu,
         "grpo_loss": grpo,
         "grpo_step": step,

@@ -365,6 +365,43 @@ size_t lmh_workspace_bytes(int64_t n_tokens, int64_t vocab) {
     return static_cast<size_t>(nc) * static_cast<size_t>(n_tokens) * 4 * sizeof(float);
 }
 
+int ceiling_impl(bool copy, const void* src, void* dst, int64_t n_rows, int64_t row_bytes,
+                 int waves, int unroll, int splits, uint32_t* sink, uint32_t magic,
+                 void* stream) {
+    const char* what = copy ? "ceiling copy" : "ceiling read";
+    if (n_rows < 0) return fail(KLP_EINVAL, "n_rows must be >= 0");
+    if (row_bytes < 16 || row_bytes % 16 != 0)
+        return fail(KLP_EINVAL, "row_bytes must be a positive multiple of 16, got %lld",
+                    static_cast<long long>(row_bytes));
+    if (n_rows == 0) return ok();
+    if (src == nullptr || !aligned(src, 16))
+        return fail(KLP_EINVAL, "src must be non-null and 16-byte aligned");
+    if (copy && (dst == nullptr || !aligned(dst, 16)))
+        return fail(KLP_EINVAL, "dst must be non-null and 16-byte aligned");
+    if (!copy && (sink == nullptr || !aligned(sink, 4)))
+        return fail(KLP_EINVAL, "sink must be non-null and 4-byte aligned");
+    const bool w = (waves == 1 || waves == 2 || waves == 4 || waves == 8 || waves == 16);
+    if (!w || (unroll != 2 && unroll != 4) || splits < 1 || splits > 1024)
+        return fail(KLP_EINVAL, "unsupported launch shape (waves=%d unroll=%d splits=%d)", waves,
+                    unroll, splits);
+    const int64_t per = ((row_bytes / 16 + splits - 1) / splits + 7) / 8 * 8 * 16;
+    if (copy && per > int64_t{INT32_MAX})
+        return fail(KLP_EINVAL, "row pieces must be under 2 GiB: use more splits");
+    int rc;
+    if ((rc = check_grid(n_rows, splits, waves * 64)) != KLP_OK) return rc;
+    klp::CeilingParams p;
+    p.src = src;
+    p.dst = dst;
+    p.n_rows = n_rows;
+    p.row_bytes = row_bytes;
+    p.splits = splits;
+    p.sink = sink;
+    p.magic = magic;
+    if (injected_failure(what)) return KLP_ELAUNCH;
+    return after_launch(
+        klp::launch_ceiling(copy, p, waves, unroll, static_cast<hipStream_t>(stream)), what);
+}
+
 }  // namespace
 
 extern "C" {
@@ -817,6 +854,18 @@ int klp_lmh_fwd(const void* hidden, int64_t ld_hidden, const void* weight, int64
     if (injected_failure("lm-head forward")) return KLP_ELAUNCH;
     return after_launch(klp::launch_lmh_fwd(p, static_cast<hipStream_t>(stream)),
                         "lm-head forward");
+}
+
+int klp_ceiling_read(const void* src, int64_t n_rows, int64_t row_bytes, int waves, int unroll,
+                     int splits, uint32_t* sink, uint32_t magic, void* stream) {
+    return ceiling_impl(false, src, nullptr, n_rows, row_bytes, waves, unroll, splits, sink,
+                        magic, stream);
+}
+
+int klp_ceiling_copy(const void* src, void* dst, int64_t n_rows, int64_t row_bytes, int waves,
+                     int unroll, int splits, void* stream) {
+    return ceiling_impl(true, src, dst, n_rows, row_bytes, waves, unroll, splits, nullptr, 0,
+                        stream);
 }
 
 }  // extern "C"

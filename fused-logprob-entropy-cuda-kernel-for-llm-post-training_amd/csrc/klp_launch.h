@@ -203,6 +203,21 @@ int64_t lmh_vocab_tiles(int64_t vocab);
 hipError_t launch_lmh_fwd(const LmhParams& p, hipStream_t stream);
 hipError_t launch_lmh_dlogits(const LmhParams& p, hipStream_t stream);
 
+// Calibration kernels (klp_ceiling.hip): rows of `row_bytes` (a multiple of
+// 16) at `src` (and `dst`), 16-byte aligned and contiguous; `splits`
+// workgroups per row.
+struct CeilingParams {
+    const void* src;
+    void* dst;           // copy only
+    int64_t n_rows;
+    int64_t row_bytes;
+    int64_t splits;
+    uint32_t* sink;      // read only: [n_rows * splits], written when fold == magic
+    uint32_t magic;
+};
+hipError_t launch_ceiling(bool copy, const CeilingParams& p, int waves, int unroll,
+                          hipStream_t stream);
+
 hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream);
 hipError_t launch_shard_merge(const ShardMergeParams& p, hipStream_t stream);
 hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream);

@@ -70,6 +70,8 @@ SIGNATURES = {
     "klp_bwd_ex": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                   _vp]),
     "klp_default_config": (None, [_i32, _i32, _i64, _i64] + [ctypes.POINTER(_i32)] * 4),
+    "klp_ceiling_read": (_i32, [_vp, _i64, _i64, _i32, _i32, _i32, _vp, ctypes.c_uint32, _vp]),
+    "klp_ceiling_copy": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp]),
 }
 
 

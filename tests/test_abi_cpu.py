@@ -374,3 +374,38 @@ def test_scale_inplace_validation_errors():
         assert scale() == KLP_ELAUNCH and "scale" in _err()
     finally:
         lib.klp_debug_fail_next_launches(0)
+
+
+def test_ceiling_validation_errors():
+    """klp_ceiling_read / klp_ceiling_copy reject bad arguments before any
+    launch; n_rows = 0 is a no-op; an injected launch failure is reported."""
+    from kernel_opt._library import KLP_EINVAL, KLP_ELAUNCH, lib
+    A = ctypes.c_void_p(0x100000)
+
+    def read(**kw):
+        a = dict(src=A, n=4, rb=4096, w=4, u=4, sp=1, sink=A)
+        a.update(kw)
+        return lib.klp_ceiling_read(a["src"], a["n"], a["rb"], a["w"], a["u"], a["sp"],
+                                    a["sink"], 7, None)
+
+    def copy(**kw):
+        a = dict(src=A, dst=A, n=4, rb=4096, w=16, u=2, sp=8)
+        a.update(kw)
+        return lib.klp_ceiling_copy(a["src"], a["dst"], a["n"], a["rb"], a["w"], a["u"],
+                                    a["sp"], None)
+    assert read(n=0, src=None, sink=None) == 0 and copy(n=0, src=None, dst=None) == 0
+    assert read(n=-1) == KLP_EINVAL and "n_rows" in _err()
+    assert read(rb=24) == KLP_EINVAL and "multiple of 16" in _err()
+    assert copy(rb=0) == KLP_EINVAL and "multiple of 16" in _err()
+    assert read(src=ctypes.c_void_p(0x100008)) == KLP_EINVAL and "src" in _err()
+    assert copy(dst=None) == KLP_EINVAL and "dst" in _err()
+    assert read(sink=None) == KLP_EINVAL and "sink" in _err()
+    assert read(w=3) == KLP_EINVAL and "launch shape" in _err()
+    assert copy(u=8) == KLP_EINVAL and "launch shape" in _err()
+    assert copy(sp=0) == KLP_EINVAL and "launch shape" in _err()
+    assert copy(n=1, rb=(1 << 31) + 16, sp=1) == KLP_EINVAL and "2 GiB" in _err()
+    lib.klp_debug_fail_next_launches(1)
+    try:
+        assert copy() == KLP_ELAUNCH and "ceiling copy" in _err()
+    finally:
+        lib.klp_debug_fail_next_launches(0)

@@ -1,0 +1,139 @@
+"""bench.py's rocprofv3 readers (--traffic-from, --trace-from) on synthetic
+rocprofv3 CSV files: counter scaling by the calibration copy, per-phase
+kernel averages, and the round trip of the machine-readable summary line
+through load_profiles (matched on build id and workload)."""
+from __future__ import annotations
+
+import csv
+import os
+
+import pytest
+
+import bench
+
+BWD = "void klp::klp_bwd_kernel<0, 16, 2, true, false>(klp::BwdParams)"
+FWD = "void klp::klp_fwd_kernel<0, 4, 4, false, false>(klp::FwdParams)"
+COPY = "void klp::klp_ceiling_copy_kernel<16, 2>(klp::CeilingParams)"
+READ = "void klp::klp_ceiling_read_kernel<4, 4>(klp::CeilingParams)"
+FLUSH = "void at::native::reduce_kernel<512, 1, at::native::ReduceOp<long> >(...)"
+
+COUNTER_COLS = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id",
+                "Thread_Id", "Grid_Size", "Kernel_Id", "Kernel_Name", "Workgroup_Size",
+                "LDS_Block_Size", "Scratch_Size", "VGPR_Count", "Accum_VGPR_Count",
+                "SGPR_Count", "Counter_Name", "Counter_Value", "Start_Timestamp",
+                "End_Timestamp"]
+TRACE_COLS = ["Kind", "Agent_Id", "Queue_Id", "Stream_Id", "Thread_Id", "Dispatch_Id",
+              "Kernel_Id", "Kernel_Name", "Correlation_Id", "Start_Timestamp", "End_Timestamp"]
+
+
+def _write(path, cols, rows):
+    os.makedirs(os.path.dirname(path), exist_ok=True)
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=cols, quoting=csv.QUOTE_NONNUMERIC)
+        w.writeheader()
+        for r in rows:
+            w.writerow({c: r.get(c, 0) for c in cols})
+
+
+def _counter_dir(tmp_path, name, counter, values):
+    rows = []
+    for i, (kernel, v) in enumerate(values):
+        rows.append({"Dispatch_Id": i + 1, "Kernel_Name": kernel, "Counter_Name": counter,
+                     "Counter_Value": v})
+    d = tmp_path / name
+    _write(str(d / "host" / "123" / "run_counter_collection.csv"), COUNTER_COLS, rows)
+    return str(d)
+
+
+def test_traffic_scaled_by_the_calibration_copy(tmp_path):
+    N, V, esz = bench._workload_sizes("C2")
+    copy_kib = bench.ceiling_row_bytes(V, esz) * N / 1024
+    # FETCH_SIZE reads half of the bytes read (as on the gfx950 box); WRITE_SIZE is exact.
+    fetch = _counter_dir(tmp_path, "f", "FETCH_SIZE", [
+        (COPY, copy_kib / 2), (COPY, copy_kib / 2), (BWD, 152100.0), (BWD, 152102.0),
+        (FWD, 152110.0), (FLUSH, 500000.0)])
+    write = _counter_dir(tmp_path, "w", "WRITE_SIZE", [
+        (COPY, copy_kib), (BWD, 304130.0), (FWD, 96.0), (FLUSH, 1.0)])
+    md, data = bench.summarize_traffic(fetch, write, "C2")
+    assert data["fetch_factor"] == pytest.approx(2.0)
+    assert data["write_factor"] == pytest.approx(1.0)
+    k = data["kernels"]
+    assert set(k) == {"klp_ceiling_copy_kernel<16, 2>", "klp_bwd_kernel<0, 16, 2, true, false>",
+                      "klp_fwd_kernel<0, 4, 4, false, false>"}
+    bwd = k["klp_bwd_kernel<0, 16, 2, true, false>"]
+    assert bwd["traffic_bytes"] == round(1024 * (152101.0 * 2 + 304130.0))
+    _, bb = bench.algorithmic_bytes(N, V, esz)
+    assert bwd["algorithmic_bytes"] == bb
+    assert bwd["ratio"] == pytest.approx(bwd["traffic_bytes"] / bb, abs=1e-4)
+    assert k["klp_ceiling_copy_kernel<16, 2>"]["ratio"] == pytest.approx(1.0)
+    assert "| `klp_bwd_kernel<0, 16, 2, true, false>` |" in md
+
+
+def test_traffic_needs_the_calibration(tmp_path):
+    fetch = _counter_dir(tmp_path, "f", "FETCH_SIZE", [(BWD, 1.0)])
+    write = _counter_dir(tmp_path, "w", "WRITE_SIZE", [(BWD, 1.0)])
+    with pytest.raises(RuntimeError, match="calibration"):
+        bench.summarize_traffic(fetch, write, "C2")
+
+
+def test_trace_phases(tmp_path):
+    # flush, fwd (flushed), fwd (back to back), bwd (after fwd), bwd (back to back),
+    # flush, bwd (flushed), read ceiling (other: after bwd -> klp), unrelated kernel
+    seq = [(FLUSH, 100), (FWD, 50), (FWD, 52), (BWD, 110), (BWD, 106), (FLUSH, 100),
+           (BWD, 120), (READ, 45), ("void at::native::elementwise(...)", 5)]
+    rows, t = [], 1000
+    for i, (k, dur) in enumerate(seq):
+        rows.append({"Kind": "KERNEL_DISPATCH", "Dispatch_Id": i + 1, "Kernel_Name": k,
+                     "Start_Timestamp": t, "End_Timestamp": t + dur * 1000})
+        t += dur * 1000 + 500
+    d = tmp_path / "trace"
+    _write(str(d / "run_kernel_trace.csv"), TRACE_COLS, rows[::-1])  # any row order
+    md, data = bench.summarize_trace(str(d), "C2")
+    fwd = data["kernels"]["klp_fwd_kernel<0, 4, 4, false, false>"]
+    bwd = data["kernels"]["klp_bwd_kernel<0, 16, 2, true, false>"]
+    assert fwd["flushed"]["avg_ns"] == 50000 and fwd["back to back"]["avg_ns"] == 52000
+    assert fwd["all"]["n"] == 2
+    assert bwd["after another klp kernel"]["avg_ns"] == 110000
+    assert bwd["back to back"]["avg_ns"] == 106000
+    assert bwd["flushed"]["avg_ns"] == 120000
+    assert bwd["all"]["avg_ns"] == pytest.approx((110000 + 106000 + 120000) / 3, abs=0.1)
+    N, V, esz = bench._workload_sizes("C2")
+    _, bb = bench.algorithmic_bytes(N, V, esz)
+    assert bwd["flushed"]["tbps"] == pytest.approx(bb / 120e-6 / 1e12, abs=1e-4)
+    assert data["kernels"]["klp_ceiling_read_kernel<4, 4>"]["after another klp kernel"]["n"] == 1
+
+
+def test_summary_round_trip(tmp_path, monkeypatch):
+    d = tmp_path / "trace"
+    _write(str(d / "run_kernel_trace.csv"), TRACE_COLS,
+           [{"Kind": "KERNEL_DISPATCH", "Kernel_Name": BWD, "Start_Timestamp": 0,
+             "End_Timestamp": 100000}])
+    md, data = bench.summarize_trace(str(d), "C2", command="rocprofv3 ... -- python3 bench.py")
+    prof = tmp_path / "profiles"
+    prof.mkdir()
+    (prof / "klp_C2_trace.md").write_text(md)
+    monkeypatch.setattr(bench, "PROFILES_DIR", str(prof))
+    got = bench.load_profiles("trace", "C2", bench.build_id())
+    assert len(got) == 1 and got[0]["kernels"] == data["kernels"]
+    assert bench.load_profiles("trace", "C2", "0000000000000000") == []
+    assert bench.load_profiles("trace", "C3", bench.build_id()) == []
+    assert bench.load_profiles("traffic", "C2", bench.build_id()) == []
+
+
+def test_build_id_tracks_the_sources(tmp_path, monkeypatch):
+    a = bench.build_id()
+    assert a == bench.build_id() and len(a) == 16
+    src = tmp_path / "pkg" / "csrc"
+    src.mkdir(parents=True)
+    (src / "k.hip").write_text("one")
+    (tmp_path / "pkg" / "Makefile").write_text("all:")
+    monkeypatch.setattr(bench, "PKG_DIR", str(tmp_path / "pkg"))
+    b = bench.build_id()
+    (src / "k.hip").write_text("two")
+    assert bench.build_id() != b
+
+
+def test_short_kernel_names():
+    assert bench.short_kernel(BWD) == "klp_bwd_kernel<0, 16, 2, true, false>"
+    assert bench.short_kernel("void klp::klp_fwd_shard_merge_kernel(klp::ShardMergeParams)") == \
+        "klp_fwd_shard_merge_kernel"
