@@ -935,7 +935,9 @@ def autograd_timing(dev, K, logits, targets, g_logp, g_ent):
     peak allocated during the calls minus allocated before;
     bench/bench_backward.py:39-56: events around loss.backward()).
     `*_transient_bytes` is the part of the peak not held after the call
-    (intermediates); the backward's held bytes are the gradient itself."""
+    (intermediates); the backward's held bytes are the gradient's block
+    (the caching allocator may round a large block up to its 2 MiB segment
+    granularity, so it can exceed the gradient's size by under 2 MiB)."""
     from kernel_opt import fused_logprob_entropy
     x = logits.detach().requires_grad_(True)
     gl, ge = g_logp.view(targets.shape), g_ent.view(targets.shape)
@@ -1001,8 +1003,8 @@ def autograd_timing(dev, K, logits, targets, g_logp, g_ent):
         "fwd_peak_bytes": fwd_peak, "fwd_output_bytes": out_bytes,
         "fwd_transient_bytes": fwd_peak - fwd_held,
         "bwd_peak_bytes": bwd_peak, "bwd_grad_bytes": grad_bytes,
+        "bwd_held_bytes": bwd_held,
         "bwd_transient_bytes": bwd_peak - bwd_held,
-        "bwd_peak_beyond_grad_bytes": bwd_peak - grad_bytes,
         "note": "kernel_opt.fused_logprob_entropy and loss.backward() from Python, events per "
                 "call (median of K); loss = sum(logp*g_logp + entropy*g_ent); peak = max "
                 "allocated during one call minus allocated before it",

@@ -7,8 +7,9 @@
 * the drop-in path's allocations at C2 (the reference publishes 0.0 MB of
   intermediates for the forward, notes/stage2_findings.md:30-38, and the
   north star asks for a backward with zero intermediate allocations):
-  the forward allocates exactly its three outputs, the backward exactly the
-  gradient plus the loss's own per-row gradient tensors.
+  the forward allocates exactly its three outputs; the backward holds the
+  gradient and allocates nothing transient but the loss's own per-row
+  gradient tensors.
 """
 from __future__ import annotations
 
@@ -96,7 +97,7 @@ def test_ceiling_read_reads_every_word(n_rows, row_bytes, waves, unroll, splits)
 def test_c2_autograd_path_allocates_no_intermediates():
     """C2 through kernel_opt.fused_logprob_entropy and loss.backward(): the
     forward's peak allocation is its three fp32 outputs, nothing transient;
-    the backward's peak beyond the gradient is the loss's per-row gradient
+    the backward's transient allocations are the loss's per-row gradient
     tensors (a few KiB, far below one row of logits), nothing [N, V]-sized."""
     import bench
     inp = bench.make_inputs("C2", DEV)
@@ -108,5 +109,9 @@ def test_c2_autograd_path_allocates_no_intermediates():
     assert r["fwd_peak_bytes"] == r["fwd_output_bytes"]
     assert r["fwd_transient_bytes"] == 0
     assert r["bwd_grad_bytes"] == inp["logits"].numel() * 2
-    assert r["bwd_peak_beyond_grad_bytes"] <= 64 * 1024
+    # what stays allocated is the gradient's block (the caching allocator
+    # may round it up to its 2 MiB segment granularity) ...
+    assert 0 <= r["bwd_held_bytes"] - r["bwd_grad_bytes"] < 2 * 1024 * 1024
+    # ... and nothing else was allocated on the way but the loss's per-row
+    # gradients (8 KiB at C2, below one 304 KB row of logits)
     assert r["bwd_transient_bytes"] <= 64 * 1024
