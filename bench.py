@@ -22,9 +22,11 @@ Timing, all with HIP events on the stream the kernels run on:
   * `ms_per_step`: one event pair around K interleaved forward+backward steps
     (the backward re-reads logits the forward has just streamed through the
     256 MB Infinity Cache, so the step can beat the per-kernel rates);
-  * `fwd_ms` / `bwd_ms`: one event pair around K back-to-back launches;
-  * `fwd_ms_flushed` / `bwd_ms_flushed`: each of K launches timed on its own
-    after a 1 GiB buffer was read (which evicts the logits from the cache);
+  * `fwd_ms` / `bwd_ms`: one event pair around max(K, 50) back-to-back
+    launches;
+  * `fwd_ms_flushed` / `bwd_ms_flushed`: each of max(K, 50) launches timed on
+    its own after a 1 GiB buffer was read (which evicts the logits from the
+    cache);
   * `ceilings`: in the same process, at the same size and launch shape, the
     library's calibration kernels (klp_ceiling_read: the forward's loads
     without arithmetic; klp_ceiling_copy: the backward's loads and stores)
@@ -73,6 +75,8 @@ import torch  # noqa: E402
 HBM_PEAK_TBPS = 8.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 FLUSH_BYTES = 1 << 30
+SETTLE_S = 0.3          # untimed busy time before the first timed loop
+KERNEL_LAUNCHES = 50    # fewest launches behind each per-kernel figure
 
 
 def build_id() -> str:
@@ -778,11 +782,12 @@ class Timer:
     (reading, or with mode "write" overwriting, a 1 GiB buffer) before each
     launch."""
 
-    def __init__(self, dev, K, flush_mode="read"):
+    def __init__(self, dev, K, flush_mode="read", buf=None):
         self.stream = torch.cuda.current_stream(dev)
         self.K = K
         self.flush_mode = flush_mode
-        self.buf = torch.ones(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+        self.buf = buf if buf is not None else torch.ones(FLUSH_BYTES, dtype=torch.uint8,
+                                                          device=dev)
 
     def b2b(self, body):
         """Average ms of `body` over K back-to-back calls: one event pair
@@ -851,16 +856,26 @@ def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None):
     for _ in range(warmup):
         fwd()
         bwd()
+    # Untimed: keep the GPU busy for a moment so that its clocks have
+    # settled before anything is timed (a few warm-up steps take ~1 ms).
+    t_spin = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < t_spin:
+        for _ in range(8):
+            fwd()
+            bwd()
+        torch.cuda.synchronize()
     torch.cuda.synchronize()
 
     t_wall0 = time.perf_counter()
     # the timed steps: forward then backward, repeated, as a training loop runs them
     step_ms = timer.b2b(lambda: (fwd(), bwd()))
     t_wall = time.perf_counter() - t_wall0
-    fwd_ms = timer.b2b(fwd)
-    bwd_ms = timer.b2b(bwd)
-    fwd_fl, fwd_fl_med = timer.flushed(fwd)
-    bwd_fl, bwd_fl_med = timer.flushed(bwd)
+    # Per-kernel figures over at least KERNEL_LAUNCHES launches each.
+    kt = Timer(dev, max(K, KERNEL_LAUNCHES), timer.flush_mode, timer.buf)
+    fwd_ms = kt.b2b(fwd)
+    bwd_ms = kt.b2b(bwd)
+    fwd_fl, fwd_fl_med = kt.flushed(fwd)
+    bwd_fl, bwd_fl_med = kt.flushed(bwd)
 
     fwd_used = tuple(fcfg) if fcfg else _C.default_config("fwd", logits.dtype, N, V)
     bwd_used = tuple(bcfg) if bcfg else _C.default_config("bwd", logits.dtype, N, V)
@@ -896,13 +911,13 @@ def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None):
 
     for fn in (ceil_read, ceil_copy):
         fn()
-    ceil = {"read_ms": timer.b2b(ceil_read), "copy_ms": timer.b2b(ceil_copy)}
-    ceil["read_ms_flushed"], _ = timer.flushed(ceil_read)
-    ceil["copy_ms_flushed"], _ = timer.flushed(ceil_copy)
+    ceil = {"read_ms": kt.b2b(ceil_read), "copy_ms": kt.b2b(ceil_copy)}
+    ceil["read_ms_flushed"], _ = kt.flushed(ceil_read)
+    ceil["copy_ms_flushed"], _ = kt.flushed(ceil_copy)
     if tdst is not None:
         torch_copy()
-        ceil["torch_copy_ms"] = timer.b2b(torch_copy)
-        ceil["torch_copy_ms_flushed"], _ = timer.flushed(torch_copy)
+        ceil["torch_copy_ms"] = kt.b2b(torch_copy)
+        ceil["torch_copy_ms_flushed"], _ = kt.flushed(torch_copy)
     del sink
     if dst is not d_logits:
         del dst
@@ -1065,9 +1080,16 @@ def sweep(name, dev, K, timer, out_md):
     fb, bb = algorithmic_bytes(N, V, x.element_size())
     fdef = _C.default_config("fwd", x.dtype, N, V)
     bdef = _C.default_config("bwd", x.dtype, N, V)
+    timer = Timer(dev, max(K, KERNEL_LAUNCHES), timer.flush_mode, timer.buf)
+    n = timer.K
+    t_spin = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < t_spin:
+        _C.fwd_launch(x, t, lp, ent, lse)
+        _C.bwd_launch(x, t, lse, ent, gl, ge, None, d)
+        torch.cuda.synchronize()
     lines = [f"# Launch-shape sweep, workload {name} (build `{build_id()}`)", "",
              f"`python bench.py --config {name} --sweep OUT.md --steps {K}`: each shape timed "
-             f"over {K} back-to-back launches (one event pair) and {K} launches each after a "
+             f"over {n} back-to-back launches (one event pair) and {n} launches each after a "
              "1 GiB read (per-launch event pairs, mean). Defaults marked *.", "",
              "| kernel | waves | unroll | splits | b2b us | b2b % of 8 TB/s | flushed us | "
              "flushed % |", "|---|---:|---:|---:|---:|---:|---:|---:|"]

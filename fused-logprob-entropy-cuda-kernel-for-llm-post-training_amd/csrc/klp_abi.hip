@@ -48,6 +48,9 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 // workgroup per row still leaves the chip short of that.  Backward: splitting
 // needs no second pass; see default_bwd_config.
 constexpr int64_t kFwdTargetWaves = 4096;
+// Wave64s resident at 8 per SIMD on 256 CUs: a grid up to this size runs as
+// one round of workgroups.
+constexpr int64_t kFwdOneRoundWaves = 8192;
 constexpr int64_t kBwdLargeGrid = 65536;
 constexpr int kMaxSplits = 64;
 
@@ -102,33 +105,58 @@ int64_t bwd_piece_bytes(int dtype, int64_t vocab, int64_t splits) {
     return ((per + 7) & ~int64_t{7}) * 16;
 }
 
+// Bytes the forward's buffer loads address for one row piece: the piece's
+// body vectors plus the kFwdRing chunks its ring may prefetch past them (out
+// of range, never read); the offsets are 32-bit, so this must stay under
+// 2 GiB.
+int64_t fwd_piece_bytes(int dtype, int64_t vocab, const klp::FwdConfig& c) {
+    const int64_t per = (body_vectors(dtype, vocab) + c.splits - 1) / c.splits;
+    return (per + int64_t{klp::kFwdRing} * c.waves * 64 * c.unroll) * 16;
+}
+
+int check_fwd_piece(int dtype, int64_t vocab, const klp::FwdConfig& c) {
+    if (fwd_piece_bytes(dtype, vocab, c) > int64_t{INT32_MAX})
+        return fail(KLP_EINVAL,
+                    "forward row pieces must be under 2 GiB (vocab %lld in %d pieces): use "
+                    "more splits",
+                    static_cast<long long>(vocab), c.splits);
+    return KLP_OK;
+}
+
 klp::FwdConfig default_fwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     klp::FwdConfig c;
-    c.unroll = 4;
     c.flags = 0;
     c.splits = 1;
     const int64_t nvec = body_vectors(dtype, vocab);
-    // Up to 4 waves per row, fewer for short rows so that each thread keeps
-    // at least 8 vectors, and unroll 2 below 32 vectors per thread (bf16,
-    // measured: a vocab-parallel shard of C4, [32768, 18992]: 4 waves unroll
-    // 2 195 us vs unroll 4 206 us; [65536, 9496]: 2 waves 206 us vs 4 waves
-    // 272 us; [8192, 4096]: 1 wave 13.4 us vs 4 waves 24.4 us).  Rows that
-    // short take few threads whatever the batch.
-    int w = 4;
+    // Up to 8 waves per row, fewer for short rows so that each thread keeps
+    // at least 8 vectors (rows that short take few threads whatever the
+    // batch: [65536, 9496] bf16, 2 waves 206 us vs 4 waves 272 us).
+    int w = 8;
     while (w > 1 && int64_t{w} * 64 * 8 > nvec) w /= 2;
-    if (n_rows * w >= kFwdTargetWaves || w < 4) {
-        c.waves = w;
-        if (nvec / (int64_t{w} * 64) < 32) c.unroll = 2;
-    } else if (n_rows * 8 >= kFwdTargetWaves) {
-        c.waves = 8;
-    } else {
+    if (w == 8 && n_rows * w < kFwdTargetWaves) {
+        // Few rows of a long vocabulary: 16-wave workgroups, split rows
+        // while still short of the wave target and every piece keeps each
+        // thread busy for at least two full chunks.
         c.waves = 16;
+        c.unroll = 4;
         const int64_t tile = static_cast<int64_t>(c.waves) * 64 * c.unroll;
-        // Split while short of the wave target and every piece still keeps
-        // each thread busy for at least two full iterations.
         while (c.splits < kMaxSplits && n_rows * c.splits * c.waves < kFwdTargetWaves &&
                nvec / (2 * c.splits) >= 2 * tile)
             c.splits *= 2;
+    } else if (n_rows * w <= kFwdOneRoundWaves) {
+        // All workgroups resident at once (C2: 1024 rows x 8 waves, 8 waves
+        // per SIMD): unroll 2 keeps a wave at 61 VGPRs (unroll 4: ~100, 4
+        // waves per SIMD).  C2, one box: 8 waves unroll 2 48.1 us, 4 waves
+        // unroll 4 48.9 us, 16 waves unroll 4 57.6 us.
+        c.waves = w;
+        c.unroll = 2;
+    } else {
+        // Several rounds of workgroups: unroll 4 for rows of at least 16
+        // vectors per thread (C3 8 waves: unroll 4 301 us vs unroll 2 312 us;
+        // a C4 vocab shard [32768, 18992], 4 waves: unroll 2 195 us vs 4
+        // 206 us); fp32 rows on 4 waves (C5: 1204 us vs 1233 us on 8).
+        c.waves = (dtype == KLP_FP32 && w > 4) ? 4 : w;
+        c.unroll = (nvec / (int64_t{c.waves} * 64) >= 16) ? 4 : 2;
     }
     return c;
 }
@@ -218,6 +246,7 @@ int fwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
                         workspace_bytes, need);
         }
     }
+    if ((rc = check_fwd_piece(dtype, vocab, cfg)) != KLP_OK) return rc;
     if ((rc = check_grid(n_rows, cfg.splits, cfg.waves * 64)) != KLP_OK) return rc;
 
     klp::FwdParams p;
@@ -591,6 +620,7 @@ int klp_fwd_shard(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
         cfg.waves = 16;
         cfg.splits = 1;
     }
+    if ((rc = check_fwd_piece(dtype, vocab, cfg)) != KLP_OK) return rc;
     if ((rc = check_grid(n_rows, 1, cfg.waves * 64)) != KLP_OK) return rc;
     klp::FwdParams p;
     p.logits = logits;

@@ -11,25 +11,57 @@
 //    thread per iteration, consecutive lanes on consecutive 16-byte words;
 //    the few elements before the first 16-byte boundary and after the last
 //    one (head / tail) are read as scalars by split 0;
-//  - every U*16 bytes cost one rescale plus one v_exp_f32 per element
+//  - U vectors per thread form a chunk; chunks are loaded kFwdRing - 1 ahead
+//    of their use into a ring of register sets (buffer loads), so that loads
+//    stay in flight while a wave computes;
+//  - every chunk costs one rescale plus one v_exp_f32 per element
 //    (absorb() in klp_device.h);
 //  - with a temperature T (FwdParams::scale = 1/T != 1) every logit is
 //    multiplied by 1/T in fp32 as it is loaded, which fuses the GRPO trainer's
 //    separate `logits.div_(temperature)` pass (reference trainer.py:101);
-//  - lanes merge with DPP and xor-shuffles, the waves' states through LDS
-//    with DPP steps in wave 0, splits through a workspace in split order, so
-//    results do not depend on timing.
+//  - lanes merge as one flat reduction (maximum, one rescale per lane, sums;
+//    DPP within rows, v_permlane16/32_swap across them), the waves' states
+//    through LDS by the same reduction in wave 0, splits through a
+//    workspace in split order, so results do not depend on timing.
 #include "klp_device.h"
 #include "klp_launch.h"
 
 namespace klp {
+
+// Chunk c of a workgroup's piece (U 16-byte vectors per thread, lanes on
+// consecutive vectors) is loaded into register set c % kFwdRing, kFwdRing - 1
+// chunks ahead of its use, by buffer loads over the piece's whole chunks:
+// the loads of the next chunks stay in flight while a wave computes (a
+// wave that loaded and then computed had nothing in flight while it
+// computed), and prefetches past the last whole chunk are out of the
+// buffer's range, so they read nothing and are never used.
+template <int DT, bool kClamp, int U, bool kScaled>
+__device__ __forceinline__ void absorb_chunk(Stat& s, const u32x4* v, float scale) {
+    constexpr int EPV = Traits<DT>::kPerVec;
+    float x[U * EPV];
+#pragma unroll
+    for (int u = 0; u < U; ++u) unpack<DT>(v[u], x + u * EPV);
+    if (kScaled) {
+#pragma unroll
+        for (int j = 0; j < U * EPV; ++j) x[j] *= scale;
+    }
+    absorb<U * EPV, kClamp>(s, x);
+}
+
+template <int U, int NTHREADS>
+__device__ __forceinline__ void load_chunk(u32x4* dst, const __amdgpu_buffer_rsrc_t rs, int c,
+                                           int tid) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        dst[u] = __builtin_amdgcn_raw_buffer_load_b128(
+            rs, ((c * U + u) * NTHREADS + tid) * 16, 0, kBufNonTemporal);
+}
 
 template <int DT, bool kClamp, int U, int NTHREADS, bool kScaled>
 __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT>::elem* rp,
                                                const u32x4* vp, int64_t head, int64_t tail_begin,
                                                int64_t vocab, bool with_edges, int64_t vb,
                                                int64_t ve, int tid, float scale) {
-    constexpr int EPV = Traits<DT>::kPerVec;
     // Scalar head / tail elements (fewer than 2 * EPV of them).
     if (with_edges) {
         const int64_t n_edge = head + (vocab - tail_begin);
@@ -40,24 +72,34 @@ __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT
             absorb<1, true>(s, &x);
         }
     }
-    const int64_t step = static_cast<int64_t>(NTHREADS) * U;
-    int64_t i = vb + tid;
-    const int64_t n_full = (ve - vb) / step;
-    for (int64_t k = 0; k < n_full; ++k) {
-        u32x4 v[U];
+    constexpr int step = NTHREADS * U;  // vectors per chunk
+    // The host keeps (piece + kFwdRing chunks) * 16 bytes under 2^31, so
+    // every buffer offset below fits in 32 bits.
+    const int n_full = static_cast<int>((ve - vb) / step);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<u32x4*>(vp + vb), 0, n_full * step * 16, 0x00020000);
+    u32x4 set[kFwdRing][U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = load16<true>(vp + i + u * NTHREADS);
-        float x[U * EPV];
+    for (int r = 0; r < kFwdRing - 1; ++r) load_chunk<U, NTHREADS>(set[r], rs, r, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    int k = 0;
+    for (; k + kFwdRing <= n_full; k += kFwdRing) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) unpack<DT>(v[u], x + u * EPV);
-        if (kScaled) {
-#pragma unroll
-            for (int j = 0; j < U * EPV; ++j) x[j] *= scale;
+        for (int r = 0; r < kFwdRing; ++r) {
+            load_chunk<U, NTHREADS>(set[(r + kFwdRing - 1) % kFwdRing], rs, k + r + kFwdRing - 1,
+                                    tid);
+            // Keeps the prefetch ahead of the arithmetic: the scheduler would
+            // otherwise sink it below to save registers.
+            __builtin_amdgcn_sched_barrier(0);
+            absorb_chunk<DT, kClamp, U, kScaled>(s, set[r], scale);
         }
-        absorb<U * EPV, kClamp>(s, x);
-        i += step;
     }
-    if (vb + n_full * step < ve) {
+#pragma unroll
+    for (int r = 0; r < kFwdRing - 1; ++r)
+        if (k + r < n_full) absorb_chunk<DT, kClamp, U, kScaled>(s, set[r], scale);
+
+    const int64_t i = vb + static_cast<int64_t>(n_full) * step + tid;
+    if (i - tid < ve) {
         // Remainder: vectors past the end read as -inf, which the clamped
         // absorb ignores.
         u32x4 v[U];
@@ -71,14 +113,7 @@ __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT
                 v[u] = u32x4{w, w, w, w};
             }
         }
-        float x[U * EPV];
-#pragma unroll
-        for (int u = 0; u < U; ++u) unpack<DT>(v[u], x + u * EPV);
-        if (kScaled) {
-#pragma unroll
-            for (int j = 0; j < U * EPV; ++j) x[j] *= scale;
-        }
-        absorb<U * EPV, true>(s, x);
+        absorb_chunk<DT, true, U, kScaled>(s, v, scale);
     }
 }
 
@@ -134,23 +169,17 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
                                                        split == 0, vb, ve, tid, p.scale);
     }
 
-    s = wave_reduce(s);
+    s = wave_reduce_flat(s);
     __shared__ Stat wave_stat[WAVES];
     const int lane = tid & 63;
     const int wave = tid >> 6;
     if (lane == 0) wave_stat[wave] = s;
     __syncthreads();
-    // Wave 0 merges the WAVES states in log2(WAVES) DPP steps (lane l reads
-    // state l % WAVES; the steps of row_reduce, as far as WAVES lanes need),
-    // rather than one LDS read and merge after another in thread 0: at 16
-    // waves (C1's 256 rows of 32000) the kernel takes 6.4 us instead of 7.6.
+    // Wave 0 merges the WAVES states as one flat reduction over a DPP row
+    // (lane l < WAVES holds state l).
     if (wave != 0) return;
     static_assert(WAVES <= 16, "one DPP row of states");
-    Stat r = wave_stat[lane & (WAVES - 1)];
-    if constexpr (WAVES >= 2) r = combine(r, stat_dpp<0xB1>(r));   // quad_perm [1,0,3,2]
-    if constexpr (WAVES >= 4) r = combine(r, stat_dpp<0x4E>(r));   // quad_perm [2,3,0,1]
-    if constexpr (WAVES >= 8) r = combine(r, stat_dpp<0x141>(r));  // row_half_mirror
-    if constexpr (WAVES >= 16) r = combine(r, stat_dpp<0x140>(r)); // row_mirror
+    const Stat r = row_reduce_flat(lane < WAVES ? wave_stat[lane] : stat_empty());
     if (lane != 0) return;  // thread 0 (it read the target logit)
 
     if (kSplit) {

@@ -10,6 +10,10 @@
 
 namespace klp {
 
+// Depth of the forward's register ring: chunks are loaded kFwdRing - 1
+// ahead of their use (klp_forward.hip).
+constexpr int kFwdRing = 3;
+
 struct FwdParams {
     const void* logits;
     RowMap rm;

@@ -125,9 +125,14 @@ def test_last_error_truncates():
 
 def test_default_launch_shapes():
     from kernel_opt import _C
-    # headline config: 1024 rows x 4 waves already fill 256 CUs, no split
-    w, u, s, f = _C.default_config("fwd", torch.bfloat16, 1024, 152064)
-    assert (w, s, f) == (4, 1, 0) and u in (2, 4)
+    # headline config: 1024 rows x 8 waves fill 256 CUs at 8 waves per SIMD,
+    # unroll 2 (61 VGPRs), no split
+    assert _C.default_config("fwd", torch.bfloat16, 1024, 152064) == (8, 2, 1, 0)
+    # several rounds of workgroups: unroll 4; fp32 rows on 4 waves
+    assert _C.default_config("fwd", torch.bfloat16, 32768, 151936) == (8, 4, 1, 0)
+    assert _C.default_config("fwd", torch.float32, 8192, 262144) == (4, 4, 1, 0)
+    # short rows (a vocab shard of C4): 4 waves, unroll 2
+    assert _C.default_config("fwd", torch.bfloat16, 32768, 18992) == (4, 2, 1, 0)
     # 256 rows: wider workgroups instead of splitting
     assert _C.default_config("fwd", torch.float32, 256, 32000)[::2] == (16, 1)
     # few rows, long vocab: split rows (two-kernel mode, needs a workspace)
