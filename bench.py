@@ -24,9 +24,11 @@ Timing, all with HIP events on the stream the kernels run on:
     256 MB Infinity Cache, so the step can beat the per-kernel rates);
   * `fwd_ms` / `bwd_ms`: one event pair around max(K, 50) back-to-back
     launches;
-  * `fwd_ms_flushed` / `bwd_ms_flushed`: each of max(K, 50) launches timed on
-    its own after a 1 GiB buffer was read (which evicts the logits from the
-    cache);
+  * `fwd_ms_flushed` / `bwd_ms_flushed`: max(K, 50) launches, each right
+    after a 1 GiB buffer was read (which evicts the logits from the cache):
+    one event pair around the (flush, launch) pairs minus one around the
+    flushes alone (`*_flushed_each` times every launch with its own event
+    pair instead, which adds the dispatch gap after the flush);
   * `ceilings`: in the same process, at the same size and launch shape, the
     library's calibration kernels (klp_ceiling_read: the forward's loads
     without arithmetic; klp_ceiling_copy: the backward's loads and stores)
@@ -809,8 +811,28 @@ class Timer:
             self.buf.fill_(k & 0xFF)
 
     def flushed(self, body):
-        """(mean, median) ms of `body` over K calls, each timed on its own
-        right after a flush."""
+        """(ms per launch, ms per launch timed on its own) of `body` right
+        after a flush.  The first figure is one event pair around K
+        (flush, body) pairs minus one around K flushes, so the dispatch gap
+        after each flush is not counted (it is what a kernel profiler
+        reports); the second times each launch with its own event pair
+        after its flush (includes that gap, about 3 us)."""
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(self.stream)
+        for k in range(self.K):
+            self.flush(k)
+            body()
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        with_body = a.elapsed_time(b)
+        a.record(self.stream)
+        for k in range(self.K):
+            self.flush(k)
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        flush_only = a.elapsed_time(b)
         ts = []
         for k in range(self.K):
             self.flush(k)
@@ -821,7 +843,7 @@ class Timer:
             b.record(self.stream)
             torch.cuda.synchronize()
             ts.append(a.elapsed_time(b))
-        return sum(ts) / len(ts), sorted(ts)[len(ts) // 2]
+        return (with_body - flush_only) / self.K, sum(ts) / len(ts)
 
 
 def _tbps(nbytes, ms):
@@ -874,8 +896,8 @@ def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None):
     kt = Timer(dev, max(K, KERNEL_LAUNCHES), timer.flush_mode, timer.buf)
     fwd_ms = kt.b2b(fwd)
     bwd_ms = kt.b2b(bwd)
-    fwd_fl, fwd_fl_med = kt.flushed(fwd)
-    bwd_fl, bwd_fl_med = kt.flushed(bwd)
+    fwd_fl, fwd_fl_each = kt.flushed(fwd)
+    bwd_fl, bwd_fl_each = kt.flushed(bwd)
 
     fwd_used = tuple(fcfg) if fcfg else _C.default_config("fwd", logits.dtype, N, V)
     bwd_used = tuple(bcfg) if bcfg else _C.default_config("bwd", logits.dtype, N, V)
@@ -938,8 +960,8 @@ def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None):
     out_ceil["bwd_over_copy_flushed"] = round(bwd_fl / ceil["copy_ms_flushed"], 4)
     return dict(inputs=inp, logits=logits, targets=targets, g_logp=g_logp, g_ent=g_ent,
                 N=N, V=V, esz=esz, fb=fb, bb=bb, step_ms=step_ms, wall=t_wall, fwd_ms=fwd_ms,
-                bwd_ms=bwd_ms, fwd_fl=fwd_fl, fwd_fl_med=fwd_fl_med, bwd_fl=bwd_fl,
-                bwd_fl_med=bwd_fl_med, fwd_used=fwd_used, bwd_used=bwd_used, ceilings=out_ceil,
+                bwd_ms=bwd_ms, fwd_fl=fwd_fl, fwd_fl_each=fwd_fl_each, bwd_fl=bwd_fl,
+                bwd_fl_each=bwd_fl_each, fwd_used=fwd_used, bwd_used=bwd_used, ceilings=out_ceil,
                 d_logits=d_logits)
 
 
@@ -1090,7 +1112,8 @@ def sweep(name, dev, K, timer, out_md):
     lines = [f"# Launch-shape sweep, workload {name} (build `{build_id()}`)", "",
              f"`python bench.py --config {name} --sweep OUT.md --steps {K}`: each shape timed "
              f"over {n} back-to-back launches (one event pair) and {n} launches each after a "
-             "1 GiB read (per-launch event pairs, mean). Defaults marked *.", "",
+             "1 GiB read (one event pair around the (read, launch) pairs minus one around "
+             "the reads alone). Defaults marked *.", "",
              "| kernel | waves | unroll | splits | b2b us | b2b % of 8 TB/s | flushed us | "
              "flushed % |", "|---|---:|---:|---:|---:|---:|---:|---:|"]
     _C.fwd_launch(x, t, lp, ent, lse)
@@ -1282,8 +1305,8 @@ def main(argv=None):
         "bwd_ms": round(bwd_ms, 5),
         "fwd_ms_flushed": round(fwd_fl, 5),
         "bwd_ms_flushed": round(bwd_fl, 5),
-        "fwd_ms_flushed_median": round(core["fwd_fl_med"], 5),
-        "bwd_ms_flushed_median": round(core["bwd_fl_med"], 5),
+        "fwd_ms_flushed_each": round(core["fwd_fl_each"], 5),
+        "bwd_ms_flushed_each": round(core["bwd_fl_each"], 5),
         "fwd_tbps": round(fwd_tbps, 4),
         "bwd_tbps": round(bwd_tbps, 4),
         "fwd_pct_peak": round(100 * fwd_tbps / HBM_PEAK_TBPS, 2),
