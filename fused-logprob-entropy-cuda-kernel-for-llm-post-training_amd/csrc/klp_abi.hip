@@ -11,11 +11,19 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/kernel_opt_hip.h"
 #include "../../include/kernel_opt_hip_tuning.h"
 #include "klp_launch.h"
+
+// Scratch of klp_fwd_noalloc: split-row partial states (one float4 per row
+// piece).  Each GPU holds its own copy until the process ends.  In host code
+// `scratch` is only a stand-in for the symbol: its address on a device comes
+// from hipGetSymbolAddress (noalloc_scratch below) and only that address is
+// ever passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[KLP_FWD_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -429,6 +437,33 @@ int ceiling_impl(bool copy, const void* src, void* dst, int64_t n_rows, int64_t 
     if (injected_failure(what)) return KLP_ELAUNCH;
     return after_launch(
         klp::launch_ceiling(copy, p, waves, unroll, static_cast<hipStream_t>(stream)), what);
+}
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int noalloc_scratch(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return fail(KLP_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(KLP_EINVAL, "device %d is beyond the %d the scratch table holds", dev,
+                    kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return fail(KLP_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return KLP_OK;
 }
 
 }  // namespace
@@ -896,6 +931,29 @@ int klp_ceiling_copy(const void* src, void* dst, int64_t n_rows, int64_t row_byt
                      int unroll, int splits, void* stream) {
     return ceiling_impl(true, src, dst, n_rows, row_bytes, waves, unroll, splits, nullptr, 0,
                         stream);
+}
+
+int klp_fwd_noalloc(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                    int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                    const int64_t* targets, float* logprob, float* entropy, float* lse,
+                    void* stream) {
+    int rc = check_rows(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
+                        targets);
+    if (rc != KLP_OK) return rc;
+    if (n_rows == 0) return ok();
+    const klp::FwdConfig cfg = default_fwd_config(dtype, n_rows, vocab);
+    const size_t need = workspace_bytes_for(n_rows, cfg.splits);
+    if (need > KLP_FWD_NOALLOC_SCRATCH_BYTES)
+        return fail(KLP_EWORKSPACE,
+                    "klp_fwd_noalloc: %lld rows in %d pieces need %zu bytes of split-row scratch, "
+                    "more than the %d it holds; use klp_fwd with a workspace",
+                    static_cast<long long>(n_rows), cfg.splits, need,
+                    KLP_FWD_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (need > 0 && (rc = noalloc_scratch(&ws)) != KLP_OK) return rc;
+    return fwd_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner, targets,
+                    logprob, entropy, lse, ws, ws ? size_t{KLP_FWD_NOALLOC_SCRATCH_BYTES} : 0, cfg,
+                    1.0f, stream);
 }
 
 }  // extern "C"

@@ -30,6 +30,8 @@ KLP_OK, KLP_EINVAL, KLP_EDTYPE, KLP_ELAUNCH, KLP_EWORKSPACE = 0, 1, 2, 3, 4
 # klp_grpo_loss_type / klp_grpo_level values
 KLP_GRPO_LOSS_GRPO, KLP_GRPO_LOSS_BNPO, KLP_GRPO_LOSS_FIXED = 0, 1, 2
 KLP_GRPO_TOKEN, KLP_GRPO_SEQUENCE = 0, 1
+# klp_fwd_noalloc's split-row scratch per GPU (KLP_FWD_NOALLOC_SCRATCH_BYTES).
+KLP_FWD_NOALLOC_SCRATCH_BYTES = 65536
 # klp_grpo_step's row counter (KLP_GRPO_STEP_SCHED_BYTES).
 KLP_GRPO_STEP_SCHED_BYTES = 16
 
@@ -45,6 +47,7 @@ SIGNATURES = {
     "klp_fwd_naive": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp]),
     "klp_bwd": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "klp_fwd_temp": (_i32, _ROWS + [_vp, ctypes.c_float, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "klp_fwd_noalloc": (_i32, _ROWS + [_vp, _vp, _vp, _vp, _vp]),
     "klp_bwd_temp": (_i32, _ROWS + [_vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "klp_debug_fail_next_launches": (None, [_i32]),
     "klp_lmh_workspace_bytes": (_sz, [_i64, _i64, _i64]),

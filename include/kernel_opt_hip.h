@@ -155,6 +155,29 @@ int klp_bwd_temp(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                  void* stream);
 
 /*
+ * klp_fwd without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  No counterpart in the reference.
+ *
+ * When the default launch shape splits rows (few rows of a long vocabulary),
+ * the split-row partial states go to a scratch array of
+ * KLP_FWD_NOALLOC_SCRATCH_BYTES that the library keeps on each GPU it runs
+ * on until the process ends; a problem whose partial states would not fit is
+ * rejected with KLP_EWORKSPACE (the current dispatcher needs at most 8 KiB:
+ * it splits only while rows x pieces < 512).  The array needs no clearing:
+ * every launch writes each state before reading it.  All calls on one GPU
+ * share that GPU's array, so calls that overlap on one GPU (on other
+ * streams, from other threads) race and must be ordered by the caller.
+ * Arguments and results as klp_fwd.
+ */
+#define KLP_FWD_NOALLOC_SCRATCH_BYTES 65536
+int klp_fwd_noalloc(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                    int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                    const int64_t* targets,
+                    float* logprob, float* entropy, float* lse,
+                    void* stream);
+
+/*
  * Vocabulary shards (a vocab-parallel LM head: each rank holds columns
  * [vocab_offset, vocab_offset + vocab) of the logits).  No counterpart in the
  * reference, which has no multi-GPU path; these are the per-rank pieces of

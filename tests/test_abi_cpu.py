@@ -414,3 +414,21 @@ def test_ceiling_validation_errors():
         assert copy() == KLP_ELAUNCH and "ceiling copy" in _err()
     finally:
         lib.klp_debug_fail_next_launches(0)
+
+
+def test_noalloc_forward_validation_errors():
+    """klp_fwd_noalloc checks its arguments before it touches a device, and
+    n_rows = 0 is a no-op."""
+    from kernel_opt._library import KLP_EDTYPE, KLP_EINVAL, lib
+    A = ctypes.c_void_p(0x100000)
+
+    def fwd(**kw):
+        a = dict(x=A, dtype=0, n=4, V=100, t=A, o=A)
+        a.update(kw)
+        return lib.klp_fwd_noalloc(a["x"], a["dtype"], a["n"], a["V"], a["n"], 0, a["V"],
+                                   a["t"], a["o"], a["o"], a["o"], None)
+    assert fwd(n=0, x=None, t=None) == 0
+    assert fwd(dtype=7) == KLP_EDTYPE and "dtype" in _err()
+    assert fwd(V=0) == KLP_EINVAL and "vocab" in _err()
+    assert fwd(x=None) == KLP_EINVAL and "non-null" in _err()
+    assert fwd(t=ctypes.c_void_p(0x100004)) == KLP_EINVAL and "targets" in _err()
