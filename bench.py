@@ -654,37 +654,50 @@ def shard_timing(dev, K, N=32768, V=151936, P=8):
     return out
 
 
-def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
-    """The fused LM head (hidden @ weight^T folded into the logprob/entropy
-    reduction, klp_lmh_*) against the unfused path (a bf16 library matmul,
-    then the logprob kernels) on Qwen2.5-7B's head shape with C2's 1024
-    tokens; random weights.  Forward, and forward + backward with upstream
-    gradients on logprob and entropy."""
+def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5, rounds=5):
+    """The fused LM head against the unfused path on Qwen2.5-7B's head shape
+    with C2's 1024 tokens (and 8x that), random weights.  Three paths:
+    "chunked" (the default: a library GEMM per vocabulary chunk, then
+    klp_fwd_shard / klp_fwd_shard_merge; the backward recomputes each chunk),
+    "mfma" (klp_lmh_fwd, the hand-written GEMM with the reduction as its
+    epilogue) and "unfused" (a bf16 library matmul to the [N, V] logits, then
+    klp_fwd / klp_bwd).  Forward, and forward + backward with upstream
+    gradients on logprob and entropy; medians over interleaved rounds of K
+    calls; peak memory beyond the inputs (and, for the backward, beyond the
+    new gradients)."""
+    import statistics
     from kernel_opt import (fused_linear_logprob_entropy, fused_linear_logprob_entropy_forward,
                             fused_logprob_entropy, fused_logprob_entropy_forward)
     g = torch.Generator(device=dev).manual_seed(3584)
-    h = torch.randn(N, D, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
     w = (torch.randn(V, D, device=dev, generator=g) / D ** 0.5 * 3).to(torch.bfloat16)
     w.requires_grad_(True)
-    t = torch.randint(0, V, (N,), device=dev, generator=g)
-    gl = torch.randn(N, device=dev, generator=g)
-    ge = torch.randn(N, device=dev, generator=g)
 
-    def fb(fused):
+    def inputs(n_tok):
+        hh = torch.randn(n_tok, D, device=dev, generator=g).to(torch.bfloat16)
+        hh.requires_grad_(True)
+        return (hh, torch.randint(0, V, (n_tok,), device=dev, generator=g),
+                torch.randn(n_tok, device=dev, generator=g),
+                torch.randn(n_tok, device=dev, generator=g))
+
+    def fwd(impl, h, t):
+        with torch.no_grad():
+            if impl == "unfused":
+                return fused_logprob_entropy_forward(h @ w.T, t)
+            return fused_linear_logprob_entropy_forward(h, w, t, impl=impl)
+
+    def fb(impl, h, t, gl, ge):
         h.grad = None
         w.grad = None
-        if fused:
-            lp, ent, _ = fused_linear_logprob_entropy(h, w, t)
-        else:
+        if impl == "unfused":
             lp, ent, _ = fused_logprob_entropy(h @ w.T, t)
+        else:
+            lp, ent, _ = fused_linear_logprob_entropy(h, w, t, impl=impl)
         ((lp * gl).sum() + (ent * ge).sum()).backward()
 
     def timed(fn):
-        for _ in range(2):
-            fn()
-        torch.cuda.synchronize()
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
         a.record()
         for _ in range(K):
             fn()
@@ -692,12 +705,47 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
         torch.cuda.synchronize()
         return a.elapsed_time(b) / K
 
-    with torch.no_grad():
-        f_fwd = timed(lambda: fused_linear_logprob_entropy_forward(h, w, t))
-        u_fwd = timed(lambda: fused_logprob_entropy_forward(h @ w.T, t))
-    f_fb = timed(lambda: fb(True))
-    u_fb = timed(lambda: fb(False))
+    def medians(fns):
+        for fn in fns.values():
+            fn()
+            fn()
+        times = {k: [] for k in fns}
+        for _ in range(rounds):
+            for k, fn in fns.items():
+                times[k].append(timed(fn))
+        return {k: round(statistics.median(v), 4) for k, v in times.items()}
 
+    def peak_mib(fn, h):
+        fn()
+        h.grad = None
+        w.grad = None
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        fn()
+        torch.cuda.synchronize()
+        extra = torch.cuda.max_memory_allocated() - base
+        if h.grad is not None:
+            extra -= h.grad.numel() * h.grad.element_size() + w.grad.numel() * 2
+        h.grad = None
+        w.grad = None
+        return round(extra / 2 ** 20, 1)
+
+    runs = []
+    for n_tok, impls in ((N, ("chunked", "mfma", "unfused")), (8 * N, ("chunked", "unfused"))):
+        h, t, gl, ge = inputs(n_tok)
+        f_ms = medians({i: (lambda i=i: fwd(i, h, t)) for i in impls})
+        fb_ms = medians({i: (lambda i=i: fb(i, h, t, gl, ge)) for i in impls})
+        run = {"tokens": n_tok}
+        for i in impls:
+            run[i] = {"fwd_ms": f_ms[i], "fwd_bwd_ms": fb_ms[i],
+                      "fwd_tflops": round(2 * n_tok * V * D / (f_ms[i] * 1e-3) / 1e12, 1),
+                      "fwd_peak_extra_mib": peak_mib(lambda i=i: fwd(i, h, t), h),
+                      "fwd_bwd_peak_beyond_grads_mib":
+                          peak_mib(lambda i=i: fb(i, h, t, gl, ge), h)}
+        runs.append(run)
+        del h, t, gl, ge
+        torch.cuda.empty_cache()
     # GRPO on the head: the chunked LM head + fused step (library GEMMs and
     # klp_grpo_step per chunk of tokens) against the unfused path (bf16
     # matmul to the full logits, the logprob op, the GRPO loss, backward), at
@@ -742,6 +790,8 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
         out = {"tokens": n_tok}
         for chunk in [0] + chunks:
             name = f"chunked_{chunk}" if chunk else "unfused"
+            run(chunk)
+            run(chunk)
             out[name + "_fwd_bwd_ms"] = round(timed(lambda: run(chunk)), 4)
             out[name + "_peak_extra_mib"] = peak_extra(chunk)
         hh.grad = None
@@ -753,16 +803,18 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
     grpo_heads = [grpo_head(N, [N, N // 4]), grpo_head(8 * N, ["default", 2 * N])]
     torch.cuda.empty_cache()
 
-    flops = 2 * N * V * D
-    out = {"shape": {"tokens": N, "vocab": V, "hidden": D}, "dtype": "bf16 in, fp32 accumulate",
-           "fused_fwd_ms": round(f_fwd, 4), "unfused_fwd_ms": round(u_fwd, 4),
-           "fused_fwd_tflops": round(flops / (f_fwd * 1e-3) / 1e12, 1),
-           "fused_fwd_bwd_ms": round(f_fb, 4), "unfused_fwd_bwd_ms": round(u_fb, 4),
-           "roofline_fwd": {"bound": "mfma", "achieved": round(flops / (f_fwd * 1e-3) / 1e12, 1),
+    c = runs[0]["chunked"]
+    out = {"shape": {"tokens": N, "vocab": V, "hidden": D}, "dtype": "bf16",
+           "runs": runs,
+           "fused_fwd_ms": c["fwd_ms"], "unfused_fwd_ms": runs[0]["unfused"]["fwd_ms"],
+           "fused_fwd_bwd_ms": c["fwd_bwd_ms"],
+           "unfused_fwd_bwd_ms": runs[0]["unfused"]["fwd_bwd_ms"],
+           "roofline_fwd": {"bound": "mfma", "achieved": c["fwd_tflops"],
                             "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                            "frac": round(flops / (f_fwd * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-                                          4)},
-           "note": "unfused = bf16 library matmul to [N, V] logits, then klp_fwd / klp_bwd",
+                            "frac": round(c["fwd_tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)},
+           "note": "fused = the chunked head (default); mfma = klp_lmh_fwd with the "
+                   "vocabulary-chunked backward; unfused = bf16 library matmul to [N, V] "
+                   "logits, then klp_fwd / klp_bwd; medians of interleaved rounds",
            "grpo_step": {
                "runs": grpo_heads,
                "note": "fused_linear_grpo_step (chunks of the given token count, 'default' "
@@ -771,7 +823,7 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5):
                        "against matmul + fused_logprob_entropy + fused_grpo_loss + backward; "
                        "loss + backward per iteration; peak memory above inputs and weights "
                        "during one iteration, the new gradients included"}}
-    del h, w
+    del w
     torch.cuda.empty_cache()
     return out
 

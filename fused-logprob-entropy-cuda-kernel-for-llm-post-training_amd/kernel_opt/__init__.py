@@ -16,6 +16,7 @@ from .linear_grpo import fused_linear_grpo_step  # noqa: F401
 from .lmhead import (  # noqa: F401
     fused_linear_logprob_entropy,
     fused_linear_logprob_entropy_forward,
+    vocab_chunk,
 )
 
 

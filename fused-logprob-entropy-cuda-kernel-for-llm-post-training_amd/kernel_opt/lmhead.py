@@ -1,21 +1,42 @@
-"""Fused LM head + per-token logprob / entropy.
+"""LM head + per-token logprob / entropy without the ``[N, V]`` logits.
 
 ``fused_linear_logprob_entropy(hidden, weight, targets)`` returns what
-``fused_logprob_entropy(hidden @ weight.T, targets)`` returns, without
-materialising the ``[N, V]`` logits in the forward: one MFMA GEMM kernel folds
-each block of logits into the online softmax state as it is produced
-(klp_lmh_fwd, csrc/klp_lmhead.hip).  The reference names this as its
-follow-up (docs/FINAL_REPORT.md:439-450) and does not build it.
+``fused_logprob_entropy(hidden @ weight.T, targets)`` returns, and so does its
+backward, while neither pass holds the ``[N, V]`` logits (or their gradient):
+the Liger-style head the reference names as its follow-up
+(docs/FINAL_REPORT.md:439-450, 490-493) and does not build.
 
-The logits are the fp32 sums of the bf16 products, not rounded to bf16 as a
-bf16 matmul output would be; the results are therefore closer to the exact
-values than the unfused bf16 path.
+Two implementations:
 
-Backward: klp_lmh_bwd_logits recomputes every logits block with the same
-MFMA order as the forward (so the softmax is rebuilt from the very values
-behind the saved lse) and writes d_logits in bf16; d_hidden = d_logits @ W
-and d_weight = d_logits^T @ hidden are plain library GEMMs.  Nothing of size
-[N, V] is kept between forward and backward.
+``impl="chunked"`` (default) walks the vocabulary in chunks of ~16K columns.
+Per chunk a library GEMM writes the chunk's logits (``[N, chunk]`` in the
+input dtype, 32 MiB at N = 1024: small enough to stay in the 256 MB
+Infinity Cache) and ``klp_fwd_shard`` folds them into each token's online
+state straight from the cache; ``klp_fwd_shard_merge`` merges the chunk
+states in chunk order.  The weight is read once, the logits never reach HBM
+as one tensor, and the logprob pass reads cache instead of HBM.  The
+backward recomputes each chunk with the same GEMM call (bit-identical
+logits), applies ``klp_bwd`` with chunk-relative targets, and accumulates
+``d_hidden += d_chunk @ W_chunk`` (fp32) and ``d_weight[chunk] = d_chunk^T @
+hidden``.  Numerics are the unfused path's: logits rounded once to the input
+dtype by the GEMM.
+
+``impl="mfma"`` is the hand-written gfx950 kernel (klp_lmh_fwd,
+csrc/klp_lmhead.hip): the GEMM with the logprob / entropy reduction as its
+epilogue, logits kept as fp32 MFMA sums (never rounded), bf16 inputs, hidden
+size a multiple of 64.  Its backward recomputes chunks of logits with the
+same MFMA order (klp_lmh_bwd_logits on a slice of the weight) and runs the
+same two library GEMMs per chunk.  It is slower than the library GEMM at
+these shapes (measured at 1024 tokens of Qwen2.5-7B's head: forward 1.30 ms
+against 0.98 chunked and 0.93 unfused).
+
+The backward of either head recomputes the logits, one GEMM more than the
+unfused path's backward: that is the price of not holding them (measured
+forward + backward at 1024 tokens: 4.82 ms chunked, 3.87 ms unfused, with
+67 MiB against 297 MiB beyond the inputs and gradients).  When the loss is
+known in the forward, :func:`kernel_opt.fused_linear_grpo_step` computes the
+gradients there and needs no recompute.
+
 ``fused_linear_logprob_entropy_forward`` is the no-grad entry point (GRPO's
 old-policy and reference log-probabilities).
 """
@@ -26,9 +47,11 @@ import threading
 
 import torch
 
-from ._library import check_status, device_guard, lib, ptr, stream_handle
+from . import _C
+from ._library import DTYPE_CODES, check_status, device_guard, lib, ptr, stream_handle
+from .linear_grpo import _accumulate_f32
 
-__all__ = ["fused_linear_logprob_entropy", "fused_linear_logprob_entropy_forward"]
+__all__ = ["fused_linear_logprob_entropy", "fused_linear_logprob_entropy_forward", "vocab_chunk"]
 
 
 _ptr = ptr
@@ -57,11 +80,15 @@ def _workspace(dev, stream, nbytes):
         return buf
 
 
-def _check(hidden, weight, targets):
+def _check(hidden, weight, targets, impl):
+    if impl not in ("chunked", "mfma"):
+        raise ValueError(f"impl must be 'chunked' or 'mfma', got {impl!r}")
     if not (hidden.is_cuda and weight.is_cuda and targets.is_cuda):
         raise RuntimeError("hidden, weight and targets must be GPU tensors")
-    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+    if impl == "mfma" and (hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16):
         raise RuntimeError("hidden and weight must be bfloat16")
+    if hidden.dtype not in DTYPE_CODES or weight.dtype != hidden.dtype:
+        raise RuntimeError("hidden and weight must share one dtype: bf16, fp16 or fp32")
     if targets.dtype != torch.int64:
         raise RuntimeError("targets must be int64")
     D = hidden.size(-1)
@@ -81,13 +108,104 @@ def _ld(t: torch.Tensor) -> int:
     return t.stride(0) if t.size(0) > 1 else t.size(1)
 
 
+# Vocabulary chunk of the chunked head: about CHUNK_COLS columns, balanced
+# over the vocabulary in whole multiples of 1024 (so that no small tail GEMM
+# runs), and fewer while one chunk of logits would exceed CHUNK_MAX_BYTES.
+CHUNK_COLS = 16384
+CHUNK_MAX_BYTES = 256 << 20
+
+
+def vocab_chunk(n_tokens: int, vocab: int, elem_bytes: int = 2,
+                chunk_vocab: int | None = None) -> int:
+    """Columns per chunk of the chunked head (the last chunk may hold
+    fewer)."""
+    if chunk_vocab is not None:
+        if chunk_vocab < 1:
+            raise ValueError(f"chunk_vocab must be >= 1, got {chunk_vocab}")
+        return min(int(chunk_vocab), max(vocab, 1))
+    cols = CHUNK_COLS
+    while cols > 1024 and n_tokens * cols * elem_bytes > CHUNK_MAX_BYTES:
+        cols //= 2
+    n_chunks = max(1, -(-vocab // cols))
+    per = -(-vocab // n_chunks)
+    return min(vocab, -(-per // 1024) * 1024)
+
+
+def _chunk_logits(buf, h2, weight, c0, n):
+    """logits[:, c0:c0+n] = h2 @ weight[c0:c0+n]^T into a contiguous view of
+    ``buf`` (the same call, hence the same values, in forward and backward)."""
+    out = buf[: h2.size(0) * n].view(h2.size(0), n)
+    torch.mm(h2, weight[c0:c0 + n].t(), out=out)
+    return out
+
+
+def _forward_chunked(h2, weight, t, T, vc, out):
+    N, V = h2.size(0), weight.size(0)
+    n_chunks = -(-V // vc)
+    dev = h2.device
+    states = torch.empty(n_chunks, N, 4, dtype=torch.float32, device=dev)
+    buf = torch.empty(N * min(vc, V), dtype=h2.dtype, device=dev)
+    code = DTYPE_CODES[h2.dtype]
+    with device_guard(dev.index):
+        stream = stream_handle(dev.index)
+        for c in range(n_chunks):
+            c0 = c * vc
+            n = min(vc, V - c0)
+            lg = _chunk_logits(buf, h2, weight, c0, n)
+            check_status(lib.klp_fwd_shard(_ptr(lg), code, N, n, *_C.row_layout(lg), _ptr(t),
+                                           c0, T, _ptr(states[c]), stream))
+        check_status(lib.klp_fwd_shard_merge(_ptr(states), n_chunks, N, _ptr(t), vc, V,
+                                             _ptr(out[0]), _ptr(out[1]), _ptr(out[2]), stream))
+
+
+def _backward_chunked(h2, weight, t, T, vc, lse, ent, gl, ge, gs, need_h, need_w, impl):
+    """d_hidden (fp32, or None) and d_weight (weight dtype, or None), one
+    vocabulary chunk at a time: d_logits exist for one chunk only."""
+    N, D, V = h2.size(0), h2.size(1), weight.size(0)
+    dev = h2.device
+    dh = torch.zeros(N, D, dtype=torch.float32, device=dev) if need_h else None
+    dw = torch.empty(V, D, dtype=weight.dtype, device=dev) if need_w else None
+    cols = min(vc, V)
+    d_buf = torch.empty(N * (-(-cols // 4) * 4), dtype=weight.dtype, device=dev)
+    lg_buf = torch.empty(N * cols, dtype=h2.dtype, device=dev) if impl == "chunked" else None
+    with device_guard(dev.index):
+        stream = stream_handle(dev.index)
+        for c0 in range(0, V, vc):
+            n = min(vc, V - c0)
+            tc = t - c0  # chunk-relative: a target outside the chunk adds no one-hot term
+            if impl == "chunked":
+                lg = _chunk_logits(lg_buf, h2, weight, c0, n)
+                d = d_buf[: N * n].view(N, n)
+                check_status(lib.klp_bwd_temp(_ptr(lg), DTYPE_CODES[lg.dtype], N, n,
+                                              *_C.row_layout(lg),
+                                              _ptr(tc), T, _ptr(lse), _ptr(ent), _ptr(gl),
+                                              _ptr(ge), _ptr(gs), _ptr(d), stream))
+            else:
+                ld_d = -(-n // 4) * 4
+                dpad = d_buf[: N * ld_d].view(N, ld_d)
+                w_c = weight[c0:c0 + n]
+                check_status(lib.klp_lmh_bwd_logits(
+                    _ptr(h2), _ld(h2), _ptr(w_c), _ld(weight), N, n, D, _ptr(tc), T, _ptr(lse),
+                    _ptr(ent), _ptr(gl), _ptr(ge), _ptr(gs), _ptr(dpad), ld_d, stream))
+                d = dpad[:, :n]
+            w_c = weight[c0:c0 + n]
+            if need_h:
+                _accumulate_f32(dh, d, w_c)
+            if need_w:
+                torch.mm(d.t(), h2, out=dw[c0:c0 + n])
+    return dh, dw
+
+
 class _FusedLinearLogprobEntropy(torch.autograd.Function):
 
     @staticmethod
-    def forward(ctx, hidden, weight, targets, temperature):
-        outs = fused_linear_logprob_entropy_forward(hidden, weight, targets, temperature)
+    def forward(ctx, hidden, weight, targets, temperature, impl, chunk_vocab):
+        outs = fused_linear_logprob_entropy_forward(hidden, weight, targets, temperature,
+                                                    impl=impl, chunk_vocab=chunk_vocab)
         ctx.save_for_backward(hidden, weight, targets, outs[2], outs[1])
         ctx.temperature = temperature
+        ctx.impl = impl
+        ctx.chunk_vocab = chunk_vocab
         ctx.set_materialize_grads(False)
         return outs
 
@@ -95,57 +213,58 @@ class _FusedLinearLogprobEntropy(torch.autograd.Function):
     def backward(ctx, g_logp, g_ent, g_lse):
         hidden, weight, targets, lse, ent = ctx.saved_tensors
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        none = (None,) * 4
         if not (need_h or need_w):
-            return None, None, None, None
-        h2, t = _check(hidden, weight, targets)
-        N, D, V = h2.size(0), h2.size(1), weight.size(0)
+            return (None, None) + none
+        h2, t = _check(hidden, weight, targets, ctx.impl)
+        N, V = h2.size(0), weight.size(0)
         if N == 0:
             return (torch.zeros_like(hidden) if need_h else None,
-                    torch.zeros_like(weight) if need_w else None, None, None)
+                    torch.zeros_like(weight) if need_w else None) + none
 
         def prep(g):
             return None if g is None else g.to(torch.float32, copy=False).reshape(-1).contiguous()
 
-        gl, ge, gs = prep(g_logp), prep(g_ent), prep(g_lse)
-        ld_d = (V + 3) // 4 * 4
-        d = torch.empty(N, ld_d, dtype=torch.bfloat16, device=hidden.device)
         T = 1.0 if ctx.temperature is None else float(ctx.temperature)
-        with device_guard(hidden.device.index):
-            stream = stream_handle(hidden.device.index)
-            rc = lib.klp_lmh_bwd_logits(
-                _ptr(h2), _ld(h2), _ptr(weight), _ld(weight), N, V, D, _ptr(t), T,
-                _ptr(lse), _ptr(ent), None if gl is None else _ptr(gl),
-                None if ge is None else _ptr(ge), None if gs is None else _ptr(gs),
-                _ptr(d), ld_d, stream)
-        check_status(rc)
-        dl = d[:, :V]
-        dh = torch.mm(dl, weight).reshape(hidden.shape) if need_h else None
-        dw = torch.mm(dl.t(), h2) if need_w else None
-        return dh, dw, None, None
+        vc = vocab_chunk(N, V, h2.element_size(), ctx.chunk_vocab)
+        dh, dw = _backward_chunked(h2, weight, t, T, vc, lse.reshape(-1), ent.reshape(-1),
+                                   prep(g_logp), prep(g_ent), prep(g_lse), need_h, need_w,
+                                   ctx.impl)
+        if dh is not None:
+            dh = dh.to(hidden.dtype).reshape(hidden.shape)
+        return (dh, dw) + none
 
 
 def fused_linear_logprob_entropy(hidden: torch.Tensor, weight: torch.Tensor,
-                                 targets: torch.Tensor, temperature: float | None = None):
-    """Autograd-aware fused LM head + logprob / entropy: gradients flow to
+                                 targets: torch.Tensor, temperature: float | None = None, *,
+                                 impl: str = "chunked", chunk_vocab: int | None = None):
+    """Autograd-aware LM head + logprob / entropy: gradients flow to
     ``hidden`` and ``weight`` (see :func:`fused_linear_logprob_entropy_forward`
     for the arguments and the module docstring for the backward)."""
-    return _FusedLinearLogprobEntropy.apply(hidden, weight, targets, temperature)
+    return _FusedLinearLogprobEntropy.apply(hidden, weight, targets, temperature, impl,
+                                            chunk_vocab)
 
 
 def fused_linear_logprob_entropy_forward(hidden: torch.Tensor, weight: torch.Tensor,
                                          targets: torch.Tensor,
-                                         temperature: float | None = None):
+                                         temperature: float | None = None, *,
+                                         impl: str = "chunked",
+                                         chunk_vocab: int | None = None):
     """Args:
-        hidden: ``[..., D]`` bf16 on the GPU, rows with unit stride (the
-            leading dims must flatten to one stride).
-        weight: ``[V, D]`` bf16 (an ``nn.Linear`` weight), rows with unit stride.
+        hidden: ``[..., D]`` on the GPU, rows with unit stride (the leading
+            dims must flatten to one stride).
+        weight: ``[V, D]`` (an ``nn.Linear`` weight) of hidden's dtype, rows
+            with unit stride.
         targets: ``[...]`` int64, same leading shape as ``hidden``.
         temperature: optional T > 0; logits are multiplied by fp32(1/T).
-    D must be a multiple of 64 and both row strides multiples of 8.
+        impl: ``"chunked"`` (bf16 / fp16 / fp32) or ``"mfma"`` (bf16, D a
+            multiple of 64, both row strides multiples of 8).
+        chunk_vocab: columns per vocabulary chunk (chunked head, and the
+            backward of both); default :func:`vocab_chunk`.
 
     Returns ``(logprob, entropy, lse)``, float32, shaped like ``targets``.
     """
-    h2, t = _check(hidden, weight, targets)
+    h2, t = _check(hidden, weight, targets, impl)
     D = h2.size(1)
     N, V = h2.size(0), weight.size(0)
     out = [torch.empty(targets.shape, dtype=torch.float32, device=hidden.device)
@@ -153,6 +272,11 @@ def fused_linear_logprob_entropy_forward(hidden: torch.Tensor, weight: torch.Ten
     if N == 0:
         return tuple(out)
     T = 1.0 if temperature is None else float(temperature)
+    if not (T > 0.0 and T != float("inf")):
+        raise RuntimeError(f"temperature must be finite and > 0, got {T}")
+    if impl == "chunked":
+        _forward_chunked(h2, weight, t, T, vocab_chunk(N, V, h2.element_size(), chunk_vocab), out)
+        return tuple(out)
     dev = hidden.device
     with device_guard(dev.index):
         stream = stream_handle(dev.index)
