@@ -843,12 +843,20 @@ class Timer:
         self.buf = buf if buf is not None else torch.ones(FLUSH_BYTES, dtype=torch.uint8,
                                                           device=dev)
 
-    def b2b(self, body):
+    QUEUE_SPIN_CYCLES = 4_000_000  # ~2 ms of shader clock
+
+    def b2b(self, body, queued=True):
         """Average ms of `body` over K back-to-back calls: one event pair
-        around the whole loop."""
+        around the whole loop.  With `queued` a spin kernel runs first
+        (before the first event), so the host enqueues the K calls while it
+        spins and the GPU then runs them without waiting for the host: the
+        figure is GPU time even where one call's host issue (~7 us through
+        ctypes) exceeds its kernel's duration."""
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        if queued:
+            torch.cuda._sleep(self.QUEUE_SPIN_CYCLES)
         a.record(self.stream)
         for _ in range(self.K):
             body()
@@ -862,29 +870,36 @@ class Timer:
         else:
             self.buf.fill_(k & 0xFF)
 
+    FLUSH_ROUNDS = 5
+
     def flushed(self, body):
         """(ms per launch, ms per launch timed on its own) of `body` right
-        after a flush.  The first figure is one event pair around K
-        (flush, body) pairs minus one around K flushes, so the dispatch gap
+        after a flush.  The first figure is the median over FLUSH_ROUNDS
+        rounds of: one event pair around K / FLUSH_ROUNDS (flush, body)
+        pairs minus one around as many flushes alone, so the dispatch gap
         after each flush is not counted (it is what a kernel profiler
-        reports); the second times each launch with its own event pair
-        after its flush (includes that gap, about 3 us)."""
-        torch.cuda.synchronize()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(self.stream)
-        for k in range(self.K):
-            self.flush(k)
-            body()
-        b.record(self.stream)
-        torch.cuda.synchronize()
-        with_body = a.elapsed_time(b)
-        a.record(self.stream)
-        for k in range(self.K):
-            self.flush(k)
-        b.record(self.stream)
-        torch.cuda.synchronize()
-        flush_only = a.elapsed_time(b)
+        reports), and a round whose flushes ran at another speed than its
+        neighbours' (clock changes) does not set the result; one round runs
+        first untimed.  The second figure times each launch with its own
+        event pair after its flush (includes that gap, about 3 us)."""
+        n = max(1, self.K // self.FLUSH_ROUNDS)
+
+        def loop(with_body):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record(self.stream)
+            for k in range(n):
+                self.flush(k)
+                if with_body:
+                    body()
+            b.record(self.stream)
+            torch.cuda.synchronize()
+            return a.elapsed_time(b)
+
+        loop(True)
+        loop(False)
+        diffs = sorted((loop(True) - loop(False)) / n for _ in range(self.FLUSH_ROUNDS))
         ts = []
         for k in range(self.K):
             self.flush(k)
@@ -895,7 +910,7 @@ class Timer:
             b.record(self.stream)
             torch.cuda.synchronize()
             ts.append(a.elapsed_time(b))
-        return (with_body - flush_only) / self.K, sum(ts) / len(ts)
+        return diffs[len(diffs) // 2], sum(ts) / len(ts)
 
 
 def _tbps(nbytes, ms):
@@ -1124,9 +1139,14 @@ def c1_leg(dev, K, timer, with_cpu):
         fwd()
         bwd()
     f_ms, b_ms = timer.b2b(fwd), timer.b2b(bwd)
+    f_host, b_host = timer.b2b(fwd, queued=False), timer.b2b(bwd, queued=False)
     out = {"workload": "C1: logits [2,128,32000] float32", "fwd_us": round(f_ms * 1e3, 3),
            "bwd_us": round(b_ms * 1e3, 3), "fwd_tbps": round(_tbps(fb, f_ms), 4),
            "bwd_tbps": round(_tbps(bb, b_ms), 4),
+           "fwd_us_host_paced": round(f_host * 1e3, 3), "bwd_us_host_paced": round(b_host * 1e3, 3),
+           "timing": "GPU time per launch, launches queued behind a spin kernel; *_host_paced: "
+                     "calls issued back to back from Python without it (at this size the "
+                     "host's issue rate, ~7 us a call, sets the pace)",
            "fwd_launch": dict(zip(("waves", "unroll", "splits", "flags"),
                                   _C.default_config("fwd", x.dtype, N, V))),
            "bwd_launch": dict(zip(("waves", "unroll", "splits", "flags"),

@@ -18,11 +18,12 @@
 #include "../../include/kernel_opt_hip_tuning.h"
 #include "klp_launch.h"
 
-// Scratch of klp_fwd_noalloc: split-row partial states (one float4 per row
-// piece).  Each GPU holds its own copy until the process ends.  In host code
+// Scratch of klp_fwd_noalloc: the split-row workspace (piece states and row
+// arrival counters), cleared once per device at set-up and left zero by every
+// call.  Each GPU holds its own copy until the process ends.  In host code
 // `scratch` is only a stand-in for the symbol: its address on a device comes
 // from hipGetSymbolAddress (noalloc_scratch below) and only that address is
-// ever passed to a kernel.
+// ever passed to a kernel or to hipMemset.
 static __device__ __align__(256) unsigned char scratch[KLP_FWD_NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -50,12 +51,12 @@ int elem_bytes(int dtype) { return dtype == KLP_FP32 ? 4 : 2; }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// Launch-shape targets.  Forward: at least kFwdTargetWaves resident wave64s
-// (16 per CU on 256 CUs) so that enough 16-byte loads are in flight to cover
-// HBM latency; rows are split across workgroups only when a whole 1024-thread
-// workgroup per row still leaves the chip short of that.  Backward: splitting
-// needs no second pass; see default_bwd_config.
+// Launch-shape targets.  Forward: grids of fewer than kFwdTargetWaves
+// wave64s (16 per CU on 256 CUs) at 8 waves per row are "few rows", where
+// rows are split across workgroups (up to kFwdSplitGrid of them, one per
+// CU) to put more loads in flight.  Backward: see default_bwd_config.
 constexpr int64_t kFwdTargetWaves = 4096;
+constexpr int64_t kFwdSplitGrid = 256;
 // Wave64s resident at 8 per SIMD on 256 CUs: a grid up to this size runs as
 // one round of workgroups.
 constexpr int64_t kFwdOneRoundWaves = 8192;
@@ -142,15 +143,31 @@ klp::FwdConfig default_fwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     int w = 8;
     while (w > 1 && int64_t{w} * 64 * 8 > nvec) w /= 2;
     if (w == 8 && n_rows * w < kFwdTargetWaves) {
-        // Few rows of a long vocabulary: 16-wave workgroups, split rows
-        // while still short of the wave target and every piece keeps each
-        // thread busy for at least two full chunks.
-        c.waves = 16;
-        c.unroll = 4;
-        const int64_t tile = static_cast<int64_t>(c.waves) * 64 * c.unroll;
-        while (c.splits < kMaxSplits && n_rows * c.splits * c.waves < kFwdTargetWaves &&
-               nvec / (2 * c.splits) >= 2 * tile)
-            c.splits *= 2;
+        // Few rows of a long vocabulary: 8-wave workgroups, unroll 2, rows
+        // split in a power of two of pieces while the grid stays within one
+        // workgroup per CU and each thread keeps at least 3 vectors.  GPU
+        // times with launches queued (one box; bf16 unless noted):
+        //   [1, 152064]   8 pieces 5.4 us   (unsplit, 16 waves 9.8 us)
+        //   [8, 152064]   8 pieces 5.9 us   (16 pieces 6.2, unsplit 10.0)
+        //   [32, 152064]  8 pieces 7.3 us   (4 pieces 7.5, unsplit 10.9)
+        //   [128, 152064] 2 pieces 10.9 us  (unsplit 11.5, 4 pieces 11.4)
+        //   [16, 128256] fp16: 8 pieces 6.8 us (unsplit 9.9)
+        //   [64, 262144] fp32: 4 pieces 13.8 us (unsplit 24.3, 8 pieces 14.5)
+        // Unsplit, rows of at least 16384 vectors also take 8 waves
+        // ([256, 152064]: 12.8 us vs 14.6 on 16 waves, unroll 4); shorter
+        // ones 16 waves, unroll 4 (C1, [256, 32000] fp32: 5.9 us vs 6.4).
+        int s = 1;
+        while (s < kMaxSplits && n_rows * 2 * s <= kFwdSplitGrid &&
+               nvec >= int64_t{3} * 8 * 64 * 2 * s)
+            s *= 2;
+        if (s > 1 || nvec >= 16384) {
+            c.waves = 8;
+            c.unroll = 2;
+            c.splits = s;
+        } else {
+            c.waves = 16;
+            c.unroll = 4;
+        }
     } else if (n_rows * w <= kFwdOneRoundWaves) {
         // All workgroups resident at once (C2: 1024 rows x 8 waves, 8 waves
         // per SIMD): unroll 2 keeps a wave at 61 VGPRs (unroll 4: ~100, 4
@@ -204,9 +221,16 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
     return c;
 }
 
+// Split-row workspace: the pieces' float4 states, then one 32-bit arrival
+// counter per row (rounded up to 16 bytes).
+size_t partials_bytes(int64_t n_rows, int splits) {
+    return static_cast<size_t>(n_rows) * static_cast<size_t>(splits) * 4 * sizeof(float);
+}
+
 size_t workspace_bytes_for(int64_t n_rows, int splits) {
     if (splits <= 1 || n_rows <= 0) return 0;
-    return static_cast<size_t>(n_rows) * static_cast<size_t>(splits) * 4 * sizeof(float);
+    const size_t counters = (static_cast<size_t>(n_rows) * sizeof(unsigned int) + 15) & ~size_t{15};
+    return partials_bytes(n_rows, splits) + counters;
 }
 
 // 1/temperature rounded once to fp32; rejects temperatures that are not
@@ -268,6 +292,10 @@ int fwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     p.lse = lse;
     p.splits = cfg.splits;
     p.partials = (cfg.splits > 1) ? static_cast<float*>(workspace) : nullptr;
+    p.counters = (cfg.splits > 1)
+                     ? reinterpret_cast<unsigned int*>(static_cast<unsigned char*>(workspace) +
+                                                       partials_bytes(n_rows, cfg.splits))
+                     : nullptr;
     p.scale = scale;
     p.target_offset = 0;
     p.state = nullptr;
@@ -459,6 +487,13 @@ int noalloc_scratch(void** out) {
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || p == nullptr)
             return fail(KLP_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(e));
+        // The split-row kernels need the scratch zero before their first
+        // launch (and leave it zero): one synchronous clear per device.
+        e = hipMemset(p, 0, KLP_FWD_NOALLOC_SCRATCH_BYTES);
+        if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+        if (e != hipSuccess)
+            return fail(KLP_ELAUNCH, "clearing the scratch failed on device %d: %s", dev,
                         hipGetErrorString(e));
         g_scratch_ptr[dev] = p;
     }

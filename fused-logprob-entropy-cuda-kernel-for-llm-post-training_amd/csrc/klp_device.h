@@ -134,6 +134,11 @@ __device__ __forceinline__ u32x4 load16(const u32x4* p) {
 // load (the "nt" bit on gfx950, which __builtin_nontemporal_load also sets).
 constexpr int kBufNonTemporal = 2;
 
+// s_waitcnt immediate (gfx9 encoding) that waits for vmcnt 0 only: vmcnt
+// bits [3:0] and [15:14] zero, expcnt [6:4] and lgkmcnt [11:8] at their
+// maxima (no wait).
+constexpr int kWaitVmcnt0 = 0x0F70;
+
 __device__ __forceinline__ float fmax_nan(float a, float b) {
     // NaN-propagating maximum (v_maximum3_f32 on gfx950): a NaN logit turns
     // the running max, and with it every output of its row, into NaN.

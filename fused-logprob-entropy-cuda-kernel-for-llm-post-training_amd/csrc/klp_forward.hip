@@ -21,8 +21,13 @@
 //    separate `logits.div_(temperature)` pass (reference trainer.py:101);
 //  - lanes merge as one flat reduction (maximum, one rescale per lane, sums;
 //    DPP within rows, v_permlane16/32_swap across them), the waves' states
-//    through LDS by the same reduction in wave 0, splits through a
-//    workspace in split order, so results do not depend on timing.
+//    through LDS by the same reduction in wave 0;
+//  - split rows merge in the same launch: each piece stores its state in the
+//    workspace and counts itself in the row's arrival counter (one
+//    acquire-release atomic); the piece that arrives last merges all of the
+//    row's states, lane k holding piece k, so the result does not depend on
+//    which piece came last, then writes the outputs and puts the row's
+//    workspace words back to zero for the next call.
 #include "klp_device.h"
 #include "klp_launch.h"
 
@@ -132,16 +137,6 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     const int64_t vocab = p.vocab;
     const elem* rp = static_cast<const elem*>(p.logits) + row_offset(p.rm, row);
 
-    // The target logit is read directly (the reference captures it inside the
-    // scan, csrc/fused_logprob.cu:180,185, leaving 0 for an out-of-range
-    // target).  Issued first so that its latency hides behind the scan.  In
-    // split mode the combine kernel reads it instead.
-    float x_target = 0.0f;
-    if (!kSplit && tid == 0) {
-        const int64_t tgt = p.targets[row] - p.target_offset;
-        if (tgt >= 0 && tgt < vocab) x_target = to_f32<DT>(rp[tgt]) * p.scale;
-    }
-
     const uintptr_t addr = reinterpret_cast<uintptr_t>(rp);
     int64_t head = static_cast<int64_t>(((16u - (addr & 15u)) & 15u) / ESZ);
     if (head > vocab) head = vocab;
@@ -149,13 +144,32 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     const int64_t tail_begin = head + nvec * EPV;
     const u32x4* vp = reinterpret_cast<const u32x4*>(rp + head);
 
-    int64_t vb = 0, ve = nvec;
+    int64_t vb = 0, ve = nvec, per = nvec;
     if (kSplit) {
-        const int64_t per = (nvec + p.splits - 1) / p.splits;
+        per = (nvec + p.splits - 1) / p.splits;
         vb = static_cast<int64_t>(split) * per;
         ve = vb + per;
         if (vb > nvec) vb = nvec;
         if (ve > nvec) ve = nvec;
+    }
+
+    // The target logit is read directly (the reference captures it inside the
+    // scan, csrc/fused_logprob.cu:180,185, leaving 0 for an out-of-range
+    // target).  Issued before the scan so that its latency hides behind it.
+    // With split rows the piece that scans the target's element reads it
+    // (split 0 owns the scalar head and tail).
+    float x_target = 0.0f;
+    if (tid == 0) {
+        const int64_t tgt = p.targets[row] - p.target_offset;
+        if (tgt >= 0 && tgt < vocab) {
+            bool mine = true;
+            if (kSplit) {
+                const int64_t owner =
+                    (tgt < head || tgt >= tail_begin) ? 0 : ((tgt - head) / EPV) / per;
+                mine = (owner == split);
+            }
+            if (mine) x_target = to_f32<DT>(rp[tgt]) * p.scale;
+        }
     }
 
     Stat s = stat_empty();
@@ -180,15 +194,60 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     if (wave != 0) return;
     static_assert(WAVES <= 16, "one DPP row of states");
     const Stat r = row_reduce_flat(lane < WAVES ? wave_stat[lane] : stat_empty());
-    if (lane != 0) return;  // thread 0 (it read the target logit)
 
-    if (kSplit) {
-        // Partial state of this piece; klp_fwd_combine_kernel merges the
-        // pieces of each row in split order after this kernel completes.
-        float4* slot = reinterpret_cast<float4*>(p.partials) + b;
-        *slot = make_float4(r.m, r.z, r.t, 0.0f);
+    if constexpr (kSplit) {
+        // This piece's state (x_target is 0 except in the piece that read
+        // the target logit), then its arrival.  The state's words are
+        // device-scope atomic stores, which write through to the device's
+        // coherence point; waiting for them (vmcnt 0) before the increment
+        // orders them before the count without the L2 write-back a release
+        // fence costs (which, once per workgroup, made grids of a few hundred
+        // pieces several times slower).  The piece that counts last acquires
+        // (one fence) before it reads the others.
+        float4* part = reinterpret_cast<float4*>(p.partials) + row * p.splits;
+        unsigned int* counter = p.counters + row;
+        unsigned int arrived = 0;
+        if (lane == 0) {
+            float* slot = reinterpret_cast<float*>(part + split);
+            __hip_atomic_store(slot + 0, r.m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(slot + 1, r.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(slot + 2, r.t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(slot + 3, x_target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+        arrived = __shfl(arrived, 0);
+        if (arrived != static_cast<unsigned int>(p.splits - 1)) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        // Last piece of the row: lane k merges pieces k, k + 64, ... in
+        // order, the lanes as one flat reduction; the target logit is the
+        // sum of the pieces' x_target, all zero but the reader's.
+        Stat acc = stat_empty();
+        float xt = 0.0f;
+        for (int k = lane; k < p.splits; k += 64) {
+            const float4 q = part[k];
+            acc = combine(acc, Stat{q.x, q.y, q.z});
+            xt += q.w;
+            float* slot = reinterpret_cast<float*>(part + k);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                __hip_atomic_store(slot + j, 0.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const Stat m = wave_reduce_flat(acc);
+        xt = xrow_sum(row_sum16(xt));
+        if (lane != 0) return;
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const RowOut o = finalize(m, xt);
+        p.logprob[row] = o.logp;
+        p.entropy[row] = o.ent;
+        p.lse[row] = o.lse;
         return;
     }
+    if (lane != 0) return;  // thread 0 (it read the target logit)
+
     if (p.state) {
         // One vocabulary shard: the row's state, merged across shards by
         // klp_fwd_shard_merge_kernel.
@@ -216,29 +275,6 @@ __global__ __launch_bounds__(256) void klp_fwd_shard_merge_kernel(ShardMergePara
     const int64_t tgt = p.targets[row];
     float x_target = 0.0f;
     if (tgt >= 0 && tgt < p.vocab) x_target = st[(tgt / p.shard_vocab) * p.n_rows + row].w;
-    const RowOut o = finalize(acc, x_target);
-    p.logprob[row] = o.logp;
-    p.entropy[row] = o.ent;
-    p.lse[row] = o.lse;
-}
-
-// Split-row second pass: one thread per row merges the row's `splits`
-// partial states in split order (a fixed order, so results do not depend on
-// which workgroup finished first) and writes the outputs.
-template <int DT>
-__global__ __launch_bounds__(256) void klp_fwd_combine_kernel(FwdParams p) {
-    typedef typename Traits<DT>::elem elem;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (row >= p.n_rows) return;
-    const elem* rp = static_cast<const elem*>(p.logits) + row_offset(p.rm, row);
-    const int64_t tgt = p.targets[row];
-    const float x_target = (tgt >= 0 && tgt < p.vocab) ? to_f32<DT>(rp[tgt]) * p.scale : 0.0f;
-    const float4* part = reinterpret_cast<const float4*>(p.partials) + row * p.splits;
-    Stat acc = stat_empty();
-    for (int k = 0; k < p.splits; ++k) {
-        const float4 q = part[k];
-        acc = combine(acc, Stat{q.x, q.y, q.z});
-    }
     const RowOut o = finalize(acc, x_target);
     p.logprob[row] = o.logp;
     p.entropy[row] = o.ent;
@@ -287,12 +323,9 @@ static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
     if (p.splits == 1)
         return launch_kernel(klp_fwd_kernel<DT, WAVES, U, false, kScaled>,
                              dim3(static_cast<unsigned>(p.n_rows)), dim3(WAVES * 64), stream, p);
-    hipError_t e = launch_kernel(klp_fwd_kernel<DT, WAVES, U, true, kScaled>,
-                                 dim3(static_cast<unsigned>(p.n_rows * p.splits)),
-                                 dim3(WAVES * 64), stream, p);
-    if (e != hipSuccess) return e;
-    return launch_kernel(klp_fwd_combine_kernel<DT>,
-                         dim3(static_cast<unsigned>((p.n_rows + 255) / 256)), dim3(256), stream, p);
+    return launch_kernel(klp_fwd_kernel<DT, WAVES, U, true, kScaled>,
+                         dim3(static_cast<unsigned>(p.n_rows * p.splits)), dim3(WAVES * 64),
+                         stream, p);
 }
 
 template <int DT>

@@ -23,7 +23,11 @@ struct FwdParams {
     float* logprob;
     float* entropy;
     float* lse;
-    float* partials;  // [n_rows * splits] float4 (m, z, t, unused) when splits > 1
+    // Split rows (splits > 1): [n_rows * splits] float4 (m, z, t, target
+    // logit or 0) piece states and [n_rows] arrival counters, all zero
+    // before the launch and left zero by it.
+    float* partials;
+    unsigned int* counters;
     int splits;
     float scale;      // 1 / temperature; logits are multiplied by it on load
     // Vocabulary shards (splits == 1 only): the row holds columns

@@ -100,13 +100,16 @@ _WS_KEEP = 16
 def _workspace(device_index: int, stream: int, nbytes: int):
     """The workspace of (device, raw stream handle) holding at least
     ``nbytes``; the device must be current and ``stream`` its current
-    stream.  Under graph capture every call gets a workspace of its own, kept
-    for the life of the process: graphs captured on one stream would
-    otherwise share one and race when replayed concurrently."""
+    stream.  Workspaces start zero-filled (by a fill kernel, not a memset),
+    as the split-row forward needs; it leaves them zero.  Under graph
+    capture every call gets a workspace of its own, kept for the life of the
+    process: graphs captured on one stream would otherwise share one and race
+    when replayed concurrently."""
     if nbytes == 0:
         return None
     if capturing():
-        return keep_for_capture(torch.empty(nbytes, dtype=torch.uint8, device=device_index))
+        return keep_for_capture(
+            torch.empty(nbytes, dtype=torch.uint8, device=device_index).zero_())
     key = (device_index, stream)
     with _ws_lock:
         buf = _workspaces.get(key)
@@ -114,7 +117,7 @@ def _workspace(device_index: int, stream: int, nbytes: int):
             # Allocated on the stream that uses it (the caching allocator then
             # reuses it only in that stream's order).
             with torch.cuda.stream(torch.cuda.current_stream(device_index)):
-                buf = torch.empty(nbytes, dtype=torch.uint8, device=device_index)
+                buf = torch.empty(nbytes, dtype=torch.uint8, device=device_index).zero_()
             _workspaces[key] = buf
         _workspaces.move_to_end(key)
         while len(_workspaces) > _WS_KEEP:

@@ -68,11 +68,16 @@ size_t klp_last_error(char* buf, size_t len);
 /*
  * Bytes of device workspace that klp_fwd can use to split each row across
  * several workgroups (split-row mode) for this problem size; 0 means the
- * dispatcher keeps one workgroup per row.  In split-row mode klp_fwd enqueues
- * two kernels: the first writes one partial (max, sum-exp, sum-x-exp) state
- * per row piece into the workspace, the second merges each row's pieces in a
- * fixed order.  The workspace needs no initialisation; launches that share
- * one workspace must be ordered (same stream, or synchronised).
+ * dispatcher keeps one workgroup per row.  In split-row mode each row piece
+ * writes its partial (max, sum-exp, sum-x-exp) state into the workspace and
+ * counts itself in its row's arrival counter there; the piece that arrives
+ * last merges the row's states in a fixed order (one kernel in all).
+ *
+ * The workspace must be zero-filled before its first use (with a fill
+ * kernel, or hipMemset outside any graph capture); every call leaves it
+ * zero-filled again, whatever the shapes of the calls that share it.
+ * Launches that share one workspace must be ordered (same stream, or
+ * synchronised): overlapping ones race on the counters.
  */
 size_t klp_fwd_workspace_bytes(int dtype, int64_t n_rows, int64_t vocab);
 
@@ -84,7 +89,8 @@ size_t klp_fwd_workspace_bytes(int dtype, int64_t n_rows, int64_t vocab);
  * (reference csrc/fused_logprob.cu:355-403, bound at csrc/bindings.cpp:21-23).
  *
  * `workspace` may be NULL (then one workgroup per row).  When it is not
- * NULL it must hold klp_fwd_workspace_bytes() bytes and be 16-byte aligned.
+ * NULL it must hold klp_fwd_workspace_bytes() bytes, be 16-byte aligned
+ * and be zero-filled (see klp_fwd_workspace_bytes).
  */
 int klp_fwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
             int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
@@ -160,14 +166,17 @@ int klp_bwd_temp(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
  * allocation).  No counterpart in the reference.
  *
  * When the default launch shape splits rows (few rows of a long vocabulary),
- * the split-row partial states go to a scratch array of
- * KLP_FWD_NOALLOC_SCRATCH_BYTES that the library keeps on each GPU it runs
- * on until the process ends; a problem whose partial states would not fit is
- * rejected with KLP_EWORKSPACE (the current dispatcher needs at most 8 KiB:
- * it splits only while rows x pieces < 512).  The array needs no clearing:
- * every launch writes each state before reading it.  All calls on one GPU
- * share that GPU's array, so calls that overlap on one GPU (on other
- * streams, from other threads) race and must be ordered by the caller.
+ * the split-row workspace (piece states and row arrival counters) is a
+ * scratch array of KLP_FWD_NOALLOC_SCRATCH_BYTES that the library keeps on
+ * each GPU it runs on until the process ends; a problem whose workspace
+ * would not fit is rejected with KLP_EWORKSPACE (the current dispatcher needs
+ * at most 5 KiB: it splits only while rows x pieces <= 256).  The first call
+ * on a device clears the array once (a synchronous hipMemset, so that first
+ * call must not be made while a stream of that device is being captured);
+ * every call leaves it zero-filled.  All calls on one GPU share that GPU's
+ * array, so calls that overlap on one GPU (on other streams, from other
+ * threads) race and must be ordered by the caller: overlapping calls can
+ * also leave the array's counters non-zero, which breaks later calls.
  * Arguments and results as klp_fwd.
  */
 #define KLP_FWD_NOALLOC_SCRATCH_BYTES 65536

@@ -30,7 +30,8 @@ extern "C" {
 /* Workspace bytes klp_fwd_ex needs for `splits` workgroups per row. */
 size_t klp_fwd_workspace_bytes_ex(int64_t n_rows, int splits);
 
-/* klp_fwd with an explicit launch shape.  splits > 1 needs a workspace. */
+/* klp_fwd with an explicit launch shape.  splits > 1 needs a zero-filled
+ * workspace (see klp_fwd_workspace_bytes). */
 int klp_fwd_ex(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
                const int64_t* targets,

@@ -76,7 +76,10 @@ def test_validation_errors():
 def test_workspace_and_launch_shape_errors():
     from kernel_opt._library import KLP_EINVAL, KLP_EWORKSPACE, lib
     need = lib.klp_fwd_workspace_bytes_ex(4, 8)
-    assert need == 4 * 8 * 16  # one float4 partial state per (row, split)
+    # one float4 state per (row, split), then a 32-bit arrival counter per
+    # row rounded up to 16 bytes
+    assert need == 4 * 8 * 16 + 16
+    assert lib.klp_fwd_workspace_bytes_ex(5, 2) == 5 * 2 * 16 + 32
     assert lib.klp_fwd_workspace_bytes_ex(4, 1) == 0
     rc = lib.klp_fwd_ex(P, 0, 4, 100, 4, 0, 100, P, P, P, P, P, need - 16, 8, 4, 8, 0, None)
     assert rc == KLP_EWORKSPACE and "workspace" in _err()
@@ -135,15 +138,21 @@ def test_default_launch_shapes():
     assert _C.default_config("fwd", torch.bfloat16, 32768, 18992) == (4, 2, 1, 0)
     # 256 rows: wider workgroups instead of splitting
     assert _C.default_config("fwd", torch.float32, 256, 32000)[::2] == (16, 1)
-    # few rows, long vocab: split rows (two-kernel mode, needs a workspace)
+    # few rows, long vocab: split rows (needs a workspace), about one
+    # workgroup per CU, at least 3 vectors per thread
     w, u, s, f = _C.default_config("fwd", torch.bfloat16, 16, 152064)
-    assert w == 16 and s >= 2
+    assert (w, u, s) == (8, 2, 8)
+    assert _C.default_config("fwd", torch.bfloat16, 1, 152064)[:3] == (8, 2, 8)
+    assert _C.default_config("fwd", torch.bfloat16, 128, 152064)[:3] == (8, 2, 2)
+    assert _C.default_config("fwd", torch.float32, 64, 262144)[:3] == (8, 2, 4)
+    # few rows that are not split: long ones on 8 waves, short ones on 16
+    assert _C.default_config("fwd", torch.bfloat16, 256, 152064)[:3] == (8, 2, 1)
     # tiny vocab: never split
     assert _C.default_config("fwd", torch.float32, 4, 64)[2] == 1
     from kernel_opt._library import lib
     assert lib.klp_fwd_workspace_bytes(0, 32768, 151936) == 0
     assert lib.klp_fwd_workspace_bytes(0, 1024, 152064) == 0
-    assert lib.klp_fwd_workspace_bytes(0, 16, 152064) == 16 * s * 16
+    assert lib.klp_fwd_workspace_bytes(0, 16, 152064) == 16 * s * 16 + 64
     # backward splits rows freely (no second pass)
     assert _C.default_config("bwd", torch.bfloat16, 1024, 152064)[2] >= 2
 
