@@ -62,6 +62,7 @@ import json
 import math
 import os
 import re
+import statistics
 import sys
 import time
 
@@ -665,7 +666,6 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5, rounds=5):
     gradients on logprob and entropy; medians over interleaved rounds of K
     calls; peak memory beyond the inputs (and, for the backward, beyond the
     new gradients)."""
-    import statistics
     from kernel_opt import (fused_linear_logprob_entropy, fused_linear_logprob_entropy_forward,
                             fused_logprob_entropy, fused_logprob_entropy_forward)
     g = torch.Generator(device=dev).manual_seed(3584)
@@ -1160,6 +1160,46 @@ def c1_leg(dev, K, timer, with_cpu):
     return out
 
 
+def small_batch_leg(dev, timer):
+    """Split-row mode where it is meant to pay: few rows of Qwen2.5-7B's
+    vocabulary (bf16 [n, 152064], n = 1, 8, 32), forward GPU time per launch
+    (queued), with the dispatcher's shape (rows split), the same rows unsplit
+    (8 waves, unroll 2; and 16 waves, unroll 4, the unsplit dispatcher's
+    choice before split rows were merged in one launch), and a plain read of
+    the same bytes (klp_ceiling_read at the split shape)."""
+    from kernel_opt import _C
+    from kernel_opt._library import check_status, lib
+    V = 152064
+    g = torch.Generator(device=dev).manual_seed(152)
+    rows = []
+    for n in (1, 8, 32):
+        x = (torch.randn(n, V, device=dev, generator=g) * 2.0).to(torch.bfloat16)
+        t = torch.randint(0, V, (n,), device=dev, generator=g)
+        o = [torch.empty(n, device=dev) for _ in range(3)]
+        cfg = _C.default_config("fwd", x.dtype, n, V)
+        sink = torch.zeros(n * cfg[2], dtype=torch.int32, device=dev)
+        st = timer.stream.cuda_stream
+
+        def run(c=None):
+            _C.fwd_launch(x, t, *o, config=c)
+
+        def read():
+            check_status(lib.klp_ceiling_read(x.data_ptr(), n, V * 2, cfg[0], cfg[1], cfg[2],
+                                              sink.data_ptr(), 0x9E3779B9, st))
+
+        res = {}
+        for key, fn in (("fwd_us", run), ("unsplit_8w_us", lambda: run((8, 2, 1, 0))),
+                        ("unsplit_16w_us", lambda: run((16, 4, 1, 0))), ("read_us", read)):
+            fn()
+            res[key] = round(statistics.median(timer.b2b(fn) for _ in range(3)) * 1e3, 2)
+        rows.append({"rows": n, "launch": dict(zip(("waves", "unroll", "splits"), cfg[:3])),
+                     **res})
+    return {"shape": "bf16 [rows, 152064]", "runs": rows,
+            "note": "GPU time per launch, launches queued behind a spin kernel; a launch this "
+                    "small is latency (dispatch, then dependent memory round trips): the read "
+                    "of the same bytes bounds it from below"}
+
+
 def sweep(name, dev, K, timer, out_md):
     """Launch-shape sweep of the forward and backward at workload `name`,
     back to back and flushed, written as a markdown table."""
@@ -1297,6 +1337,7 @@ def main(argv=None):
     autograd = (autograd_timing(dev, K, logits, targets, core["g_logp"], core["g_ent"])
                 if extra else None)
     c1 = c1_leg(dev, K, timer, not args.no_cpu_baseline) if extra and name != "C1" else None
+    small = small_batch_leg(dev, timer) if extra else None
 
     cpu = None
     if extra and not args.no_cpu_baseline:
@@ -1408,6 +1449,7 @@ def main(argv=None):
         },
         "autograd": autograd,
         "C1": c1,
+        "small_batch": small,
         "cpu_baseline": cpu,
         "grpo_loss": grpo,
         "grpo_step": step,
