@@ -141,9 +141,10 @@ struct StepShared {
     int64_t next_row;   // persistent kernel: the workgroup's next row
 };
 
-// The row's results: the wave reduction, the 16 wave states through LDS,
-// merged by wave 0 (each of its 16-lane DPP rows reads all of them and
-// reduces them, every lane ending with the same bits), which computes the
+// The row's results: the wave reduction (flat: one maximum, one rescale per
+// lane, two sums), the 16 wave states through LDS, merged by wave 0 (each of
+// its 16-lane DPP rows reads all of them and reduces them the same way, every
+// lane ending with the same bits), which computes the
 // row's results and the token's GRPO terms, writes them, and hands the
 // backward's constants to the other waves through LDS.  Both barriers are
 // here; `s` is this thread's state.  With kPublishNext, thread 0 also
@@ -158,13 +159,13 @@ __device__ __forceinline__ RowGrad row_results(const GrpoStepParams& p, int64_t 
     // Uniform in the wave: an SGPR (as a VGPR it is one more register live
     // across the persistent kernel's loop).
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    s = wave_reduce(s);
+    s = wave_reduce_flat(s);
     if (lane == 0) sh.wave_stat[wave] = s;
     __syncthreads();
     static_assert(kStepWaves == 16, "one wave state per lane of a DPP row");
     if (wave == 0) {
         const RowOut o =
-            finalize(row_reduce(sh.wave_stat[lane & 15]), has_t ? sh.target_logit : 0.0f);
+            finalize(row_reduce_flat(sh.wave_stat[lane & 15]), has_t ? sh.target_logit : 0.0f);
         // GRPO terms of this token (token-level importance weight).
         const TokenLoss tl = grpo_token_loss(eps_low, eps_high, beta, o.logp - in.old_lp,
                                              in.adv, o.logp, in.ref_lp, has_ref);
