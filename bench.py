@@ -362,12 +362,14 @@ def _phase(prev: str | None, name: str) -> str:
     return "other"
 
 
-def summarize_trace(trace_dir: str, config: str, command: str = ""):
+def summarize_trace(trace_dir: str, config: str, command: str = "", label: str | None = None):
     """Average kernel durations of the klp kernels from a rocprofv3
     --kernel-trace run, overall and per phase of bench.py (a launch right
     after the 1 GiB flush read: "flushed"; after a launch of the same kernel:
     "back to back"; after the other klp kernel: the interleaved step).
-    Returns (markdown, data)."""
+    `label` (default: the config) tags the summary; the bench line's
+    trace_check reads the summaries tagged with the bare config name, i.e.
+    those of a `--core-only` run.  Returns (markdown, data)."""
     rows = _rocprof_csv(trace_dir, "kernel_trace.csv")
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     stats = {}
@@ -384,7 +386,9 @@ def summarize_trace(trace_dir: str, config: str, command: str = ""):
     kernels = {}
     lines = []
     for k in sorted(stats):
-        alg = kernel_bytes(k, config)
+        # A labelled run launches kernels at several shapes (other configs'
+        # legs, small batches): no bytes per launch to divide by.
+        alg = None if label else kernel_bytes(k, config)
         kernels[k] = {}
         for ph in ("all", "back to back", "flushed", "after another klp kernel", "other"):
             ds = stats[k].get(ph)
@@ -400,16 +404,21 @@ def summarize_trace(trace_dir: str, config: str, command: str = ""):
                          f"{min(ds) / 1e3:.2f} | {max(ds) / 1e3:.2f} | "
                          f"{'-' if tb is None else f'{tb:.3f} ({100 * tb / HBM_PEAK_TBPS:.1f}%)'} |")
     bid = build_id()
-    data = {"kind": "trace", "config": config, "build_id": bid, "git_head": _git_head(),
+    tag = label or config
+    data = {"kind": "trace", "config": tag, "build_id": bid, "git_head": _git_head(),
             "kernels": kernels}
-    md = [f"# rocprofv3 kernel trace: klp kernels, workload {config}", "",
+    md = [f"# rocprofv3 kernel trace: klp kernels, workload {tag}", "",
           f"Build id `{bid}` (hash of the library sources, as `bench.py` computes it); "
           f"summarised at git `{data['git_head']}` by `python bench.py --trace-from "
-          f"{trace_dir} --config {config}`.", ""]
+          f"{trace_dir} --config {config}" + (f" --label {label}" if label else "") + "`.",
+          ""]
     if command:
         md += ["Command (MI355X):", "```", command, "```", ""]
-    md += ["TB/s = algorithmic bytes per launch / average duration (forward "
-           "N*V*s + 20N, backward 2*N*V*s + 24N, calibration kernels their buffer bytes).", "",
+    md += [("TB/s: not given; this run launches kernels at several shapes (its other "
+            "legs), so a kernel's launches are not all of the config's size." if label else
+            "TB/s = algorithmic bytes per launch / average duration (forward "
+            "N*V*s + 20N, backward 2*N*V*s + 24N, calibration kernels their buffer bytes)."),
+           "",
            "| kernel | phase | launches | avg us | median us | min us | max us | TB/s (% of 8) |",
            "|---|---|---:|---:|---:|---:|---:|---:|"]
     md += lines + ["", _profile_line(data), ""]
@@ -1297,10 +1306,13 @@ def main(argv=None):
     ap.add_argument("--command", default="",
                     help="the profiling command, quoted in the --trace-from / --traffic-from "
                          "summary")
+    ap.add_argument("--label", default=None,
+                    help="tag of a --trace-from summary other than the config name (a run "
+                         "that is not --core-only)")
     args = ap.parse_args(argv)
 
     if args.trace_from:
-        md, _ = summarize_trace(args.trace_from, args.config, args.command)
+        md, _ = summarize_trace(args.trace_from, args.config, args.command, args.label)
         print(md)
         return 0
     if args.traffic_from:
