@@ -485,6 +485,81 @@ def test_workspace_reuse_across_shapes(oracle):
         _check_fwd(oracle, x_cpu, t_cpu, outs, 2e-5, label=f"N={N} splits={s}")
 
 
+# ---------------------------------------------------------------------------
+# Split rows merged in one launch (the last piece of a row merges the pieces)
+# ---------------------------------------------------------------------------
+def _piece_edges(V, dtype, offset, splits):
+    """Element indices at the edges of each piece of a row that starts
+    `offset` elements past a 16-byte boundary (the kernel's split: scalar
+    head and tail elements, then the 16-byte vectors in `splits` pieces)."""
+    epv = 16 // torch.tensor([], dtype=dtype).element_size()
+    head = min((-offset) % epv, V)
+    nvec = (V - head) // epv
+    tail = head + nvec * epv
+    per = -(-nvec // splits)
+    idx = set(range(head)) | set(range(tail, V))
+    for k in range(splits):
+        v0, v1 = min(k * per, nvec), min((k + 1) * per, nvec)
+        if v1 > v0:
+            idx |= {head + v0 * epv, head + v0 * epv + 1, head + v1 * epv - 1,
+                    head + v1 * epv - 2}
+    return sorted(i for i in idx if 0 <= i < V)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("splits", [2, 8, 64, 256])
+def test_split_rows_targets_at_piece_edges(dtype, splits, oracle):
+    """Every row's target on a piece edge, a scalar head or tail element, or
+    out of range: the piece that scans the target reads it, the last piece to
+    arrive merges; results against the oracle, rows that start off a 16-byte
+    boundary included.  256 pieces exceed a wave: lanes merge several."""
+    from kernel_opt import _C
+    V, offset = 65541, 1
+    edges = _piece_edges(V, dtype, offset, splits)
+    targets = edges + [-1, V, V + 7]
+    N = len(targets)
+    x_cpu = seeded_logits((N, V), dtype, seed=700 + splits)
+    buf = torch.empty(N * V + offset, dtype=dtype, device=DEV)
+    x = buf[offset:].view(N, V)
+    x.copy_(x_cpu.to(DEV))
+    t_cpu = torch.tensor(targets, dtype=torch.int64)
+    outs = [torch.full((N,), float("nan"), device=DEV) for _ in range(3)]
+    _C.fwd_launch(x, t_cpu.to(DEV), *outs, config=(4, 2, splits, 0))
+    _check_fwd(oracle, x_cpu, t_cpu, outs, FWD_TOL[dtype], label=f"splits={splits}")
+    # same bits as a second call (the merge does not depend on arrival order)
+    again = [torch.empty(N, device=DEV) for _ in range(3)]
+    _C.fwd_launch(x, t_cpu.to(DEV), *again, config=(4, 2, splits, 0))
+    assert all(torch.equal(a, b) for a, b in zip(outs, again))
+
+
+def test_split_workspace_left_zero():
+    """Through the C ABI with a caller workspace: zero-filled before the first
+    call, zero-filled after each call, whatever the shapes of the calls that
+    share it; the results match the unsplit launch to fp32 merge noise."""
+    import ctypes
+    from kernel_opt import _C
+    from kernel_opt._library import DTYPE_CODES, check_status, lib
+    ws_bytes = lib.klp_fwd_workspace_bytes_ex(64, 64)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    for i, (N, V, splits) in enumerate([(64, 30011, 8), (3, 152064, 64), (40, 9001, 2),
+                                        (64, 70000, 64)]):
+        x = seeded_logits((N, V), torch.bfloat16, seed=800 + i, device=DEV)
+        t = seeded_targets((N,), V, seed=800 + i, device=DEV)
+        outs = [torch.empty(N, device=DEV) for _ in range(3)]
+        need = lib.klp_fwd_workspace_bytes_ex(N, splits)
+        assert 0 < need <= ws_bytes
+        check_status(lib.klp_fwd_ex(x.data_ptr(), DTYPE_CODES[x.dtype], N, V, *_C.row_layout(x),
+                                    t.data_ptr(), *(o.data_ptr() for o in outs), ws.data_ptr(),
+                                    ws_bytes, 8, 2, splits, 0, st))
+        torch.cuda.synchronize()
+        assert int(ws.count_nonzero()) == 0, f"call {i}: workspace not left zero"
+        ref = [torch.empty(N, device=DEV) for _ in range(3)]
+        _C.fwd_launch(x, t, *ref, config=(8, 2, 1, 0))
+        for a, b in zip(outs, ref):
+            assert (a - b).abs().max().item() <= 4e-6 * max(1.0, b.abs().max().item())
+
+
 def test_multiple_streams(oracle):
     """Launches on two streams use separate workspaces."""
     from kernel_opt import _C
