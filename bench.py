@@ -879,7 +879,7 @@ class Timer:
         else:
             self.buf.fill_(k & 0xFF)
 
-    FLUSH_ROUNDS = 5
+    FLUSH_ROUNDS = 9
 
     def flushed(self, body):
         """(ms per launch, ms per launch timed on its own) of `body` right
@@ -1232,9 +1232,11 @@ def sweep(name, dev, K, timer, out_md):
         torch.cuda.synchronize()
     lines = [f"# Launch-shape sweep, workload {name} (build `{build_id()}`)", "",
              f"`python bench.py --config {name} --sweep OUT.md --steps {K}`: each shape timed "
-             f"over {n} back-to-back launches (one event pair) and {n} launches each after a "
-             "1 GiB read (one event pair around the (read, launch) pairs minus one around "
-             "the reads alone). Defaults marked *.", "",
+             f"over {n} back-to-back launches queued behind a spin kernel (one event pair), "
+             "and right after a 1 GiB read (the median over 9 rounds of one event pair "
+             "around K / 9 (read, launch) pairs minus one around as many reads alone, per "
+             "launch). "
+             "Defaults marked *.", "",
              "| kernel | waves | unroll | splits | b2b us | b2b % of 8 TB/s | flushed us | "
              "flushed % |", "|---|---:|---:|---:|---:|---:|---:|---:|"]
     _C.fwd_launch(x, t, lp, ent, lse)

@@ -61,6 +61,7 @@ constexpr int64_t kFwdSplitGrid = 256;
 // one round of workgroups.
 constexpr int64_t kFwdOneRoundWaves = 8192;
 constexpr int64_t kBwdLargeGrid = 65536;
+constexpr int64_t kBwdSmallGrid = 16384;
 constexpr int kMaxSplits = 64;
 
 // Shared checks of the row-addressed logits operand.
@@ -213,6 +214,16 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
         int64_t e = (nvec + tile - 1) / tile;
         if (e > kMaxSplits) e = kMaxSplits;
         if (e >= 1 && nvec / e >= tile - tile / 8) s = e;
+    }
+    // Small grids (up to kBwdSmallGrid workgroups of 16 waves: C1, C2):
+    // 8-wave workgroups over twice the pieces, each the same fraction of
+    // its iteration.  C2 [1024, 152064] bf16: 101.7 us against 104.5-105.2
+    // back to back, 101.4-101.9 against 102.1-103.0 flushed (two boxes); C1
+    // equal back to back, 14.4-14.8 against 15.4-15.7 flushed.  Larger grids
+    // keep 16 waves (C3 666 against 662 us, C4 3251 against 3131 us).
+    if (c.waves == 16 && n_rows * s <= kBwdSmallGrid && 2 * s <= kMaxSplits) {
+        c.waves = 8;
+        s *= 2;
     }
     // Rows of more than 2 GiB per 64 pieces (never a real vocabulary) take
     // more pieces.
