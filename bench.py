@@ -1085,6 +1085,21 @@ def autograd_timing(dev, K, logits, targets, g_logp, g_ent):
     torch.cuda.synchronize()
     fwd_t = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
 
+    def queued(call):
+        """GPU time of one call: a spin kernel first, so that the host has
+        issued the call's kernels before the first event's turn comes."""
+        torch.cuda.synchronize()
+        torch.cuda._sleep(Timer.QUEUE_SPIN_CYCLES)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        call()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b)
+
+    fwd_q = sorted(queued(lambda: fused_logprob_entropy(x, targets)) for _ in range(K))
+
     # backward: allocation of one call, then timing over K calls
     lp, ent, _ = fused_logprob_entropy(x, targets)
     loss = loss_of(lp, ent)
@@ -1110,17 +1125,28 @@ def autograd_timing(dev, K, logits, targets, g_logp, g_ent):
         torch.cuda.synchronize()
         bts.append(a.elapsed_time(b))
     bts.sort()
+    bq = []
+    for i in range(K):
+        lp, ent, _ = fused_logprob_entropy(x, targets)
+        loss = loss_of(lp, ent)
+        bq.append(queued(loss.backward))
+        x.grad = None
+    bq.sort()
     return {
         "fwd_ms_median": round(fwd_t[len(fwd_t) // 2], 5),
         "bwd_ms_median": round(bts[len(bts) // 2], 5),
+        "fwd_ms_median_queued": round(fwd_q[len(fwd_q) // 2], 5),
+        "bwd_ms_median_queued": round(bq[len(bq) // 2], 5),
         "fwd_peak_bytes": fwd_peak, "fwd_output_bytes": out_bytes,
         "fwd_transient_bytes": fwd_peak - fwd_held,
         "bwd_peak_bytes": bwd_peak, "bwd_grad_bytes": grad_bytes,
         "bwd_held_bytes": bwd_held,
         "bwd_transient_bytes": bwd_peak - bwd_held,
         "note": "kernel_opt.fused_logprob_entropy and loss.backward() from Python, events per "
-                "call (median of K); loss = sum(logp*g_logp + entropy*g_ent); peak = max "
-                "allocated during one call minus allocated before it",
+                "call (median of K); loss = sum(logp*g_logp + entropy*g_ent); *_queued: the "
+                "same calls behind a spin kernel, i.e. their GPU time without the host's "
+                "latency (autograd's engine, the loss's own backward ops, the launch); peak "
+                "= max allocated during one call minus allocated before it",
     }
 
 
