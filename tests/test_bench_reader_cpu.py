@@ -137,3 +137,22 @@ def test_short_kernel_names():
     assert bench.short_kernel(BWD) == "klp_bwd_kernel<0, 16, 2, true, false>"
     assert bench.short_kernel("void klp::klp_fwd_shard_merge_kernel(klp::ShardMergeParams)") == \
         "klp_fwd_shard_merge_kernel"
+
+
+def test_labelled_trace_is_not_the_configs(tmp_path, monkeypatch):
+    """A run that mixes shapes (--label): tagged with the label, so the bench
+    line's trace_check does not read it as the config's, and without TB/s."""
+    d = tmp_path / "trace"
+    _write(str(d / "run_kernel_trace.csv"), TRACE_COLS,
+           [{"Kind": "KERNEL_DISPATCH", "Kernel_Name": BWD, "Start_Timestamp": 0,
+             "End_Timestamp": 100000}])
+    md, data = bench.summarize_trace(str(d), "C2", label="C2-grpo-run")
+    assert data["config"] == "C2-grpo-run"
+    assert data["kernels"]["klp_bwd_kernel<0, 16, 2, true, false>"]["all"]["tbps"] is None
+    assert "--label C2-grpo-run" in md
+    prof = tmp_path / "profiles"
+    prof.mkdir()
+    (prof / "klp_C2_grpo_trace.md").write_text(md)
+    monkeypatch.setattr(bench, "PROFILES_DIR", str(prof))
+    assert bench.load_profiles("trace", "C2", bench.build_id()) == []
+    assert len(bench.load_profiles("trace", "C2-grpo-run", bench.build_id())) == 1
