@@ -774,7 +774,11 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5, rounds=5):
         def run(chunk):
             hh.grad = None
             w.grad = None
-            if chunk:
+            if chunk == "head":
+                # the vocabulary-chunked LM head, then the GRPO loss (autograd)
+                lp, _, _ = fused_linear_logprob_entropy(hh, w, tt)
+                loss, _ = fused_grpo_loss(lp, old, adv, mask, **kw)
+            elif chunk:
                 loss, _, _ = fused_linear_grpo_step(
                     hh, w, tt, old, adv, mask,
                     chunk_tokens=None if chunk == "default" else chunk, **kw)
@@ -797,8 +801,9 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5, rounds=5):
             return round((torch.cuda.max_memory_allocated() - base) / 2 ** 20, 1)
 
         out = {"tokens": n_tok}
-        for chunk in [0] + chunks:
-            name = f"chunked_{chunk}" if chunk else "unfused"
+        for chunk in [0] + chunks + ["head"]:
+            name = ("vocab_chunked_head" if chunk == "head" else f"chunked_{chunk}" if chunk
+                    else "unfused")
             run(chunk)
             run(chunk)
             out[name + "_fwd_bwd_ms"] = round(timed(lambda: run(chunk)), 4)
@@ -828,7 +833,9 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5, rounds=5):
                "runs": grpo_heads,
                "note": "fused_linear_grpo_step (chunks of the given token count, 'default' "
                        "its own chunking: library "
-                       "GEMMs + klp_grpo_step, d_hidden / d_weight computed in the forward) "
+                       "GEMMs + klp_grpo_step, d_hidden / d_weight computed in the forward), "
+                       "and vocab_chunked_head (fused_linear_logprob_entropy, the "
+                       "vocabulary-chunked head, + fused_grpo_loss + backward), "
                        "against matmul + fused_logprob_entropy + fused_grpo_loss + backward; "
                        "loss + backward per iteration; peak memory above inputs and weights "
                        "during one iteration, the new gradients included"}}
