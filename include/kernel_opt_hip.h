@@ -176,8 +176,9 @@ int klp_bwd_temp(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
  * every call leaves it zero-filled.  All calls on one GPU share that GPU's
  * array, so calls that overlap on one GPU (on other streams, from other
  * threads) race and must be ordered by the caller: overlapping calls can
- * also leave the array's counters non-zero, which breaks later calls.
- * Arguments and results as klp_fwd.
+ * also leave the array's counters non-zero, which breaks later calls.  The
+ * array used is the current device's (hipGetDevice): `stream` must belong to
+ * the current device.  Arguments and results as klp_fwd.
  */
 #define KLP_FWD_NOALLOC_SCRATCH_BYTES 65536
 int klp_fwd_noalloc(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
