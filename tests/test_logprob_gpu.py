@@ -532,6 +532,24 @@ def test_split_rows_targets_at_piece_edges(dtype, splits, oracle):
     assert all(torch.equal(a, b) for a, b in zip(outs, again))
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_split_rows_more_pieces_than_vectors(dtype, oracle):
+    """Most pieces empty (V = 100: 12 or 25 vectors in 64 pieces) and a row
+    that is all scalar head and tail (V = 3): the empty pieces still count
+    themselves, and the last one to arrive merges."""
+    from kernel_opt import _C
+    for V, offset in ((100, 0), (100, 1), (3, 1)):
+        N = 9
+        x_cpu = seeded_logits((N, V), dtype, seed=900 + V + offset)
+        t_cpu = seeded_targets((N,), V, seed=900 + V)
+        buf = torch.empty(N * V + offset, dtype=dtype, device=DEV)
+        x = buf[offset:].view(N, V)
+        x.copy_(x_cpu.to(DEV))
+        outs = [torch.full((N,), float("nan"), device=DEV) for _ in range(3)]
+        _C.fwd_launch(x, t_cpu.to(DEV), *outs, config=(4, 2, 64, 0))
+        _check_fwd(oracle, x_cpu, t_cpu, outs, FWD_TOL[dtype], label=f"V={V} off={offset}")
+
+
 def test_split_workspace_left_zero():
     """Through the C ABI with a caller workspace: zero-filled before the first
     call, zero-filled after each call, whatever the shapes of the calls that
