@@ -215,13 +215,18 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
         if (e > kMaxSplits) e = kMaxSplits;
         if (e >= 1 && nvec / e >= tile - tile / 8) s = e;
     }
-    // Small grids (up to kBwdSmallGrid workgroups of 16 waves: C1, C2):
-    // 8-wave workgroups over twice the pieces, each the same fraction of
-    // its iteration.  C2 [1024, 152064] bf16: 101.7 us against 104.5-105.2
-    // back to back, 101.4-101.9 against 102.1-103.0 flushed (two boxes); C1
-    // equal back to back, 14.4-14.8 against 15.4-15.7 flushed.  Larger grids
-    // keep 16 waves (C3 666 against 662 us, C4 3251 against 3131 us).
-    if (c.waves == 16 && n_rows * s <= kBwdSmallGrid && 2 * s <= kMaxSplits) {
+    // Small grids (up to kBwdSmallGrid workgroups of 16 waves: C1, C2) and
+    // fp32 rows: 8-wave workgroups over twice the pieces, each the same
+    // fraction of its iteration.  C2 [1024, 152064] bf16: 101.7 us against
+    // 104.5-105.2 back to back, 101.4-101.9 against 102.1-103.0 flushed (two
+    // boxes); C1 equal back to back, 14.4-14.8 against 15.4-15.7 flushed.
+    // fp32 (half the arithmetic per byte of bf16 / fp16): C5 2829 against
+    // 2895 us, [8192, 32000] 329 against 344, [32768, 32000] 1283 against
+    // 1331, [4096, 152064] 802 against 825, [2048, 262144] 697 against 685.
+    // Larger bf16 / fp16 grids keep 16 waves (C3 666 against 662 us, C4
+    // 3251 against 3131 us).
+    if (c.waves == 16 && (n_rows * s <= kBwdSmallGrid || dtype == KLP_FP32) &&
+        2 * s <= kMaxSplits) {
         c.waves = 8;
         s *= 2;
     }

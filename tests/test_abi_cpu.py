@@ -161,6 +161,8 @@ def test_default_launch_shapes():
     assert _C.default_config("bwd", torch.float32, 256, 32000)[:3] == (8, 2, 8)
     assert _C.default_config("bwd", torch.float16, 8192, 128256)[:3] == (16, 2, 8)
     assert _C.default_config("bwd", torch.bfloat16, 32768, 151936)[:3] == (16, 2, 10)
+    # fp32 rows: 8 waves as well (C5)
+    assert _C.default_config("bwd", torch.float32, 8192, 262144)[:3] == (8, 2, 64)
 
 
 def test_shim_rejects_cpu_tensors_with_reference_messages():
