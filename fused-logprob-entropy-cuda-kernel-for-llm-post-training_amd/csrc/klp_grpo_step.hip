@@ -54,6 +54,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uin
                                              static_cast<int>(bytes), 0x00020000);
 }
 
+// A 16-byte non-temporal buffer store, then two wait states before the
+// wave's next instruction.  A VALU write to the store's data registers in the
+// cycles right after a buffer store whose offset is an SGPR reached memory in
+// the store's place on gfx950: a pass 2 that reused each stored register at
+// once for the next vector's unpack wrote that unpack's first dword instead of
+// the gradient's in ~2% of its vectors.  The compiler puts wait states there
+// only for a constant offset, so they are written here.
+__device__ __forceinline__ void store_vec_nt(u32x4 v, __amdgpu_buffer_rsrc_t rs, uint32_t voff,
+                                             uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, voff, soff, kCachePolicyNt);
+    asm volatile("s_nop 1");
+}
+
 // The token's GRPO inputs.
 struct RowInputs {
     int64_t tgt;
@@ -259,26 +272,30 @@ __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_kernel(GrpoStepPar
     for (int k = 0; k < NV; ++k) {
         const uint32_t i = tid + k * kStepThreads;
         if (k <= n_full)
-            __builtin_amdgcn_raw_buffer_store_b128(
-                grad_vec<DT, kScaled>(r[k], i, g, t_vec, t_elem, p.scale), ds, i * 16u, 0,
-                kCachePolicyNt);
+            store_vec_nt(grad_vec<DT, kScaled>(r[k], i, g, t_vec, t_elem, p.scale), ds, i * 16u,
+                         0);
     }
 }
 
 // Persistent workgroups (one per CU the kernel fits) that take rows one
 // after another, the next row from a counter (StepSched), so that a CU that
-// streams faster gets more rows.  While a row's gradient is stored, each
-// register is refilled with the next row's vector right after its gradient
-// leaves: the next row streams in under the current row's pass 2 instead of
-// after the workgroup ends.
+// streams faster gets more rows.  Once a row's gradient stores are issued,
+// the next row's loads follow at once, into the same registers: the next
+// row arrives while the workgroup would otherwise end and a new one start,
+// and its scan runs as its vectors arrive.  The stores all go ahead of the
+// loads: a CU writes, then reads, in long runs.  Refilling each register
+// right after its own store instead (stores and loads alternating) measured
+// 7% slower at bf16 [32768, 151936] (3601-3629 against 3339-3361 us), where
+// the scan then ran on a row already in registers, with no memory traffic
+// from the CU.
 //
 // The loads of each row are counted, not waited for as a whole: after a
 // pass 2 the vector memory operations in flight are, oldest first, the next
-// row's GRPO inputs, then store 0, load 0, store 1, load 1, ...; vector k of
-// the next scan waits until at most 2 * (NV - 1 - k) of them remain.  The
-// first row's loads follow the same pattern (each after a store that a
-// zero-length descriptor drops), so the compiler's waits at the loop head are
-// those of the steady state.
+// row's GRPO inputs, then stores 0 .. NV-1, then loads 0 .. NV-1; vector k of
+// the next scan waits until at most NV - 1 - k of them remain.  The first
+// row's loads follow the same pattern (behind NV stores that a zero-length
+// descriptor drops), so the compiler's waits at the loop head are those of
+// the steady state.
 template <int DT, int NV, bool kScaled>
 __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_rows_kernel(GrpoStepParams p) {
     typedef typename Traits<DT>::elem elem;
@@ -305,8 +322,11 @@ __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_rows_kernel(GrpoSt
         const __amdgpu_buffer_rsrc_t none = row_rsrc(p.d_logits, 0u);
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{0, 0, 0, 0}, none, voff,
-                                                   k * kStepThreads * 16, kCachePolicyNt);
+            store_vec_nt(u32x4{0, 0, 0, 0}, none, voff, k * kStepThreads * 16);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
             r[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, k * kStepThreads * 16,
                                                          kCachePolicyNt);
             __builtin_amdgcn_sched_barrier(0);
@@ -365,9 +385,9 @@ __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_rows_kernel(GrpoSt
         const __amdgpu_buffer_rsrc_t ns = row_rsrc(
             static_cast<const elem*>(p.logits) + row_offset(p.rm, nrow), more ? row_bytes : 0u);
 
-        // Pass 2: d_logits from the registers, each register refilled with
-        // the next row's vector after its gradient is stored.  Every vector
-        // is stored and loaded, past the row's end too (the descriptors drop
+        // Pass 2: d_logits from the registers, then the next row's loads
+        // into them, all issued at once behind the stores.  Every vector is
+        // stored and loaded, past the row's end too (the descriptors drop
         // those stores and return zeros for those loads), which keeps the
         // count of operations in flight the same on every path.
         const __amdgpu_buffer_rsrc_t ds =
@@ -377,9 +397,12 @@ __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_rows_kernel(GrpoSt
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const uint32_t i = tid + k * kStepThreads;
-            __builtin_amdgcn_raw_buffer_store_b128(
-                grad_vec<DT, kScaled>(r[k], i, g, t_vec, t_elem, p.scale), ds, voff,
-                k * kStepThreads * 16, kCachePolicyNt);
+            store_vec_nt(grad_vec<DT, kScaled>(r[k], i, g, t_vec, t_elem, p.scale), ds, voff,
+                         k * kStepThreads * 16);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
             r[k] = __builtin_amdgcn_raw_buffer_load_b128(ns, voff, k * kStepThreads * 16,
                                                          kCachePolicyNt);
             __builtin_amdgcn_sched_barrier(0);
@@ -396,20 +419,27 @@ __global__ __launch_bounds__(kStepThreads) void klp_grpo_step_rows_kernel(GrpoSt
     }
 }
 
-// Where the persistent kernel runs (given a counter): bf16 rows of 16 or
-// more vectors per thread, from 16 rows per workgroup on.  Measured on one
-// box against the one-row-per-workgroup kernel (us, same inputs):
-//   bf16 [32768, 151936]  3639 against 3994      bf16 [8192, 128256]  768 against 824
-//   bf16 [4096, 152064]    471 against 473       bf16 [2048, 152064]  244 against 240
-//   fp16 [8192, 128256]    767 against 754       fp32 [8192, 32000]   364 against 355
-//   bf16 [8192, 32000]     207 against 178 (the one-row kernel fits two
-//                          workgroups per CU there, the persistent one one).
-// fp16 rows convert inside v_fma_mix, and the one-row kernel then keeps up.
-constexpr int64_t kPersistMinRowsPerWorkgroup = 16;
+// Where the persistent kernel runs (given a counter): rows of 8 or more
+// vectors per thread (bf16 and fp16 V > 32768, fp32 V > 16384), from 8 rows
+// per workgroup on.  Measured on one box against the one-row-per-workgroup
+// kernel (us, same inputs, two runs each):
+//   bf16 [32768, 151936]  3339-3342 against 3619-3620
+//   bf16 [8192, 128256]    716-762  against 765-774
+//   fp16 [8192, 128256]    703-704  against 789-791
+//   bf16 [4096, 152064]    434      against 466-467
+//   bf16 [4096, 65536]     189-190  against 206-211
+//   fp32 [8192, 32000]     337-339  against 354-355
+//   bf16 [2048, 152064]    230-234  against 236
+//   bf16 [1024, 152064]    123-126  against 124   (4 rows per workgroup)
+//   fp32 [256, 32000]       14.5    against 11-12  (1 row per workgroup)
+//   bf16 [8192, 32000]     194-200  against 177   (4 vectors per thread: the
+//                          one-row kernel fits two workgroups per CU there,
+//                          the persistent one one).
+constexpr int64_t kPersistMinRowsPerWorkgroup = 8;
 
 template <int DT, int NV>
 constexpr bool persistent_pays() {
-    return DT == kBF16 && NV >= 16;
+    return NV >= 8;
 }
 
 // Workgroups of the persistent kernel: as many as are resident at once (CUs

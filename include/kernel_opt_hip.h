@@ -309,9 +309,10 @@ int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp
  * klp_bwd instead.
  * sched (nullable): KLP_GRPO_STEP_SCHED_BYTES of device memory, 8-byte
  * aligned, zero before the first call that gets it; every call leaves it
- * zero.  With it, batches of many rows (8 or more per resident workgroup)
- * run on persistent workgroups that take rows from a counter held there;
- * without it, or for fewer rows, each row has a workgroup of its own.
+ * zero.  With it, batches of many rows longer than 64 KiB (8 or more rows
+ * per resident workgroup) run on persistent workgroups that take rows from
+ * a counter held there; without it, or for fewer or shorter rows, each row
+ * has a workgroup of its own.
  * Results are the same bits either way.  Calls that share one must be
  * ordered (one stream): concurrent calls on one counter skip rows.
  */

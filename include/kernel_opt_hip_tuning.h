@@ -58,7 +58,8 @@ void klp_default_config(int which, int dtype, int64_t n_rows, int64_t vocab,
  * Fewest rows from which klp_grpo_step, given a `sched` counter, runs its
  * persistent kernel on the current device for rows of `vocab` elements of
  * `dtype` (temperature 1 or not: the two variants are separate kernels);
- * -1 if the device cannot be queried, 0 for an unsupported dtype or vocab.
+ * -1 if the device cannot be queried; 0 for an unsupported dtype or vocab,
+ * and for rows of at most 64 KiB, which always run one row per workgroup.
  */
 int64_t klp_grpo_step_persistent_min_rows(int dtype, int64_t vocab, int scaled);
 

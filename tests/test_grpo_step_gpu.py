@@ -466,6 +466,11 @@ def _step_abi(x, t, old, ref, adv, w, temperature, per_token, sched):
     (torch.bfloat16, 5, 1100, 100000, 0.7, 1, True, False),    # 16 vectors, a partial one;
                                                                # temperature, per-token adv
     (torch.bfloat16, 5, 1030, 155648, 1.3, 0, False, True),    # the row capacity, strided
+    (torch.bfloat16, 3, 1024, 50000, 1.0, 0, True, True),      # 8 vectors, strided
+    (torch.float16, 3, 1024, 128256, 1.0, 0, True, False),     # the C3 vocabulary
+    (torch.float16, 3, 1024, 90000, 0.9, 1, False, False),     # 12 vectors
+    (torch.float32, 3, 1024, 32000, 0.8, 1, False, False),     # fp32, 8 vectors
+    (torch.float32, 3, 1024, 77824, 1.0, 0, True, False),      # fp32 row capacity
 ])
 def test_persistent_rows_match_one_row_per_workgroup(dtype, B, S, V, temperature, per_token,
                                                      with_ref, sliced):
@@ -511,16 +516,18 @@ def test_persistent_rows_match_one_row_per_workgroup(dtype, B, S, V, temperature
 
 
 def test_persistent_rows_only_where_they_pay():
-    """The persistent kernel is used for bf16 rows of 16 or more 16-byte
-    vectors per thread (V > 98304), from 16 rows per resident workgroup on;
-    elsewhere the one-row kernel measured as fast or faster, and the query
-    reports 0."""
+    """The persistent kernel is used for rows of 8 or more 16-byte vectors
+    per thread (bf16 / fp16 V > 32768, fp32 V > 16384), from 8 rows per
+    resident workgroup on; for shorter rows the one-row kernel fits two
+    workgroups per CU and measured faster, and the query reports 0."""
     from kernel_opt._library import KLP_BF16, KLP_FP16, KLP_FP32, lib
     n_cu = torch.cuda.get_device_properties(0).multi_processor_count
     for scaled in (0, 1):
-        for V in (100000, 152064, 155648):
-            assert lib.klp_grpo_step_persistent_min_rows(KLP_BF16, V, scaled) == 16 * n_cu
-        for dtype, V in ((KLP_BF16, 32000), (KLP_BF16, 98304), (KLP_FP16, 128256),
-                         (KLP_FP32, 77824)):
-            assert lib.klp_grpo_step_persistent_min_rows(dtype, V, scaled) == 0
+        for dtype, V in ((KLP_BF16, 32776), (KLP_BF16, 100000), (KLP_BF16, 152064),
+                         (KLP_BF16, 155648), (KLP_FP16, 128256), (KLP_FP32, 16388),
+                         (KLP_FP32, 32000), (KLP_FP32, 77824)):
+            assert lib.klp_grpo_step_persistent_min_rows(dtype, V, scaled) == 8 * n_cu, (dtype, V)
+        for dtype, V in ((KLP_BF16, 32000), (KLP_BF16, 32768), (KLP_FP16, 32768),
+                         (KLP_FP32, 16384)):
+            assert lib.klp_grpo_step_persistent_min_rows(dtype, V, scaled) == 0, (dtype, V)
         assert lib.klp_grpo_step_persistent_min_rows(KLP_BF16, 155656, scaled) == 0
