@@ -108,14 +108,27 @@ def _ld(t: torch.Tensor) -> int:
     return t.stride(0) if t.size(0) > 1 else t.size(1)
 
 
-# Vocabulary chunk of the chunked head: about CHUNK_COLS columns, balanced
-# over the vocabulary in whole multiples of 1024 (so that no small tail GEMM
-# runs), and fewer while one chunk of logits would exceed CHUNK_MAX_BYTES,
-# half of the 256 MB Infinity Cache, so that the logprob pass over a chunk
-# reads it from the cache.  Measured at Qwen2.5-7B's head (V = 152064,
-# D = 3584): 1024 tokens, 15360 columns 0.99 ms (12288: 1.11, unfused 0.96);
-# 8192 tokens, 8192 columns 6.58 ms (15360, 240 MiB a chunk: 6.85; unfused
-# 6.65).  The library GEMM's speed at the chunk shape dominates.
+# Vocabulary chunk of the chunked head.  Small batches (a chunk of
+# CHUNK_COLS_WIDE columns within CHUNK_WIDE_MAX_BYTES: up to 1024 bf16 tokens)
+# take chunks of CHUNK_COLS_WIDE columns, the last one holding the rest.
+# Larger batches take about CHUNK_COLS columns, balanced over the vocabulary
+# in whole multiples of 1024 (so that no small tail GEMM runs), and fewer
+# while one chunk of logits would exceed CHUNK_MAX_BYTES, half of the 256 MB
+# Infinity Cache, so that the logprob pass over a chunk reads it from the
+# cache.  The library GEMM's speed at the chunk shape dominates, and it does
+# not follow the width monotonically.  Measured at Qwen2.5-7B's head
+# (V = 152064, D = 3584; forward, forward + backward, ms; two runs):
+#   1024 tokens: 32768 columns 0.934-0.940, 4.75-4.76; balanced 15360
+#                0.975-0.979, 4.79; unfused 0.927-0.932, 3.84
+#   2048 tokens: balanced 15360 1.75-1.76, 8.40-8.44; 16384 1.70-1.71,
+#                9.80-9.82 (its backward GEMMs are slow); unfused 1.70, 7.04
+#   4096 tokens: balanced 15360 3.34, 15.22-15.24; 8192 3.30-3.31,
+#                15.30-15.31; unfused 3.25-3.27, 12.94
+#   8192 tokens: balanced 8192 6.39-6.40, 30.40-30.46; unfused 6.41-6.43, 24.65
+# The forward and the backward use the same chunks: the backward recomputes
+# each chunk's logits with the same GEMM call, hence the same values.
+CHUNK_COLS_WIDE = 32768
+CHUNK_WIDE_MAX_BYTES = 64 << 20
 CHUNK_COLS = 16384
 CHUNK_MAX_BYTES = 128 << 20
 
@@ -128,6 +141,8 @@ def vocab_chunk(n_tokens: int, vocab: int, elem_bytes: int = 2,
         if chunk_vocab < 1:
             raise ValueError(f"chunk_vocab must be >= 1, got {chunk_vocab}")
         return min(int(chunk_vocab), max(vocab, 1))
+    if n_tokens * CHUNK_COLS_WIDE * elem_bytes <= CHUNK_WIDE_MAX_BYTES:
+        return min(vocab, CHUNK_COLS_WIDE)
     cols = CHUNK_COLS
     while cols > 1024 and n_tokens * cols * elem_bytes > CHUNK_MAX_BYTES:
         cols //= 2
