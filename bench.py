@@ -664,7 +664,7 @@ def shard_timing(dev, K, N=32768, V=151936, P=8):
     return out
 
 
-def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5, rounds=5):
+def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5, rounds=6):
     """The fused LM head against the unfused path on Qwen2.5-7B's head shape
     with C2's 1024 tokens (and 8x that), random weights.  Three paths:
     "chunked" (the default: a library GEMM per vocabulary chunk, then
@@ -719,9 +719,13 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5, rounds=5):
             fn()
             fn()
         times = {k: [] for k in fns}
-        for _ in range(rounds):
-            for k, fn in fns.items():
-                times[k].append(timed(fn))
+        order = list(fns)
+        for r in range(rounds):
+            # the order reverses every round: under sustained GEMM load the
+            # clock drifts within a round, and a fixed order would hand the
+            # same path the same share of it
+            for k in (order if r % 2 == 0 else order[::-1]):
+                times[k].append(timed(fns[k]))
         return {k: round(statistics.median(v), 4) for k, v in times.items()}
 
     def peak_mib(fn, h):
@@ -828,7 +832,8 @@ def lmhead_timing(dev, N=1024, V=152064, D=3584, K=5, rounds=5):
                             "frac": round(c["fwd_tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)},
            "note": "fused = the chunked head (default); mfma = klp_lmh_fwd with the "
                    "vocabulary-chunked backward; unfused = bf16 library matmul to [N, V] "
-                   "logits, then klp_fwd / klp_bwd; medians of interleaved rounds",
+                   "logits, then klp_fwd / klp_bwd; medians of 6 interleaved rounds of 5 "
+                   "calls, the order reversed every round",
            "grpo_step": {
                "runs": grpo_heads,
                "note": "fused_linear_grpo_step (chunks of the given token count, 'default' "

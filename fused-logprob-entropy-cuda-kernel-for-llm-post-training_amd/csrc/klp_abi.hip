@@ -315,6 +315,8 @@ int fwd_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64
     p.scale = scale;
     p.target_offset = 0;
     p.state = nullptr;
+    p.merge_states = nullptr;
+    p.merge_count = 0;
     if (injected_failure("forward")) return KLP_ELAUNCH;
     return after_launch(klp::launch_fwd(dtype, p, cfg, static_cast<hipStream_t>(stream)),
                         "forward");
@@ -687,6 +689,45 @@ int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp
                         "grpo backward");
 }
 
+// One launch over a vocabulary shard or chunk (one workgroup per row):
+// writes the rows' states to `state`, or, with `merge_states` non-null (the
+// last chunk of klp_fwd_chunk), merges the earlier chunks' states with its
+// own and writes the outputs.
+static int shard_impl(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                      int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                      const int64_t* targets, int64_t vocab_offset, float scale, float* state,
+                      const float* merge_states, int64_t merge_count, float* logprob,
+                      float* entropy, float* lse, void* stream, const char* what) {
+    // One workgroup per row (the states are per row, not per piece).
+    klp::FwdConfig cfg = default_fwd_config(dtype, n_rows, vocab);
+    if (cfg.splits > 1) {
+        cfg.waves = 16;
+        cfg.splits = 1;
+    }
+    int rc;
+    if ((rc = check_fwd_piece(dtype, vocab, cfg)) != KLP_OK) return rc;
+    if ((rc = check_grid(n_rows, 1, cfg.waves * 64)) != KLP_OK) return rc;
+    klp::FwdParams p;
+    p.logits = logits;
+    p.rm = klp::RowMap{rows_inner, stride_outer, stride_inner};
+    p.n_rows = n_rows;
+    p.vocab = vocab;
+    p.targets = targets;
+    p.logprob = logprob;
+    p.entropy = entropy;
+    p.lse = lse;
+    p.splits = 1;
+    p.partials = nullptr;
+    p.counters = nullptr;
+    p.scale = scale;
+    p.target_offset = vocab_offset;
+    p.state = state;
+    p.merge_states = merge_states;
+    p.merge_count = merge_count;
+    if (injected_failure(what)) return KLP_ELAUNCH;
+    return after_launch(klp::launch_fwd(dtype, p, cfg, static_cast<hipStream_t>(stream)), what);
+}
+
 int klp_fwd_shard(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                   int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
                   const int64_t* targets, int64_t vocab_offset, float temperature, float* state,
@@ -700,31 +741,40 @@ int klp_fwd_shard(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
     if (n_rows == 0) return ok();
     if (state == nullptr || !aligned(state, 16))
         return fail(KLP_EINVAL, "state must be non-null and 16-byte aligned");
-    // One workgroup per row (the states are per row, not per piece).
-    klp::FwdConfig cfg = default_fwd_config(dtype, n_rows, vocab);
-    if (cfg.splits > 1) {
-        cfg.waves = 16;
-        cfg.splits = 1;
-    }
-    if ((rc = check_fwd_piece(dtype, vocab, cfg)) != KLP_OK) return rc;
-    if ((rc = check_grid(n_rows, 1, cfg.waves * 64)) != KLP_OK) return rc;
-    klp::FwdParams p;
-    p.logits = logits;
-    p.rm = klp::RowMap{rows_inner, stride_outer, stride_inner};
-    p.n_rows = n_rows;
-    p.vocab = vocab;
-    p.targets = targets;
-    p.logprob = nullptr;
-    p.entropy = nullptr;
-    p.lse = nullptr;
-    p.splits = 1;
-    p.partials = nullptr;
-    p.scale = scale;
-    p.target_offset = vocab_offset;
-    p.state = state;
-    if (injected_failure("shard forward")) return KLP_ELAUNCH;
-    return after_launch(klp::launch_fwd(dtype, p, cfg, static_cast<hipStream_t>(stream)),
-                        "shard forward");
+    return shard_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
+                      targets, vocab_offset, scale, state, nullptr, 0, nullptr, nullptr, nullptr,
+                      stream, "shard forward");
+}
+
+int klp_fwd_chunk(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                  int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                  const int64_t* targets, int64_t vocab_offset, float temperature, float* states,
+                  int64_t chunk_index, int64_t n_chunks, float* logprob, float* entropy,
+                  float* lse, void* stream) {
+    int rc = check_rows(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
+                        targets);
+    if (rc != KLP_OK) return rc;
+    float scale;
+    if (!scale_from_temperature(temperature, &scale)) return KLP_EINVAL;
+    if (vocab_offset < 0) return fail(KLP_EINVAL, "vocab_offset must be >= 0");
+    if (n_chunks < 1 || chunk_index < 0 || chunk_index >= n_chunks)
+        return fail(KLP_EINVAL, "chunk_index (%lld) must lie in [0, n_chunks) (n_chunks %lld)",
+                    static_cast<long long>(chunk_index), static_cast<long long>(n_chunks));
+    if (n_rows == 0) return ok();
+    if (states == nullptr || !aligned(states, 16))
+        return fail(KLP_EINVAL, "states must be non-null and 16-byte aligned");
+    if (n_chunks > (int64_t{1} << 62) / 16 / n_rows)
+        return fail(KLP_EINVAL, "n_chunks * n_rows states overflow");
+    if (chunk_index + 1 < n_chunks)
+        return shard_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
+                          targets, vocab_offset, scale, states + chunk_index * n_rows * 4,
+                          nullptr, 0, nullptr, nullptr, nullptr, stream, "chunk forward");
+    if ((rc = check_f32(logprob, "logprob")) != KLP_OK) return rc;
+    if ((rc = check_f32(entropy, "entropy")) != KLP_OK) return rc;
+    if ((rc = check_f32(lse, "lse")) != KLP_OK) return rc;
+    return shard_impl(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
+                      targets, vocab_offset, scale, nullptr, states, n_chunks - 1, logprob,
+                      entropy, lse, stream, "chunk forward");
 }
 
 int klp_fwd_shard_merge(const float* states, int64_t n_shards, int64_t n_rows,

@@ -122,8 +122,53 @@ __device__ __forceinline__ void scan_row_piece(Stat& s, const typename Traits<DT
     }
 }
 
-template <int DT, int WAVES, int U, bool kSplit, bool kScaled>
-__global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Last chunk of a row set cut into vocabulary chunks (klp_fwd_chunk): wave 0
+// merges the states of the earlier chunks, p.merge_states[k][row] for
+// k < p.merge_count (written by the earlier chunks' launches on the same
+// stream), in chunk order and then this chunk's own state `own` (lane 0's),
+// the same sequence of combine() calls klp_fwd_shard_merge_kernel makes over
+// the same states, so the outputs are bitwise equal to its.  The target logit
+// is the one recorded by the chunk that holds the target: every other chunk
+// records +0.0, so the last word whose bits are not all zero is taken (a
+// target logit of +0.0 leaves +0.0, its own value).  Lanes load 64 states
+// at a time; the combines run on lane-uniform values.
+__device__ __forceinline__ void merge_chunks_final(const FwdParams& p, int64_t row,
+                                                   const Stat own, float own_xt, int lane) {
+    const float4* st = reinterpret_cast<const float4*>(p.merge_states);
+    Stat acc = stat_empty();
+    float xt = 0.0f;
+    for (int64_t base = 0; base < p.merge_count; base += 64) {
+        const int64_t k = base + lane;
+        float4 q = make_float4(-INFINITY, 0.0f, 0.0f, 0.0f);
+        if (k < p.merge_count) q = st[k * p.n_rows + row];
+        const int cnt = static_cast<int>(p.merge_count - base < 64 ? p.merge_count - base : 64);
+        for (int j = 0; j < cnt; ++j) {
+            acc = combine(acc, Stat{readlane_f32(q.x, j), readlane_f32(q.y, j),
+                                    readlane_f32(q.z, j)});
+            const float w = readlane_f32(q.w, j);
+            if (__float_as_uint(w) != 0u) xt = w;
+        }
+    }
+    acc = combine(acc, Stat{readlane_f32(own.m, 0), readlane_f32(own.z, 0),
+                            readlane_f32(own.t, 0)});
+    const float w = readlane_f32(own_xt, 0);
+    if (__float_as_uint(w) != 0u) xt = w;
+    if (lane != 0) return;
+    const RowOut o = finalize(acc, xt);
+    p.logprob[row] = o.logp;
+    p.entropy[row] = o.ent;
+    p.lse[row] = o.lse;
+}
+
+// One workgroup's row (or row piece); the body of klp_fwd_kernel and of
+// klp_fwd_chunk_final_kernel (kMergeChunks: the last chunk's launch of
+// klp_fwd_chunk, which merges the chunks' states instead of writing its own).
+template <int DT, int WAVES, int U, bool kSplit, bool kScaled, bool kMergeChunks>
+__device__ __forceinline__ void fwd_row(const FwdParams& p) {
     typedef typename Traits<DT>::elem elem;
     constexpr int NTHREADS = WAVES * 64;
     constexpr int EPV = Traits<DT>::kPerVec;
@@ -246,6 +291,10 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
         p.lse[row] = o.lse;
         return;
     }
+    if constexpr (kMergeChunks) {
+        merge_chunks_final(p, row, r, x_target, lane);
+        return;
+    }
     if (lane != 0) return;  // thread 0 (it read the target logit)
 
     if (p.state) {
@@ -258,6 +307,16 @@ __global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
     p.logprob[row] = o.logp;
     p.entropy[row] = o.ent;
     p.lse[row] = o.lse;
+}
+
+template <int DT, int WAVES, int U, bool kSplit, bool kScaled>
+__global__ __launch_bounds__(WAVES * 64) void klp_fwd_kernel(FwdParams p) {
+    fwd_row<DT, WAVES, U, kSplit, kScaled, false>(p);
+}
+
+template <int DT, int WAVES, int U, bool kScaled>
+__global__ __launch_bounds__(WAVES * 64) void klp_fwd_chunk_final_kernel(FwdParams p) {
+    fwd_row<DT, WAVES, U, false, kScaled, true>(p);
 }
 
 // Merge of the row states of `n_shards` vocabulary shards, one thread per row,
@@ -320,6 +379,9 @@ __global__ __launch_bounds__(128) void klp_fwd_naive_kernel(NaiveParams p) {
 // ---------------------------------------------------------------------------
 template <int DT, int WAVES, int U, bool kScaled>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
+    if (p.merge_states != nullptr)
+        return launch_kernel(klp_fwd_chunk_final_kernel<DT, WAVES, U, kScaled>,
+                             dim3(static_cast<unsigned>(p.n_rows)), dim3(WAVES * 64), stream, p);
     if (p.splits == 1)
         return launch_kernel(klp_fwd_kernel<DT, WAVES, U, false, kScaled>,
                              dim3(static_cast<unsigned>(p.n_rows)), dim3(WAVES * 64), stream, p);

@@ -36,6 +36,12 @@ struct FwdParams {
     // written there instead of the outputs.
     int64_t target_offset;
     float* state;
+    // Last vocabulary chunk of klp_fwd_chunk (splits == 1, state null): the
+    // earlier chunks' row states, [merge_count][n_rows] float4, merged in
+    // chunk order with this launch's own before the outputs are written.
+    // Null for every other launch.
+    const float* merge_states;
+    int64_t merge_count;
 };
 
 // Merge of per-shard row states (klp_fwd_shard_merge).

@@ -17,6 +17,7 @@ from .lmhead import (  # noqa: F401
     fused_linear_logprob_entropy,
     fused_linear_logprob_entropy_forward,
     vocab_chunk,
+    vocab_chunks,
 )
 
 

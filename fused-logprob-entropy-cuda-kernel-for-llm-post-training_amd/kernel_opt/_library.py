@@ -62,6 +62,8 @@ SIGNATURES = {
                      + [_vp, _vp, _vp, _sz, _vp]),
     "klp_fwd_shard": (_i32, _ROWS + [_vp, _i64, ctypes.c_float, _vp, _vp]),
     "klp_fwd_shard_merge": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "klp_fwd_chunk": (_i32, _ROWS + [_vp, _i64, ctypes.c_float, _vp, _i64, _i64, _vp, _vp, _vp,
+                                     _vp]),
     "klp_grpo_step_max_vocab": (_i64, [_i32]),
     "klp_scale_inplace": (_i32, [_vp, _i32, _i64, _vp, _vp]),
     "klp_grpo_step": (_i32, _ROWS + [_vp, ctypes.c_float] + [_vp] * 4 + [_i64]

@@ -8,18 +8,17 @@ the Liger-style head the reference names as its follow-up
 
 Two implementations:
 
-``impl="chunked"`` (default) walks the vocabulary in chunks of ~16K columns.
-Per chunk a library GEMM writes the chunk's logits (``[N, chunk]`` in the
-input dtype, 30 MiB at N = 1024, at most 128 MiB: small enough to stay in
-the 256 MB Infinity Cache) and ``klp_fwd_shard`` folds them into each token's online
-state straight from the cache; ``klp_fwd_shard_merge`` merges the chunk
-states in chunk order.  The weight is read once, the logits never reach HBM
-as one tensor, and the logprob pass reads cache instead of HBM.  The
-backward recomputes each chunk with the same GEMM call (bit-identical
-logits), applies ``klp_bwd`` with chunk-relative targets, and accumulates
-``d_hidden += d_chunk @ W_chunk`` (fp32) and ``d_weight[chunk] = d_chunk^T @
-hidden``.  Numerics are the unfused path's: logits rounded once to the input
-dtype by the GEMM.
+``impl="chunked"`` (default) walks the vocabulary in chunks
+(:func:`vocab_chunks`: 32768 columns for small batches, ~16K for larger
+ones).  Per chunk a library GEMM writes the chunk's logits (``[N, chunk]``
+in the input dtype, at most 128 MiB) and ``klp_fwd_chunk`` folds them into
+each token's online state; the last chunk's launch merges the chunk states
+in chunk order and writes the outputs.  The weight is read once and the
+logits never exist as one ``[N, V]`` tensor.  The backward recomputes each
+chunk with the same GEMM call (bit-identical logits), applies ``klp_bwd``
+with chunk-relative targets, and accumulates ``d_hidden += d_chunk @
+W_chunk`` (fp32) and ``d_weight[chunk] = d_chunk^T @ hidden``.  Numerics are
+the unfused path's: logits rounded once to the input dtype by the GEMM.
 
 ``impl="mfma"`` is the hand-written gfx950 kernel (klp_lmh_fwd,
 csrc/klp_lmhead.hip): the GEMM with the logprob / entropy reduction as its
@@ -51,7 +50,8 @@ from . import _C
 from ._library import DTYPE_CODES, check_status, device_guard, lib, ptr, stream_handle
 from .linear_grpo import _accumulate_f32
 
-__all__ = ["fused_linear_logprob_entropy", "fused_linear_logprob_entropy_forward", "vocab_chunk"]
+__all__ = ["fused_linear_logprob_entropy", "fused_linear_logprob_entropy_forward", "vocab_chunk",
+           "vocab_chunks"]
 
 
 _ptr = ptr
@@ -127,6 +127,14 @@ def _ld(t: torch.Tensor) -> int:
 #   8192 tokens: balanced 8192 6.39-6.40, 30.40-30.46; unfused 6.41-6.43, 24.65
 # The forward and the backward use the same chunks: the backward recomputes
 # each chunk's logits with the same GEMM call, hence the same values.
+# In the small-batch regime a last chunk wider than CHUNK_COLS_WIDE / 2 is
+# cut into CHUNK_COLS_WIDE / 2 columns plus the rest: the library GEMM runs
+# widths of 16384 and 32768 columns at 5.0-5.1 us per 1024 columns (1024
+# tokens, D = 3584), but 18432-22528 at 6.2-6.8 us (V = 152064's remainder of
+# 20992: 138.8 us, against 83.4 + ~36 us as 16384 + 4608).  Qwen2.5-7B's head
+# at 1024 tokens, forward, one box, launches queued (host-issued): chunks
+# 4 x 32768 + 20992 950.3 (927.2) us, 4 x 32768 + 16384 + 4608 942.4
+# (908.4) us, unfused 957.7 (923.2) us.
 CHUNK_COLS_WIDE = 32768
 CHUNK_WIDE_MAX_BYTES = 64 << 20
 CHUNK_COLS = 16384
@@ -151,6 +159,23 @@ def vocab_chunk(n_tokens: int, vocab: int, elem_bytes: int = 2,
     return min(vocab, -(-per // 1024) * 1024)
 
 
+def vocab_chunks(n_tokens: int, vocab: int, elem_bytes: int = 2,
+                 chunk_vocab: int | None = None) -> list:
+    """``(first column, width)`` of every vocabulary chunk of the chunked
+    head, in order: chunks of :func:`vocab_chunk` columns, the last one the
+    rest; in the small-batch regime a rest of at least half a chunk plus 1024
+    columns is cut in two (``CHUNK_COLS_WIDE // 2`` columns, then the
+    remainder).  The forward and the backward use the same chunks."""
+    vc = vocab_chunk(n_tokens, vocab, elem_bytes, chunk_vocab)
+    plan = [(c0, min(vc, vocab - c0)) for c0 in range(0, vocab, vc)]
+    wide = n_tokens * CHUNK_COLS_WIDE * elem_bytes <= CHUNK_WIDE_MAX_BYTES
+    half = CHUNK_COLS_WIDE // 2
+    if chunk_vocab is None and wide and plan and half + 1024 <= plan[-1][1] < CHUNK_COLS_WIDE:
+        c0, n = plan[-1]
+        plan[-1:] = [(c0, half), (c0 + half, n - half)]
+    return plan
+
+
 def _chunk_logits(buf, h2, weight, c0, n):
     """logits[:, c0:c0+n] = h2 @ weight[c0:c0+n]^T into a contiguous view of
     ``buf`` (the same call, hence the same values, in forward and backward)."""
@@ -159,39 +184,36 @@ def _chunk_logits(buf, h2, weight, c0, n):
     return out
 
 
-def _forward_chunked(h2, weight, t, T, vc, out):
-    N, V = h2.size(0), weight.size(0)
-    n_chunks = -(-V // vc)
+def _forward_chunked(h2, weight, t, T, plan, out):
+    N = h2.size(0)
+    n_chunks = len(plan)
     dev = h2.device
     states = torch.empty(n_chunks, N, 4, dtype=torch.float32, device=dev)
-    buf = torch.empty(N * min(vc, V), dtype=h2.dtype, device=dev)
+    buf = torch.empty(N * max(n for _, n in plan), dtype=h2.dtype, device=dev)
     code = DTYPE_CODES[h2.dtype]
     with device_guard(dev.index):
         stream = stream_handle(dev.index)
-        for c in range(n_chunks):
-            c0 = c * vc
-            n = min(vc, V - c0)
+        for c, (c0, n) in enumerate(plan):
             lg = _chunk_logits(buf, h2, weight, c0, n)
-            check_status(lib.klp_fwd_shard(_ptr(lg), code, N, n, *_C.row_layout(lg), _ptr(t),
-                                           c0, T, _ptr(states[c]), stream))
-        check_status(lib.klp_fwd_shard_merge(_ptr(states), n_chunks, N, _ptr(t), vc, V,
-                                             _ptr(out[0]), _ptr(out[1]), _ptr(out[2]), stream))
+            check_status(lib.klp_fwd_chunk(_ptr(lg), code, N, n, *_C.row_layout(lg), _ptr(t),
+                                           c0, T, _ptr(states), c, n_chunks, _ptr(out[0]),
+                                           _ptr(out[1]), _ptr(out[2]), stream))
 
 
-def _backward_chunked(h2, weight, t, T, vc, lse, ent, gl, ge, gs, need_h, need_w, impl):
+def _backward_chunked(h2, weight, t, T, plan, lse, ent, gl, ge, gs, need_h, need_w, impl):
     """d_hidden (fp32, or None) and d_weight (weight dtype, or None), one
-    vocabulary chunk at a time: d_logits exist for one chunk only."""
+    vocabulary chunk of ``plan`` at a time: d_logits exist for one chunk
+    only."""
     N, D, V = h2.size(0), h2.size(1), weight.size(0)
     dev = h2.device
     dh = torch.zeros(N, D, dtype=torch.float32, device=dev) if need_h else None
     dw = torch.empty(V, D, dtype=weight.dtype, device=dev) if need_w else None
-    cols = min(vc, V)
+    cols = max(n for _, n in plan)
     d_buf = torch.empty(N * (-(-cols // 4) * 4), dtype=weight.dtype, device=dev)
     lg_buf = torch.empty(N * cols, dtype=h2.dtype, device=dev) if impl == "chunked" else None
     with device_guard(dev.index):
         stream = stream_handle(dev.index)
-        for c0 in range(0, V, vc):
-            n = min(vc, V - c0)
+        for c0, n in plan:
             tc = t - c0  # chunk-relative: a target outside the chunk adds no one-hot term
             if impl == "chunked":
                 lg = _chunk_logits(lg_buf, h2, weight, c0, n)
@@ -246,8 +268,8 @@ class _FusedLinearLogprobEntropy(torch.autograd.Function):
             return None if g is None else g.to(torch.float32, copy=False).reshape(-1).contiguous()
 
         T = 1.0 if ctx.temperature is None else float(ctx.temperature)
-        vc = vocab_chunk(N, V, h2.element_size(), ctx.chunk_vocab)
-        dh, dw = _backward_chunked(h2, weight, t, T, vc, lse.reshape(-1), ent.reshape(-1),
+        plan = vocab_chunks(N, V, h2.element_size(), ctx.chunk_vocab)
+        dh, dw = _backward_chunked(h2, weight, t, T, plan, lse.reshape(-1), ent.reshape(-1),
                                    prep(g_logp), prep(g_ent), prep(g_lse), need_h, need_w,
                                    ctx.impl)
         if dh is not None:
@@ -280,7 +302,7 @@ def fused_linear_logprob_entropy_forward(hidden: torch.Tensor, weight: torch.Ten
         impl: ``"chunked"`` (bf16 / fp16 / fp32) or ``"mfma"`` (bf16, D a
             multiple of 64, both row strides multiples of 8).
         chunk_vocab: columns per vocabulary chunk (chunked head, and the
-            backward of both); default :func:`vocab_chunk`.
+            backward of both); default :func:`vocab_chunks`.
 
     Returns ``(logprob, entropy, lse)``, float32, shaped like ``targets``.
     """
@@ -295,7 +317,8 @@ def fused_linear_logprob_entropy_forward(hidden: torch.Tensor, weight: torch.Ten
     if not (T > 0.0 and T != float("inf")):
         raise RuntimeError(f"temperature must be finite and > 0, got {T}")
     if impl == "chunked":
-        _forward_chunked(h2, weight, t, T, vocab_chunk(N, V, h2.element_size(), chunk_vocab), out)
+        _forward_chunked(h2, weight, t, T, vocab_chunks(N, V, h2.element_size(), chunk_vocab),
+                         out)
         return tuple(out)
     dev = hidden.device
     with device_guard(dev.index):

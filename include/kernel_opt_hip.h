@@ -218,6 +218,30 @@ int klp_fwd_shard_merge(const float* states, int64_t n_shards, int64_t n_rows,
                         float* logprob, float* entropy, float* lse, void* stream);
 
 /*
+ * Vocabulary chunks on one GPU (the chunked LM head: the logits of one chunk
+ * of columns exist at a time).  No counterpart in the reference, whose
+ * Liger-style fused LM head is a stated follow-up it does not build
+ * (docs/FINAL_REPORT.md:439-450).  Call it once per chunk, in chunk order on
+ * one stream, with chunk `chunk_index` of `n_chunks` holding columns
+ * [vocab_offset, vocab_offset + vocab) of the full vocabulary (chunks may
+ * have any widths):
+ *   chunk_index < n_chunks - 1: writes the rows' states to
+ *     states[chunk_index] ([n_chunks][n_rows][4] float32, 16-byte aligned),
+ *     as klp_fwd_shard does; the outputs are not read.
+ *   chunk_index == n_chunks - 1: merges states[0 .. n_chunks - 2] (written
+ *     by the earlier calls) in chunk order with its own chunk's and writes
+ *     logprob, entropy and lse as klp_fwd; states[n_chunks - 1] is not used.
+ * The outputs equal klp_fwd_shard on every chunk followed by
+ * klp_fwd_shard_merge, bit for bit, in one launch fewer and without that
+ * function's equal-width rule.
+ */
+int klp_fwd_chunk(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                  int64_t rows_inner, int64_t stride_outer, int64_t stride_inner,
+                  const int64_t* targets, int64_t vocab_offset, float temperature,
+                  float* states, int64_t chunk_index, int64_t n_chunks,
+                  float* logprob, float* entropy, float* lse, void* stream);
+
+/*
  * GRPO policy loss over per-token log-probabilities.  The reference plans it
  * as kernel "K2 fused_grpo_loss" (notes/PLAN.md:59) but ships it only as
  * eager PyTorch (examples/compare_one_step.py:232-236, the clipped surrogate

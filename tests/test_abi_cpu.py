@@ -372,6 +372,40 @@ def test_shard_validation_errors():
         lib.klp_debug_fail_next_launches(0)
 
 
+def test_chunk_validation_errors():
+    """klp_fwd_chunk rejects bad arguments before any launch: the chunk index
+    must lie in [0, n_chunks), the states must be 16-byte aligned, and only
+    the last chunk (which writes them) checks the outputs."""
+    from kernel_opt._library import KLP_EDTYPE, KLP_EINVAL, KLP_ELAUNCH, lib
+    A = ctypes.c_void_p(0x100000)
+
+    def chunk(**kw):
+        a = dict(x=A, dtype=0, n=8, v=1000, ri=8, so=0, si=1000, t=A, off=0, temp=1.0, st=A,
+                 c=0, nc=3, lp=A, ent=A, lse=A)
+        a.update(kw)
+        return lib.klp_fwd_chunk(a["x"], a["dtype"], a["n"], a["v"], a["ri"], a["so"], a["si"],
+                                 a["t"], a["off"], a["temp"], a["st"], a["c"], a["nc"], a["lp"],
+                                 a["ent"], a["lse"], None)
+    assert chunk(n=0) == 0
+    assert chunk(dtype=7) == KLP_EDTYPE
+    assert chunk(temp=0.0) == KLP_EINVAL and "temperature" in _err()
+    assert chunk(off=-1) == KLP_EINVAL and "vocab_offset" in _err()
+    assert chunk(c=3) == KLP_EINVAL and "chunk_index" in _err()
+    assert chunk(c=-1) == KLP_EINVAL and "chunk_index" in _err()
+    assert chunk(nc=0) == KLP_EINVAL and "chunk_index" in _err()
+    assert chunk(st=None) == KLP_EINVAL and "states" in _err()
+    assert chunk(st=ctypes.c_void_p(0x100008)) == KLP_EINVAL and "states" in _err()
+    assert chunk(c=2, lse=None) == KLP_EINVAL and "lse" in _err()
+    assert chunk(c=2, lp=ctypes.c_void_p(0x100002)) == KLP_EINVAL and "logprob" in _err()
+    lib.klp_debug_fail_next_launches(2)
+    try:
+        # an earlier chunk does not read the outputs
+        assert chunk(c=0, lse=None) == KLP_ELAUNCH and "chunk forward" in _err()
+        assert chunk(c=2) == KLP_ELAUNCH and "chunk forward" in _err()
+    finally:
+        lib.klp_debug_fail_next_launches(0)
+
+
 def test_scale_inplace_validation_errors():
     """klp_scale_inplace rejects bad arguments before any launch; n = 0 is a
     no-op; an injected launch failure is reported."""

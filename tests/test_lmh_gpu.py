@@ -251,15 +251,18 @@ def test_backward_matches_unfused_path(impl):
 SIG_BITS = {torch.bfloat16: 8, torch.float16: 11, torch.float32: 24}
 
 
-def _chunk_logits(hd, wd, vc):
-    """The logits the chunked head computes: the same GEMM call per chunk
-    (deterministic, so bit-identical to the head's own), concatenated."""
+def _chunk_logits(hd, wd, plan):
+    """The logits the chunked head computes: the same GEMM call per chunk of
+    ``plan`` (a vocab_chunks list, or a width for equal chunks; the GEMM is
+    deterministic, so the values are bit-identical to the head's own),
+    concatenated."""
     from kernel_opt import lmhead
     h2 = hd.reshape(-1, hd.size(-1))
     N, V = h2.size(0), wd.size(0)
+    if isinstance(plan, int):
+        plan = [(c0, min(plan, V - c0)) for c0 in range(0, V, plan)]
     parts = []
-    for c0 in range(0, V, vc):
-        n = min(vc, V - c0)
+    for c0, n in plan:
         buf = torch.empty(N * n, dtype=hd.dtype, device=DEV)
         parts.append(lmhead._chunk_logits(buf, h2, wd, c0, n).clone())
     return torch.cat(parts, dim=1)
@@ -282,15 +285,14 @@ CHUNK_CASES = [  # N, V, D, dtype, chunk_vocab, temperature
 
 @pytest.mark.parametrize("N,V,D,dtype,chunk,T", CHUNK_CASES)
 def test_chunked_forward(N, V, D, dtype, chunk, T, oracle):
-    from kernel_opt import fused_linear_logprob_entropy_forward, vocab_chunk
+    from kernel_opt import fused_linear_logprob_entropy_forward, vocab_chunks
     from klp_testutil import FWD_TOL
     h, w, t = make(N, V, D, seed=40 + N + V, dtype=dtype)
     t[::7] = -100
     t[3::11] = V
     hd, wd, td = h.to(DEV), w.to(DEV), t.to(DEV)
     lp, ent, lse = fused_linear_logprob_entropy_forward(hd, wd, td, T, chunk_vocab=chunk)
-    vc = vocab_chunk(N, V, h.element_size(), chunk)
-    x = _chunk_logits(hd, wd, vc)
+    x = _chunk_logits(hd, wd, vocab_chunks(N, V, h.element_size(), chunk))
     # (1) the logprob bar on the logits the chunks computed
     ref = oracle.forward(x.cpu(), t.numpy(), temperature=T)
     for name, o, r in zip(("logp", "entropy", "lse"), (lp, ent, lse), ref):
@@ -323,11 +325,11 @@ def test_chunked_forward(N, V, D, dtype, chunk, T, oracle):
 def test_chunked_headline_vocab_and_hidden(oracle):
     """Qwen2.5-7B's head (V = 152064, D = 3584), 300 tokens, default chunks:
     the logprob bar on the chunks' logits."""
-    from kernel_opt import fused_linear_logprob_entropy_forward, vocab_chunk
+    from kernel_opt import fused_linear_logprob_entropy_forward, vocab_chunks
     h, w, t = make(300, 152064, 3584, seed=7, spike=True)
     hd, wd, td = h.to(DEV), w.to(DEV), t.to(DEV)
     outs = fused_linear_logprob_entropy_forward(hd, wd, td)
-    x = _chunk_logits(hd, wd, vocab_chunk(300, 152064))
+    x = _chunk_logits(hd, wd, vocab_chunks(300, 152064))
     ref = oracle.forward(x.cpu(), t.numpy())
     for name, o, r in zip(("logp", "entropy", "lse"), outs, ref):
         err = np.abs(_f64(o) - r).max()
@@ -364,7 +366,7 @@ def test_chunked_backward(N, V, D, dtype, chunk, T, need_w, oracle):
     logits: d_logits within one rounding to the input dtype (plus the fp32
     evaluation noise of its row), carried through the two products, whose
     outputs are rounded once more and accumulate in fp32."""
-    from kernel_opt import fused_linear_logprob_entropy, vocab_chunk
+    from kernel_opt import fused_linear_logprob_entropy, vocab_chunks
     h, w, t = make(N, V, D, seed=60 + N, dtype=dtype)
     t[::9] = -100
     t[1::13] = V
@@ -374,7 +376,7 @@ def test_chunked_backward(N, V, D, dtype, chunk, T, need_w, oracle):
     td = t.to(DEV)
     lp, ent, lse = fused_linear_logprob_entropy(hd, wd, td, T, chunk_vocab=chunk)
     ((lp * gl.to(DEV)).sum() + (ent * ge.to(DEV)).sum() + (lse * gs.to(DEV)).sum()).backward()
-    x = _chunk_logits(hd.detach(), wd.detach(), vocab_chunk(N, V, h.element_size(), chunk))
+    x = _chunk_logits(hd.detach(), wd.detach(), vocab_chunks(N, V, h.element_size(), chunk))
     r_lp, r_h, r_l = oracle.forward(x.cpu(), t.numpy(), temperature=T)
     dl = oracle.backward(x.cpu(), t.numpy(), r_l, r_h, gl.double().numpy(), ge.double().numpy(),
                          gs.double().numpy(), temperature=T)
