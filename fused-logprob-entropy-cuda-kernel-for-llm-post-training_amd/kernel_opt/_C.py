@@ -19,6 +19,14 @@ messages (``csrc/fused_logprob.cu:294-311,362-374,412-424``).  Differences:
   upstream gradient), so callers need not materialise zero tensors.
 * Work runs on the current stream of ``logits``' device, with that device
   made current for the call.
+
+The three functions, and ``fwd_launch`` / ``bwd_launch`` without a pinned
+launch shape, are the compiled binding's (``binding/klp_torch.cpp``, loaded
+as ``_library.binding``): the checks, workspace and launch in C++, a few us
+of host time per call.  A pinned launch shape (the tuning ABI, for sweeps and
+tests) goes through ctypes, and so does every call while the current stream
+is being captured into a graph (the binding declines those with
+``binding.CaptureDeclined`` before it allocates or launches anything).
 """
 from __future__ import annotations
 
@@ -28,8 +36,8 @@ import threading
 
 import torch
 
-from ._library import (DTYPE_CODES, capturing, check_status, device_guard, keep_for_capture, lib,
-                       ptr, stream_handle)
+from ._library import (DTYPE_CODES, binding, capturing, check_status, device_guard,
+                       keep_for_capture, lib, ptr, stream_handle)
 
 __all__ = [
     "fused_logprob_entropy_naive",
@@ -172,6 +180,12 @@ def fwd_launch(logits, targets, logprob, entropy, lse_out, config=None, temperat
     splits, flags)`` pins a launch shape (tuning ABI); ``None`` lets the
     native dispatcher choose.  ``temperature`` T divides the logits (as
     x * fp32(1/T)) inside the kernel."""
+    if config is None:
+        try:
+            binding.fwd_launch(logits, targets, logprob, entropy, lse_out, temperature)
+            return
+        except binding.CaptureDeclined:
+            pass
     rows, N, V = _common_forward_checks(logits, targets, logprob, entropy, lse_out, False)
     temp = _temperature(temperature, config)
     if N == 0:
@@ -205,6 +219,11 @@ def fused_logprob_entropy_v1(logits, targets, logprob, entropy, lse_out) -> None
 
 def fused_logprob_entropy_naive(logits, targets, logprob, entropy, lse_out) -> None:
     """Naive forward, one thread per row (reference csrc/fused_logprob.cu:405-458)."""
+    try:
+        binding.fused_logprob_entropy_naive(logits, targets, logprob, entropy, lse_out)
+        return
+    except binding.CaptureDeclined:
+        pass
     rows, N, V = _common_forward_checks(logits, targets, logprob, entropy, lse_out, True)
     if N == 0:
         return
@@ -248,6 +267,13 @@ def bwd_launch(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits,
     """Backward into caller-allocated ``d_logits``; ``config`` and
     ``temperature`` as in fwd_launch (the gradient is with respect to the
     unscaled logits)."""
+    if config is None:
+        try:
+            binding.bwd_launch(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits,
+                               temperature)
+            return
+        except binding.CaptureDeclined:
+            pass
     rows, N, V = _backward_checks(logits, targets, lse, entropy, g_logp, g_ent, g_lse, d_logits)
     temp = _temperature(temperature, config)
     if N == 0:

@@ -1,8 +1,12 @@
-"""Loader for the HIP shared library ``_lib/libkernel_opt_hip.so``.
+"""Loader for the HIP shared library ``_lib/libkernel_opt_hip.so`` and its
+compiled torch binding ``_lib/klp_torch*.so``.
 
-The library is built in-tree by ``__graft_entry__.build()`` (hipcc,
-``--offload-arch=gfx950``).  There is no fallback: if the library is missing
-or does not load, importing :mod:`kernel_opt` raises ``ImportError``.
+Both are built in-tree by ``__graft_entry__.build()`` (hipcc,
+``--offload-arch=gfx950``; the binding by ``setup.py build_ext --inplace``).
+There is no fallback: if either is missing or does not load, importing
+:mod:`kernel_opt` raises ``ImportError``.  ``lib`` is the library through
+ctypes (every entry point of the public headers); ``binding`` is the compiled
+module that the logprob op's per-call path goes through.
 
 ``torch`` is imported first so that the library's ``libamdhip64.so.7``
 dependency resolves (by soname) to the HIP runtime torch already loaded; the
@@ -12,7 +16,10 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import glob
+import importlib.util
 import os
+import sysconfig
 
 import torch  # noqa: F401  (must precede the dlopen below, see module docstring)
 
@@ -101,6 +108,28 @@ def _load() -> ctypes.CDLL:
 
 
 lib = _load()
+
+
+def _load_binding():
+    path = os.path.join(os.path.dirname(LIB_PATH),
+                        "klp_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+    if not os.path.exists(path):
+        found = glob.glob(os.path.join(os.path.dirname(LIB_PATH), "klp_torch*.so"))
+        raise ImportError(
+            f"kernel_opt: the compiled binding {path} is not built"
+            + (f" (found {found[0]}, built for another Python)" if found else "")
+            + ". Build it with `python -c 'import __graft_entry__ as g; g.build()'` from "
+            "the repository root.")
+    spec = importlib.util.spec_from_file_location("kernel_opt._lib.klp_torch", path)
+    mod = importlib.util.module_from_spec(spec)
+    try:
+        spec.loader.exec_module(mod)
+    except ImportError as e:  # pragma: no cover - depends on the machine
+        raise ImportError(f"kernel_opt: cannot load {path}: {e}") from e
+    return mod
+
+
+binding = _load_binding()
 
 
 def last_error() -> str:

