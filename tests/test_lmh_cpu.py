@@ -94,3 +94,43 @@ def test_backward_matches_float64_autograd():
     loss.backward()
     np.testing.assert_allclose(dh, H.grad.numpy(), rtol=1e-10, atol=1e-12)
     np.testing.assert_allclose(dw, W.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_vocab_chunk_plan():
+    """The chunked head's vocabulary plan (host logic): chunks cover the
+    vocabulary in order without gaps; small batches take 32768-column chunks
+    with a remainder of at least 16384 + 1024 columns cut into 16384 + the
+    rest; larger batches take balanced chunks of a multiple of 1024 columns
+    within 128 MiB; an explicit width gives equal chunks and no cut."""
+    from kernel_opt import vocab_chunk, vocab_chunks
+
+    def check_cover(plan, V):
+        c = 0
+        for c0, n in plan:
+            assert c0 == c and n >= 1
+            c += n
+        assert c == V
+
+    qwen = vocab_chunks(1024, 152064)
+    check_cover(qwen, 152064)
+    assert [n for _, n in qwen] == [32768] * 4 + [16384, 4608]
+    assert [n for _, n in vocab_chunks(300, 152064)] == [32768] * 4 + [16384, 4608]
+    # a remainder below 16384 + 1024 stays whole; 16384 + 1024 is cut
+    assert [n for _, n in vocab_chunks(1024, 32768 + 17407)] == [32768, 17407]
+    assert [n for _, n in vocab_chunks(1024, 32768 + 17408)] == [32768, 16384, 1024]
+    assert [n for _, n in vocab_chunks(1024, 20000)] == [16384, 3616]
+    assert [n for _, n in vocab_chunks(1024, 32768)] == [32768]
+    assert [n for _, n in vocab_chunks(5, 300)] == [300]
+    # larger batches: balanced, whole multiples of 1024 but the last, <= 128 MiB
+    for N, V in ((2048, 152064), (8192, 152064), (4096, 151936), (32768, 262144)):
+        plan = vocab_chunks(N, V)
+        check_cover(plan, V)
+        widths = [n for _, n in plan]
+        assert all(w == widths[0] for w in widths[:-1]) and widths[-1] <= widths[0]
+        assert widths[0] % 1024 == 0 and N * widths[0] * 2 <= 128 << 20
+        assert widths[0] == vocab_chunk(N, V)
+    # an explicit width: equal chunks, the last the rest, never cut
+    assert [n for _, n in vocab_chunks(1024, 152064, chunk_vocab=20000)] == [20000] * 7 + [12064]
+    assert [n for _, n in vocab_chunks(1024, 100, chunk_vocab=1000)] == [100]
+    # fp32 halves the columns that fit the small-batch rule
+    assert vocab_chunk(1024, 152064, elem_bytes=4) != 32768
