@@ -70,7 +70,7 @@ def grad_score(oracle, x_cpu, t_cpu, lse_np, ent_np, d_ours, d_ref, gl=None, ge=
     (|x - lse| ulps of p) included.  Any fp32 evaluation of
     p * (g_lse - g_logp - g_ent (log p + H)) + [v == t] g_logp, the
     reference's own fp32 path included, carries errors of that size.  With a
-    temperature T, x is the scaled logit fp32(x * fp32(1/T)) and the noise
+    temperature T, x is the scaled logit fp32(x * s), s = fp32(1/fp32(T)), and the noise
     carries the chain-rule factor 1/T.
     Returns (worst score, detail string); a score <= 1 passes."""
     V = x_cpu.shape[-1]
@@ -78,8 +78,8 @@ def grad_score(oracle, x_cpu, t_cpu, lse_np, ent_np, d_ours, d_ref, gl=None, ge=
     t_np = t_cpu.numpy().reshape(-1)
     x64 = x_cpu.detach().cpu().float().numpy().reshape(n, V)
     scale = 1.0
-    if temperature is not None:  # the kernels' scaled logit fp32(x * fp32(1/T))
-        scale = float(np.float32(1.0 / float(temperature)))
+    if temperature is not None:  # the kernels' scaled logit fp32(x * s)
+        scale = oracle.scale_of(temperature)
         x64 = x64 * np.float32(scale)
     x64 = x64.astype(np.float64)
     lp = x64 - lse_np[:, None]

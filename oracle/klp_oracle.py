@@ -102,7 +102,7 @@ class Oracle:
     # -- API ---------------------------------------------------------------
     def forward(self, logits, targets, dtype=None, naive: bool = False, temperature=None):
         """(logp, entropy, lse) float64 for dense [..., V] logits; with a
-        temperature T the logits are first multiplied by fp32(1/T) in fp32."""
+        temperature T the logits are first multiplied by scale_of(T) in fp32."""
         arr, code = self._as_storage(logits, dtype)
         V = arr.shape[-1]
         n = arr.size // V
@@ -122,10 +122,13 @@ class Oracle:
 
     @staticmethod
     def scale_of(temperature):
-        """fp32(1/T), as the kernels compute it (1.0 for None)."""
+        """The kernels' scale (1.0 for None): the temperature crosses the C ABI
+        as a float T32 = fp32(T), and the kernels multiply each logit by the
+        float nearest 1/T32.  For some T (1.7, for one) fp32(1/T) is one ulp
+        away from it."""
         if temperature is None:
             return 1.0
-        return float(np.float32(1.0 / float(temperature)))
+        return float(np.float32(1.0 / float(np.float32(temperature))))
 
     def backward(self, logits, targets, lse, ent, g_logp=None, g_ent=None, g_lse=None,
                  dtype=None, temperature=None):

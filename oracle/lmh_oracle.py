@@ -29,9 +29,11 @@ def bf16_to_f64(bits: np.ndarray) -> np.ndarray:
 
 
 def scale_of(temperature):
+    """The float nearest 1/fp32(T): the temperature crosses the C ABI as a
+    float (1.0 for None)."""
     if temperature is None:
         return 1.0
-    return float(np.float32(1.0 / float(temperature)))
+    return float(np.float32(1.0 / float(np.float32(temperature))))
 
 
 def logits(hidden_bits, weight_bits, temperature=None):

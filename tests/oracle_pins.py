@@ -376,13 +376,14 @@ def pin_down_conversions(o):
 
 
 def _scaled(x32, T):
-    """numpy's own fp32 product x * fp32(1/T), as float64."""
-    s = np.float32(1.0 / T)
+    """numpy's own fp32 product x * s, as float64, where s is the float
+    nearest 1/fp32(T) (the temperature crosses the C ABI as a float)."""
+    s = np.float32(1.0 / float(np.float32(T)))
     return (x32.astype(np.float32) * s).astype(np.float64), float(s)
 
 
 def pin_temperature_forward(o):
-    """Temperature T: brute force on the logits scaled by fp32(1/T) in numpy;
+    """Temperature T: brute force on the logits scaled by fp32(1/fp32(T)) in numpy;
     T = 1 is exactly the plain forward."""
     x, t = _case("randn", 2001, n=4, k=50)
     for T in (0.7, 1.3, 2.0):
