@@ -63,6 +63,8 @@ constexpr int64_t kFwdOneRoundWaves = 8192;
 constexpr int64_t kBwdLargeGrid = 65536;
 constexpr int64_t kBwdSmallGrid = 16384;
 constexpr int kMaxSplits = 64;
+// fp32 backward rows of 4-wave workgroups (C5: 128 pieces of one iteration).
+constexpr int kMaxSplitsFp32 = 256;
 
 // Shared checks of the row-addressed logits operand.
 int check_rows(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t rows_inner,
@@ -229,6 +231,15 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
         2 * s <= kMaxSplits) {
         c.waves = 8;
         s *= 2;
+        // fp32 rows halve again: 4-wave workgroups over twice the pieces.
+        // C5 2742-2769 us against 2837-2839 (two boxes), [32768, 32000] 1280
+        // against 1302, [8192, 32000] 322 against 326, [2048, 262144] 689
+        // against 698, C1 10.1 against 10.4 back to back; [4096, 152064] and
+        // [64, 32000] equal, [256, 152064] 46.1 against 45.6.
+        if (dtype == KLP_FP32 && 2 * s <= kMaxSplitsFp32) {
+            c.waves = 4;
+            s *= 2;
+        }
     }
     // Rows of more than 2 GiB per 64 pieces (never a real vocabulary) take
     // more pieces.

@@ -155,14 +155,14 @@ def test_default_launch_shapes():
     assert lib.klp_fwd_workspace_bytes(0, 16, 152064) == 16 * s * 16 + 64
     # backward splits rows freely (no second pass)
     assert _C.default_config("bwd", torch.bfloat16, 1024, 152064)[2] >= 2
-    # small grids: 8-wave workgroups over twice the pieces (C1, C2); larger
-    # grids 16 waves (C3, C4)
+    # small bf16 / fp16 grids: 8-wave workgroups over twice the pieces (C2);
+    # larger grids 16 waves (C3, C4); fp32 rows 4 waves over four times (C1)
     assert _C.default_config("bwd", torch.bfloat16, 1024, 152064)[:3] == (8, 2, 16)
-    assert _C.default_config("bwd", torch.float32, 256, 32000)[:3] == (8, 2, 8)
+    assert _C.default_config("bwd", torch.float32, 256, 32000)[:3] == (4, 2, 16)
     assert _C.default_config("bwd", torch.float16, 8192, 128256)[:3] == (16, 2, 8)
     assert _C.default_config("bwd", torch.bfloat16, 32768, 151936)[:3] == (16, 2, 10)
-    # fp32 rows: 8 waves as well (C5)
-    assert _C.default_config("bwd", torch.float32, 8192, 262144)[:3] == (8, 2, 64)
+    # fp32 rows: 4 waves at every grid size (C5)
+    assert _C.default_config("bwd", torch.float32, 8192, 262144)[:3] == (4, 2, 128)
 
 
 def test_shim_rejects_cpu_tensors_with_reference_messages():
