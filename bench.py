@@ -507,19 +507,26 @@ def grpo_timing(dev, K, B=16, S=2048):
     for name, fn in (("fused", fused), ("eager", eager)):
         for _ in range(5):
             fn()
-        torch.cuda.synchronize()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(K):
-            fn()
-        b.record()
-        torch.cuda.synchronize()
-        res[name] = a.elapsed_time(b) / K * 1e3
+        for queued in (False, True):
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            if queued:  # long enough to hold K host-issued calls of ~100 us
+                torch.cuda._sleep(max(Timer.QUEUE_SPIN_CYCLES, K * 250_000))
+            a.record()
+            for _ in range(K):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            res[name + ("_queued" if queued else "")] = a.elapsed_time(b) / K * 1e3
     return {"shape": [B, S], "loss_type": "grpo", "beta": 0.04,
             "fused_fwd_bwd_us": round(res["fused"], 2),
             "eager_fwd_bwd_us": round(res["eager"], 2),
-            "note": "loss + loss.backward() per iteration, end to end from Python"}
+            "fused_fwd_bwd_us_queued": round(res["fused_queued"], 2),
+            "eager_fwd_bwd_us_queued": round(res["eager_queued"], 2),
+            "note": "loss + loss.backward() per iteration, end to end from Python (the "
+                    "fused loss through the compiled binding); *_queued: the same calls "
+                    "behind a spin kernel, i.e. GPU time without the host's latency"}
 
 
 def grpo_step_timing(dev, K, logits, targets):

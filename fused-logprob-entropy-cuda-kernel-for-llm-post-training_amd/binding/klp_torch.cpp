@@ -414,6 +414,134 @@ std::vector<at::Tensor> fused_logprob_entropy_naive(const at::Tensor& logits,
     return {out[0], out[1], out[2]};
 }
 
+// ---------------------------------------------------------------------------
+// GRPO loss over per-token log-probabilities: kernel_opt.grpo's autograd op
+// (the loss the reference writes in eager PyTorch at
+// examples/compare_one_step.py:232-236; klp_grpo_fwd / klp_grpo_bwd).  The
+// argument handling restates grpo._f32 and grpo.fused_grpo_loss with the same
+// messages; loss-type strings are resolved in Python.
+// ---------------------------------------------------------------------------
+std::string tuple_str(at::IntArrayRef s) {
+    std::string r = "(";
+    for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
+    return r + (s.size() == 1 ? ",)" : ")");
+}
+
+// A constant operand: on logp's device, float32, of the given shape,
+// contiguous; undefined when absent.
+at::Tensor grpo_operand(const std::optional<at::Tensor>& t, const char* name,
+                        at::IntArrayRef shape, const at::Device& dev) {
+    if (!t.has_value() || !t->defined()) return at::Tensor();
+    if (t->device() != dev) throw std::runtime_error(std::string(name) + " must be on " + dev.str());
+    at::Tensor f = t->detach().to(at::kFloat);
+    if (f.sizes() != shape)
+        throw std::runtime_error(std::string(name) + " has shape " + tuple_str(f.sizes()) +
+                                 ", expected " + tuple_str(shape));
+    return f.contiguous();
+}
+
+struct GrpoArgs {
+    double eps_low, eps_high, beta, norm;
+    int64_t kind, level, per_token;
+};
+
+class FusedGrpoLoss : public torch::autograd::Function<FusedGrpoLoss> {
+   public:
+    static variable_list forward(AutogradContext* ctx, const at::Tensor& logp, const at::Tensor& old,
+                                 const std::optional<at::Tensor>& ref, const at::Tensor& adv,
+                                 const std::optional<at::Tensor>& mask, double eps_low,
+                                 double eps_high, double beta, double norm, int64_t kind,
+                                 int64_t level, int64_t per_token) {
+        const int64_t B = logp.size(0), S = logp.size(1);
+        const at::Tensor lp = logp.contiguous();
+        const at::Tensor r = ref.value_or(at::Tensor()), m = mask.value_or(at::Tensor());
+        const auto f32 = at::TensorOptions().dtype(at::kFloat).device(logp.device());
+        at::Tensor ws = at::empty({static_cast<int64_t>(klp_grpo_workspace_bytes(B))},
+                                  f32.dtype(at::kByte));
+        at::Tensor loss = at::empty({}, f32);
+        at::Tensor stats = at::empty({4}, f32);
+        const int dev = logp.get_device();
+        const c10::hip::HIPGuard guard(static_cast<c10::DeviceIndex>(dev));
+        hipStream_t stream =
+            c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev)).stream();
+        check_status(klp_grpo_fwd(fptr(lp), fptr(old), fptr(r), fptr(adv), fptr(m), B, S,
+                                  static_cast<float>(eps_low), static_cast<float>(eps_high),
+                                  static_cast<float>(beta), static_cast<float>(norm),
+                                  static_cast<int>(kind), static_cast<int>(level),
+                                  static_cast<int>(per_token), out_ptr(loss), out_ptr(stats),
+                                  ws.data_ptr(), static_cast<size_t>(ws.numel()), stream));
+        ctx->save_for_backward({lp, old, r, adv, m, ws});
+        ctx->saved_data["args"] = c10::List<double>({eps_low, eps_high, beta, norm,
+                                                     static_cast<double>(kind),
+                                                     static_cast<double>(level),
+                                                     static_cast<double>(per_token)});
+        ctx->mark_non_differentiable({stats});
+        ctx->set_materialize_grads(false);
+        return {loss, stats};
+    }
+
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        variable_list none(12);
+        if (!grads[0].defined() || !ctx->needs_input_grad(0)) return none;
+        const auto saved = ctx->get_saved_variables();
+        const at::Tensor &lp = saved[0], &old = saved[1], &ref = saved[2], &adv = saved[3],
+                         &mask = saved[4], &ws = saved[5];
+        const auto a = ctx->saved_data["args"].toDoubleList();
+        const int dev = lp.get_device();
+        hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(
+                c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev)).stream(),
+                &status) != hipSuccess ||
+            status != hipStreamCaptureStatusNone)
+            throw std::runtime_error(
+                "kernel_opt: this backward belongs to a forward run outside graph capture and "
+                "cannot itself be captured; capture the forward with it");
+        const at::Tensor g = grads[0].detach().to(at::kFloat).reshape({1}).contiguous();
+        at::Tensor d = at::empty_like(lp);
+        const c10::hip::HIPGuard guard(static_cast<c10::DeviceIndex>(dev));
+        hipStream_t stream =
+            c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev)).stream();
+        check_status(klp_grpo_bwd(fptr(lp), fptr(old), fptr(ref), fptr(adv), fptr(mask),
+                                  lp.size(0), lp.size(1), static_cast<float>(a[0]),
+                                  static_cast<float>(a[1]), static_cast<float>(a[2]),
+                                  static_cast<float>(a[3]), static_cast<int>(a[4]),
+                                  static_cast<int>(a[5]), static_cast<int>(a[6]), fptr(g),
+                                  out_ptr(d), ws.data_ptr(), static_cast<size_t>(ws.numel()),
+                                  stream));
+        none[0] = d;
+        return none;
+    }
+};
+
+// grpo.fused_grpo_loss after its loss-type resolution (grpo._config).
+std::vector<at::Tensor> fused_grpo_loss(const at::Tensor& logp, const std::optional<at::Tensor>& old,
+                                        const at::Tensor& advantages,
+                                        const std::optional<at::Tensor>& mask,
+                                        const std::optional<at::Tensor>& ref, double eps_low,
+                                        double eps_high, double beta, double norm, int64_t kind,
+                                        int64_t level) {
+    if (logp.dim() != 2)
+        throw std::runtime_error("logp must be [B, S], got shape " + tuple_str(logp.sizes()));
+    if (!logp.is_cuda()) throw std::runtime_error("logp must be a GPU tensor");
+    if (logp.scalar_type() != at::kFloat) throw std::runtime_error("logp must be float32");
+    decline_under_capture(logp.get_device());
+    const int64_t B = logp.size(0), S = logp.size(1);
+    const at::Device dev = logp.device();
+    const at::Tensor o = grpo_operand(old, "old_logp", {B, S}, dev);
+    const bool per_token = advantages.dim() != 1;
+    const at::Tensor adv = per_token ? grpo_operand(advantages, "advantages", {B, S}, dev)
+                                     : grpo_operand(advantages, "advantages", {B}, dev);
+    const at::Tensor m = grpo_operand(mask, "mask", {B, S}, dev);
+    const at::Tensor r = beta != 0.0 ? grpo_operand(ref, "ref_logp", {B, S}, dev) : at::Tensor();
+    if (B == 0 || S == 0)  // no tokens: every normaliser sees an empty (zero) masked sum
+        return {logp.sum() * 0.0, at::zeros({4}, logp.options())};
+    auto out = FusedGrpoLoss::apply(logp, o, r.defined() ? std::optional<at::Tensor>(r) : std::nullopt,
+                                    adv, m.defined() ? std::optional<at::Tensor>(m) : std::nullopt,
+                                    eps_low, eps_high, beta, norm, kind, level,
+                                    static_cast<int64_t>(per_token));
+    return {out[0], out[1]};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(klp_torch, m) {
@@ -477,6 +605,11 @@ PYBIND11_MODULE(klp_torch, m) {
           pybind11::arg("temperature") = pybind11::none());
     m.def("fused_logprob_entropy_naive_op", &fused_logprob_entropy_naive, pybind11::arg("logits"),
           pybind11::arg("targets"));
+    // kernel_opt.grpo (the GRPO loss of per-token log-probabilities)
+    m.def("fused_grpo_loss", &fused_grpo_loss, pybind11::arg("logp"), pybind11::arg("old_logp"),
+          pybind11::arg("advantages"), pybind11::arg("mask"), pybind11::arg("ref_logp"),
+          pybind11::arg("eps_low"), pybind11::arg("eps_high"), pybind11::arg("beta"),
+          pybind11::arg("norm"), pybind11::arg("kind"), pybind11::arg("level"));
     m.def(
         "workspaces_cached",
         []() {

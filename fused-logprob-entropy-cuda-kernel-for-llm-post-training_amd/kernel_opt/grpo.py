@@ -29,8 +29,8 @@ from __future__ import annotations
 import torch
 
 from ._library import (KLP_GRPO_LOSS_BNPO, KLP_GRPO_LOSS_FIXED, KLP_GRPO_LOSS_GRPO,
-                       KLP_GRPO_SEQUENCE, KLP_GRPO_TOKEN, check_status, device_guard, lib, ptr,
-                       stream_handle)
+                       KLP_GRPO_SEQUENCE, KLP_GRPO_TOKEN, binding, check_status, device_guard,
+                       lib, ptr, stream_handle)
 
 __all__ = ["fused_grpo_loss"]
 
@@ -141,6 +141,22 @@ def fused_grpo_loss(logp: torch.Tensor, old_logp: torch.Tensor, advantages: torc
     """
     if logp.dim() != 2:
         raise RuntimeError(f"logp must be [B, S], got shape {tuple(logp.shape)}")
+    kind, level, norm = _config(logp.size(0), logp.size(1), loss_type, importance_level,
+                                max_completion_length, normalizer)
+    eh = eps_low if eps_high is None else eps_high
+    for name, t in (("old_logp", old_logp), ("advantages", advantages), ("mask", mask),
+                    ("ref_logp", ref_logp)):
+        if t is not None and not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a tensor")
+    # The compiled binding runs the checks, conversions and launches below in
+    # C++ (binding/klp_torch.cpp); under graph capture it declines and this
+    # Python statement of them runs.
+    try:
+        return tuple(binding.fused_grpo_loss(logp, old_logp, advantages, mask, ref_logp,
+                                             float(eps_low), float(eh), float(beta), norm, kind,
+                                             level))
+    except binding.CaptureDeclined:
+        pass
     if not logp.is_cuda:
         raise RuntimeError("logp must be a GPU tensor")
     if logp.dtype != torch.float32:
@@ -154,11 +170,8 @@ def fused_grpo_loss(logp: torch.Tensor, old_logp: torch.Tensor, advantages: torc
         adv, per_token = _f32(advantages, "advantages", (B, S), dev), 1
     m = _f32(mask, "mask", (B, S), dev)
     ref = _f32(ref_logp, "ref_logp", (B, S), dev) if beta != 0.0 else None
-    kind, level, norm = _config(B, S, loss_type, importance_level, max_completion_length,
-                                normalizer)
     if B == 0 or S == 0:
         # No tokens: every normaliser sees an empty (zero) masked sum.
         return logp.sum() * 0.0, torch.zeros(4, dtype=torch.float32, device=dev)
-    eh = eps_low if eps_high is None else eps_high
     params = (float(eps_low), float(eh), float(beta), norm, kind, level, per_token)
     return _FusedGrpoLoss.apply(logp, old, ref, adv, m, params)

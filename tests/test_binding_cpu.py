@@ -19,7 +19,8 @@ def test_exports():
     for name in ("fused_logprob_entropy_v1", "fused_logprob_entropy_naive",
                  "fused_logprob_entropy_v1_backward", "fwd_launch", "bwd_launch",
                  "fused_logprob_entropy", "fused_logprob_entropy_forward",
-                 "fused_logprob_entropy_naive_op", "row_layout", "workspaces_cached"):
+                 "fused_logprob_entropy_naive_op", "row_layout", "workspaces_cached",
+                 "fused_grpo_loss"):
         assert callable(getattr(b, name)), name
     assert issubclass(b.InputAssertionError, AssertionError)
 
@@ -64,3 +65,25 @@ def test_c_entry_points_raise_reference_messages():
         b.fused_logprob_entropy_v1_backward(x, t, o[0], o[1], None, None, None, x)
     with pytest.raises(RuntimeError, match="logits must be contiguous CUDA"):
         b.bwd_launch(x, t, o[0], o[1], None, None, None, x, None)
+
+
+def test_grpo_loss_errors_before_the_gpu():
+    """The GRPO loss through the binding raises what grpo.py's Python
+    statement raises, for the checks that need no GPU."""
+    from kernel_opt import fused_grpo_loss
+    b = _binding()
+    lp = torch.zeros(2, 3)
+    adv = torch.zeros(2)
+    args = (1.0, 0.2, 0.2, 0.0, 1.0, 0, 0)
+    with pytest.raises(RuntimeError, match=r"logp must be \[B, S\], got shape \(6,\)"):
+        b.fused_grpo_loss(lp.reshape(-1), lp, adv, None, None, *args[1:5], 0, 0)
+    with pytest.raises(RuntimeError, match="logp must be a GPU tensor"):
+        b.fused_grpo_loss(lp, lp, adv, None, None, *args[1:5], 0, 0)
+    with pytest.raises(RuntimeError, match="logp must be a GPU tensor"):
+        fused_grpo_loss(lp, lp, adv)
+    with pytest.raises(RuntimeError, match=r"logp must be \[B, S\]"):
+        fused_grpo_loss(lp.reshape(-1), lp, adv)
+    with pytest.raises(TypeError, match="mask must be a tensor"):
+        fused_grpo_loss(lp, lp, adv, mask=[1, 0])
+    with pytest.raises(ValueError, match="loss_type"):
+        fused_grpo_loss(lp, lp, adv, loss_type="nope")

@@ -170,3 +170,71 @@ def test_errors_on_gpu_tensors():
         fused_logprob_entropy(x, t, -1.0)
     with pytest.raises(RuntimeError, match="outputs must be float32"):
         _C.fused_logprob_entropy_v1(x, t, lse.half(), lse, lse)
+
+
+class _PythonPathOnly:
+    """Stands in for the binding so that kernel_opt.grpo runs its Python
+    statement of the GRPO loss (the path graph capture takes)."""
+
+    class CaptureDeclined(Exception):
+        pass
+
+    @staticmethod
+    def fused_grpo_loss(*args, **kwargs):
+        raise _PythonPathOnly.CaptureDeclined()
+
+
+GRPO_CASES = [  # loss_type, importance level, beta, per-token advantages, mask, loss scale
+    ("bnpo", "token", 0.0, False, "float", 1.0),
+    ("grpo", "token", 0.04, True, "bool", 1.0),
+    ("dr_grpo", "sequence", 0.04, False, None, 2.5),
+    ("dapo", "token", 0.0, True, "int", -0.5),
+    ("grpo", "sequence", 0.0, True, "bool", 1.0),
+]
+
+
+@pytest.mark.parametrize("loss_type,level,beta,per_token,mask_kind,scale", GRPO_CASES)
+def test_compiled_grpo_loss_equals_python_function(monkeypatch, loss_type, level, beta, per_token,
+                                                   mask_kind, scale):
+    """fused_grpo_loss through the binding's C++ autograd op and through
+    grpo.py's Python autograd.Function: loss, stats and d_logp bit for bit."""
+    from kernel_opt import fused_grpo_loss, grpo
+    B, S = 6, 37
+    g = torch.Generator().manual_seed(B * S + len(loss_type))
+    lp0 = (-torch.rand(B, S, generator=g) * 3).to(DEV)
+    old = (lp0.cpu() + torch.randn(B, S, generator=g) * 0.1).to(DEV)
+    ref = (lp0.cpu() + torch.randn(B, S, generator=g) * 0.2).to(DEV)
+    adv = torch.randn((B, S) if per_token else (B,), generator=g).to(DEV)
+    m = torch.rand(B, S, generator=g) < 0.8
+    mask = None if mask_kind is None else {"float": m.float(), "bool": m,
+                                           "int": m.to(torch.int32)}[mask_kind].to(DEV)
+    kw = dict(beta=beta, loss_type=loss_type, importance_level=level, eps_high=0.28,
+              max_completion_length=48 if loss_type == "dr_grpo" else None,
+              normalizer=123.0 if loss_type == "dapo" else None)
+    results = []
+    for python_path in (False, True):
+        if python_path:
+            monkeypatch.setattr(grpo, "binding", _PythonPathOnly)
+        lp = lp0.clone().requires_grad_(True)
+        loss, stats = fused_grpo_loss(lp, old, adv, mask, ref, **kw)
+        (loss * scale).backward()
+        results.append((loss.detach(), stats, lp.grad, type(loss.grad_fn).__name__))
+    (l1, s1, d1, n1), (l2, s2, d2, n2) = results
+    assert torch.equal(l1, l2) and torch.equal(s1, s2) and torch.equal(d1, d2)
+    assert l1.dim() == 0 and l2.dim() == 0
+    assert n1 != n2, (n1, n2)
+
+
+def test_compiled_grpo_loss_edges():
+    from kernel_opt import fused_grpo_loss
+    lp = torch.zeros(0, 5, device=DEV, requires_grad=True)
+    loss, stats = fused_grpo_loss(lp, lp.detach(), torch.zeros(0, device=DEV))
+    loss.backward()
+    assert loss.item() == 0.0 and torch.equal(stats, torch.zeros(4, device=DEV))
+    x = torch.zeros(2, 3, device=DEV)
+    with pytest.raises(RuntimeError, match=r"old_logp has shape \(1, 3\), expected \(2, 3\)"):
+        fused_grpo_loss(x, x[:1], torch.zeros(2, device=DEV))
+    with pytest.raises(RuntimeError, match="advantages must be on cuda:0"):
+        fused_grpo_loss(x, x, torch.zeros(2))
+    with pytest.raises(RuntimeError, match="eps_low"):
+        fused_grpo_loss(x, x, torch.zeros(2, device=DEV), eps_low=-0.1)
