@@ -271,6 +271,32 @@ def test_every_launch_shape_matches_oracle(dtype, oracle):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+def test_backward_small_pieces_bitwise(dtype, oracle):
+    """Rows cut into many small backward pieces (4-wave workgroups over 64 to
+    256 pieces, the fp32 dispatcher's form; pieces past a row's end are empty)
+    write the same gradient bits as one piece a row, for rows that start off
+    a 16-byte boundary and a strided batch."""
+    from kernel_opt import _C
+    N, V = 6, 262147
+    base = seeded_logits((N + 1, V + 3), dtype, seed=77).to(DEV)
+    x = base[:N, 1:1 + V]                           # strided rows, misaligned start
+    t = seeded_targets((N,), V, seed=77).to(DEV)
+    t[0], t[1] = 0, V - 1
+    outs = [torch.empty(N, device=DEV) for _ in range(3)]
+    _C.fwd_launch(x, t, *outs)
+    g = torch.Generator().manual_seed(78)
+    gl, ge, gs = [(torch.randn(N, generator=g) * 0.5).to(DEV) for _ in range(3)]
+    ref = torch.empty(N, V, dtype=dtype, device=DEV)
+    _C.bwd_launch(x, t, outs[2], outs[1], gl, ge, gs, ref, config=(16, 2, 1, 1))
+    ulps, kind = _grad_ulps(oracle, x.cpu().contiguous(), t.cpu(), outs[2], outs[1], ref, gl, ge, gs)
+    assert ulps <= 1.0, f"{kind}: {ulps}"
+    for cfg in ((4, 2, 64, 1), (4, 2, 128, 1), (4, 2, 256, 1), (8, 2, 64, 1), (4, 4, 128, 0)):
+        d = torch.empty_like(ref)
+        _C.bwd_launch(x, t, outs[2], outs[1], gl, ge, gs, d, config=cfg)
+        assert np.array_equal(storage_bits(d), storage_bits(ref)), f"backward differs for {cfg}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("V", [1, 2, 3, 7, 8, 9, 15, 16, 17, 63, 64, 65, 1000, 4097])
 @pytest.mark.parametrize("offset", [0, 1, 3])
 def test_small_and_misaligned_rows(dtype, V, offset, oracle):
