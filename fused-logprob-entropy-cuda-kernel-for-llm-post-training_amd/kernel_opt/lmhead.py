@@ -27,12 +27,12 @@ size a multiple of 64.  Its backward recomputes chunks of logits with the
 same MFMA order (klp_lmh_bwd_logits on a slice of the weight) and runs the
 same two library GEMMs per chunk.  It is slower than the library GEMM at
 these shapes (measured at 1024 tokens of Qwen2.5-7B's head: forward 1.30 ms
-against 0.98 chunked and 0.93 unfused).
+against 0.91-0.92 chunked and 0.91-0.93 unfused).
 
 The backward of either head recomputes the logits, one GEMM more than the
 unfused path's backward: that is the price of not holding them (measured
-forward + backward at 1024 tokens: 4.82 ms chunked, 3.87 ms unfused, with
-67 MiB against 297 MiB beyond the inputs and gradients).  When the loss is
+forward + backward at 1024 tokens: 4.72 ms chunked, 3.87 ms unfused, with
+135 MiB against 297 MiB beyond the inputs and gradients).  When the loss is
 known in the forward, :func:`kernel_opt.fused_linear_grpo_step` computes the
 gradients there and needs no recompute.
 
