@@ -542,6 +542,153 @@ std::vector<at::Tensor> fused_grpo_loss(const at::Tensor& logp, const std::optio
     return {out[0], out[1]};
 }
 
+// ---------------------------------------------------------------------------
+// Fused GRPO step: kernel_opt.grpo_step's autograd op over klp_grpo_step
+// (logprob, entropy, the token's GRPO loss and d_logits in one read of the
+// logits).  Restates grpo_step.grpo_token_weights, grpo_step_launch and
+// _FusedGrpoStep; the Python wrapper keeps the argument checks, the choice
+// between this and the unfused composition, and the stats.
+// ---------------------------------------------------------------------------
+// klp_grpo_step's row counters, one per (device, stream): zeroed when
+// allocated (a fill kernel on that stream) and left zero by every launch, so
+// launches on one stream share one; the 16 most recently used are kept.
+struct Sched {
+    int device;
+    hipStream_t stream;
+    at::Tensor buf;
+};
+std::mutex g_sched_mutex;
+std::list<Sched>& g_sched = *new std::list<Sched>();  // never destroyed, as g_ws
+
+at::Tensor sched_counter(int device, hipStream_t stream) {
+    std::lock_guard<std::mutex> lock(g_sched_mutex);
+    for (auto it = g_sched.begin(); it != g_sched.end(); ++it) {
+        if (it->device != device || it->stream != stream) continue;
+        g_sched.splice(g_sched.begin(), g_sched, it);
+        return g_sched.front().buf;
+    }
+    const auto opts = at::TensorOptions().dtype(at::kLong).device(at::kCUDA, device);
+    g_sched.push_front(Sched{device, stream, at::zeros({KLP_GRPO_STEP_SCHED_BYTES / 8}, opts)});
+    while (g_sched.size() > kWorkspacesKept) g_sched.pop_back();
+    return g_sched.front().buf;
+}
+
+// grpo_step.grpo_token_weights on a float32 mask, the same torch operations
+// in the same order (so the same bits): kind 0 "grpo" (B * max(row sum, 1)),
+// 1 "bnpo" (max(mask sum, 1)), 2 a fixed normaliser whose float32 reciprocal
+// the caller passes as `scale` ("dr_grpo", "dapo").
+at::Tensor token_weights(const at::Tensor& m, int64_t kind, double scale) {
+    if (kind == 0) {
+        const at::Tensor den = m.sum({1}, true).clamp_min(1.0) * static_cast<double>(m.size(0));
+        return m * (den.reciprocal() * 1.0);
+    }
+    if (kind == 1) return m * (m.sum().clamp_min(1.0).reciprocal() * 1.0);
+    return m * scale;
+}
+
+// True when klp_grpo_step takes these rows (grpo_step._fused_supported).
+bool grpo_step_supported(const at::Tensor& logits, const std::optional<std::array<int64_t, 3>>& rows) {
+    const int code = dtype_code(logits.scalar_type());
+    if (!rows.has_value() || code < 0) return false;
+    const int64_t V = logits.size(-1), esz = logits.element_size();
+    if (V > klp_grpo_step_max_vocab(code)) return false;
+    const auto& L = *rows;
+    return (V * esz) % 16 == 0 && reinterpret_cast<uintptr_t>(logits.data_ptr()) % 16 == 0 &&
+           (L[2] * esz) % 16 == 0 && (L[1] * esz) % 16 == 0;
+}
+
+class FusedGrpoStep : public torch::autograd::Function<FusedGrpoStep> {
+   public:
+    static variable_list forward(AutogradContext* ctx, const at::Tensor& logits,
+                                 const at::Tensor& targets, const at::Tensor& old,
+                                 const std::optional<at::Tensor>& ref, const at::Tensor& adv,
+                                 const at::Tensor& weight, double temperature, double eps_low,
+                                 double eps_high, double beta, int64_t per_token) {
+        const int64_t B = logits.size(0), S = logits.size(1), V = logits.size(2);
+        const auto rows = row_layout(logits);
+        require(rows.has_value(), "logits must be contiguous");
+        const auto f32 = at::TensorOptions().dtype(at::kFloat).device(logits.device());
+        at::Tensor logp = at::empty({B, S}, f32), ent = at::empty({B, S}, f32),
+                   lse = at::empty({B, S}, f32), loss_tok = at::empty({B, S}, f32);
+        at::Tensor d_logits = at::empty({B, S, V}, logits.options());
+        const int dev = logits.get_device();
+        const c10::hip::HIPGuard guard(static_cast<c10::DeviceIndex>(dev));
+        hipStream_t stream =
+            c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev)).stream();
+        const at::Tensor sched = sched_counter(dev, stream);
+        const at::Tensor r = ref.value_or(at::Tensor());
+        const auto& L = *rows;
+        check_status(klp_grpo_step(
+            logits.data_ptr(), dtype_code(logits.scalar_type()), B * S, V, L[0], L[1], L[2],
+            targets.data_ptr<int64_t>(), static_cast<float>(temperature), fptr(old), fptr(r),
+            fptr(adv), fptr(weight), S, static_cast<float>(eps_low), static_cast<float>(eps_high),
+            static_cast<float>(beta), static_cast<int>(per_token), out_ptr(logp), out_ptr(ent),
+            out_ptr(lse), out_ptr(loss_tok), d_logits.data_ptr(), sched.data_ptr(), stream));
+        ctx->saved_data["d_logits"] = d_logits;
+        ctx->mark_non_differentiable({logp, ent});
+        return {loss_tok.sum(), logp, ent};
+    }
+
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        variable_list none(11);
+        c10::IValue& held = ctx->saved_data["d_logits"];
+        if (!held.isTensor())
+            throw std::runtime_error(
+                "fused_grpo_step: the backward can run only once per forward (retain_graph "
+                "replays are not supported)");
+        at::Tensor d = held.toTensor();
+        held = c10::IValue();
+        if (!grads[0].defined() || !ctx->needs_input_grad(0)) return none;
+        const int dev = d.get_device();
+        hipStream_t stream =
+            c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev)).stream();
+        hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &status) != hipSuccess ||
+            status != hipStreamCaptureStatusNone)
+            throw std::runtime_error(
+                "kernel_opt: this backward belongs to a forward run outside graph capture and "
+                "cannot itself be captured; capture the forward with it");
+        // d *= g on the device (grpo_step.scale_by_upstream): nothing is
+        // written when g is exactly 1.
+        const at::Tensor g = grads[0].detach().to(d.device(), at::kFloat).reshape({1}).contiguous();
+        const c10::hip::HIPGuard guard(static_cast<c10::DeviceIndex>(dev));
+        check_status(klp_scale_inplace(d.data_ptr(), dtype_code(d.scalar_type()), d.numel(),
+                                       fptr(g), stream));
+        none[0] = d;
+        return none;
+    }
+};
+
+// The fused path of grpo_step.fused_grpo_step after its argument checks:
+// (loss, logp, entropy), or nothing when klp_grpo_step does not take these
+// logits (the caller then runs the unfused composition).
+std::optional<std::vector<at::Tensor>> fused_grpo_step(
+    const at::Tensor& logits, const at::Tensor& targets, const at::Tensor& old_logp,
+    const at::Tensor& advantages, const std::optional<at::Tensor>& mask,
+    const std::optional<at::Tensor>& ref_logp, double temperature, double eps_low,
+    double eps_high, double beta, int64_t weight_kind, double weight_scale) {
+    require(logits.is_cuda() && logits.dim() == 3, "logits must be a [B, S, V] GPU tensor");
+    decline_under_capture(logits.get_device());
+    if (!grpo_step_supported(logits, row_layout(logits))) return std::nullopt;
+    const int64_t B = logits.size(0), S = logits.size(1);
+    const at::Device dev = logits.device();
+    const at::Tensor old = grpo_operand(old_logp, "old_logp", {B, S}, dev);
+    const bool per_token = advantages.dim() != 1;
+    const at::Tensor adv = per_token ? grpo_operand(advantages, "advantages", {B, S}, dev)
+                                     : grpo_operand(advantages, "advantages", {B}, dev);
+    at::Tensor m = grpo_operand(mask, "mask", {B, S}, dev);
+    if (!m.defined()) m = at::ones({B, S}, at::TensorOptions().dtype(at::kFloat).device(dev));
+    const at::Tensor ref = (beta != 0.0 && ref_logp.has_value() && ref_logp->defined())
+                               ? grpo_operand(ref_logp, "ref_logp", {B, S}, dev)
+                               : at::Tensor();
+    const at::Tensor weight = token_weights(m, weight_kind, weight_scale).contiguous();
+    auto out = FusedGrpoStep::apply(logits, targets, old,
+                                    ref.defined() ? std::optional<at::Tensor>(ref) : std::nullopt,
+                                    adv, weight, temperature, eps_low, eps_high, beta,
+                                    static_cast<int64_t>(per_token));
+    return std::vector<at::Tensor>{out[0], out[1], out[2]};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(klp_torch, m) {
@@ -610,6 +757,12 @@ PYBIND11_MODULE(klp_torch, m) {
           pybind11::arg("advantages"), pybind11::arg("mask"), pybind11::arg("ref_logp"),
           pybind11::arg("eps_low"), pybind11::arg("eps_high"), pybind11::arg("beta"),
           pybind11::arg("norm"), pybind11::arg("kind"), pybind11::arg("level"));
+    // kernel_opt.grpo_step (the fused GRPO step)
+    m.def("fused_grpo_step", &fused_grpo_step, pybind11::arg("logits"), pybind11::arg("targets"),
+          pybind11::arg("old_logp"), pybind11::arg("advantages"), pybind11::arg("mask"),
+          pybind11::arg("ref_logp"), pybind11::arg("temperature"), pybind11::arg("eps_low"),
+          pybind11::arg("eps_high"), pybind11::arg("beta"), pybind11::arg("weight_kind"),
+          pybind11::arg("weight_scale"));
     m.def(
         "workspaces_cached",
         []() {

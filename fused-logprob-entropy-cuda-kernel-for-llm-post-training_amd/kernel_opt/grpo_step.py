@@ -40,8 +40,8 @@ import numpy as np
 import torch
 
 from . import _C
-from ._library import (DTYPE_CODES, KLP_GRPO_STEP_SCHED_BYTES, capturing, check_status,
-                       device_guard, keep_for_capture, lib, ptr, stream_handle)
+from ._library import (DTYPE_CODES, KLP_GRPO_STEP_SCHED_BYTES, binding, capturing,
+                       check_status, device_guard, keep_for_capture, lib, ptr, stream_handle)
 from .grpo import fused_grpo_loss
 from .ops import fused_logprob_entropy
 
@@ -233,19 +233,62 @@ def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch
                    importance_level=importance_level,
                    max_completion_length=max_completion_length, normalizer=normalizer)
 
-    rows = _C.row_layout(logits)
     wants_grad = torch.is_grad_enabled() and logits.requires_grad
-    if (not wants_grad or importance_level != "token" or B * S == 0
-            or not targets.is_contiguous() or targets.dtype != torch.int64
-            or not _fused_supported(logits, rows)):
-        # The unfused composition: same loss, logp / entropy differentiable.
-        # It also serves calls that need no gradient (evaluation, logging,
-        # torch.no_grad()): the fused kernel would allocate and write a
-        # full [B, S, V] d_logits that nothing reads.
-        logp, ent, _ = fused_logprob_entropy(logits, targets, temperature)
-        loss, stats = fused_grpo_loss(logp, old_logp, advantages, mask, ref_logp, **loss_kw)
-        return (loss, logp, ent, stats) if return_stats else (loss, logp, ent)
+    if (wants_grad and importance_level == "token" and B * S > 0 and targets.is_contiguous()
+            and targets.dtype == torch.int64):
+        eh = eps_low if eps_high is None else eps_high
+        kind, scale = _weight_kind(B, S, loss_type, max_completion_length, normalizer)
+        # The compiled binding (binding/klp_torch.cpp) runs the conversions,
+        # the token weights and the autograd op below in C++; under graph
+        # capture it declines and this module's statement of them runs.
+        try:
+            out = binding.fused_grpo_step(logits, targets, old_logp, advantages, mask,
+                                          ref_logp, t, float(eps_low), float(eh), float(beta),
+                                          kind, scale)
+        except binding.CaptureDeclined:
+            out = _fused_python(logits, targets, old_logp, advantages, mask, ref_logp, t,
+                                float(eps_low), float(eh), float(beta), loss_type,
+                                max_completion_length, normalizer)
+        if out is not None:
+            loss, logp, ent = out
+            if not return_stats:
+                return loss, logp, ent
+            with torch.no_grad():
+                _, stats = fused_grpo_loss(logp, old_logp, advantages, mask, ref_logp, **loss_kw)
+            return loss, logp, ent, stats
+    # The unfused composition: same loss, logp / entropy differentiable.  It
+    # also serves calls that need no gradient (evaluation, logging,
+    # torch.no_grad()): the fused kernel would allocate and write a full
+    # [B, S, V] d_logits that nothing reads.
+    logp, ent, _ = fused_logprob_entropy(logits, targets, temperature)
+    loss, stats = fused_grpo_loss(logp, old_logp, advantages, mask, ref_logp, **loss_kw)
+    return (loss, logp, ent, stats) if return_stats else (loss, logp, ent)
 
+
+def _weight_kind(B, S, loss_type, max_completion_length, normalizer):
+    """(kind, scale) of grpo_token_weights for the compiled binding: 0 "grpo",
+    1 "bnpo", 2 a fixed normaliser with its float32 reciprocal."""
+    if loss_type == "grpo":
+        return 0, 1.0
+    if loss_type == "bnpo":
+        return 1, 1.0
+    if loss_type == "dr_grpo":
+        L = S if max_completion_length is None else max_completion_length
+        return 2, _f32_reciprocal(B * L)
+    if loss_type == "dapo":
+        if normalizer is None:
+            raise ValueError("loss_type='dapo' needs `normalizer`")
+        return 2, _f32_reciprocal(normalizer)
+    raise ValueError(f"unknown loss_type {loss_type!r}")
+
+
+def _fused_python(logits, targets, old_logp, advantages, mask, ref_logp, t, eps_low, eps_high,
+                  beta, loss_type, max_completion_length, normalizer):
+    """The fused path in Python (graph capture): (loss, logp, entropy), or
+    None when klp_grpo_step does not take these logits."""
+    if not _fused_supported(logits, _C.row_layout(logits)):
+        return None
+    B, S, _ = logits.shape
     dev = logits.device
 
     def f32(x, name, shape):
@@ -263,11 +306,5 @@ def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch
          else torch.ones((B, S), dtype=torch.float32, device=dev))
     ref = f32(ref_logp, "ref_logp", (B, S)) if (beta != 0.0 and ref_logp is not None) else None
     weight = grpo_token_weights(m, loss_type, max_completion_length, normalizer).contiguous()
-    eh = eps_low if eps_high is None else eps_high
-    params = (t, float(eps_low), float(eh), float(beta), int(per_token))
-    loss, logp, ent = _FusedGrpoStep.apply(logits, targets, old, ref, adv, weight, params)
-    if not return_stats:
-        return loss, logp, ent
-    with torch.no_grad():
-        _, stats = fused_grpo_loss(logp, old, adv, m, ref, **loss_kw)
-    return loss, logp, ent, stats
+    params = (t, eps_low, eps_high, beta, int(per_token))
+    return _FusedGrpoStep.apply(logits, targets, old, ref, adv, weight, params)

@@ -20,7 +20,7 @@ def test_exports():
                  "fused_logprob_entropy_v1_backward", "fwd_launch", "bwd_launch",
                  "fused_logprob_entropy", "fused_logprob_entropy_forward",
                  "fused_logprob_entropy_naive_op", "row_layout", "workspaces_cached",
-                 "fused_grpo_loss"):
+                 "fused_grpo_loss", "fused_grpo_step"):
         assert callable(getattr(b, name)), name
     assert issubclass(b.InputAssertionError, AssertionError)
 

@@ -238,3 +238,79 @@ def test_compiled_grpo_loss_edges():
         fused_grpo_loss(x, x, torch.zeros(2))
     with pytest.raises(RuntimeError, match="eps_low"):
         fused_grpo_loss(x, x, torch.zeros(2, device=DEV), eps_low=-0.1)
+
+
+class _StepPythonPathOnly:
+    """Stands in for the binding so that kernel_opt.grpo_step runs its Python
+    statement of the fused step (the path graph capture takes)."""
+
+    class CaptureDeclined(Exception):
+        pass
+
+    @staticmethod
+    def fused_grpo_step(*args, **kwargs):
+        raise _StepPythonPathOnly.CaptureDeclined()
+
+
+STEP_CASES = [  # dtype, (B, S, V), strided rows, loss_type, beta, per-token adv, mask, T, scale
+    (torch.bfloat16, (3, 40, 4096), False, "grpo", 0.0, False, "bool", None, 1.0),
+    (torch.bfloat16, (2, 33, 152064), True, "bnpo", 0.04, True, None, 0.7, 1.0),
+    (torch.float16, (4, 17, 8200), False, "dr_grpo", 0.04, False, "float", None, 2.5),
+    (torch.float32, (2, 9, 32000), True, "dapo", 0.0, True, "int", 1.3, -0.5),
+    (torch.bfloat16, (8, 300, 40960), False, "grpo", 0.04, False, "bool", None, 1.0),  # persistent
+]
+
+
+@pytest.mark.parametrize("dtype,shape,strided,loss_type,beta,per_token,mask_kind,T,scale",
+                         STEP_CASES)
+def test_compiled_grpo_step_equals_python_function(monkeypatch, dtype, shape, strided, loss_type,
+                                                   beta, per_token, mask_kind, T, scale):
+    """fused_grpo_step through the binding's C++ autograd op and through
+    grpo_step.py's Python statement: loss, logp, entropy, d_logits and the
+    stats bit for bit, on the same row counter scheme."""
+    from kernel_opt import fused_grpo_step, grpo_step
+    B, S, V = shape
+    full = (B, S + 1, V) if strided else (B, S, V)
+    base = seeded_logits(full, dtype, seed=B * S + V).to(DEV)
+    t = seeded_targets((B, S), V, seed=5).to(DEV)
+    g = torch.Generator().manual_seed(S)
+    old = (-torch.rand(B, S, generator=g) * 3).to(DEV)
+    ref = (-torch.rand(B, S, generator=g) * 3).to(DEV)
+    adv = torch.randn((B, S) if per_token else (B,), generator=g).to(DEV)
+    m = torch.rand(B, S, generator=g) < 0.8
+    mask = None if mask_kind is None else {"float": m.float(), "bool": m,
+                                           "int": m.to(torch.int32)}[mask_kind].to(DEV)
+    kw = dict(beta=beta, loss_type=loss_type, eps_high=0.28, temperature=T,
+              normalizer=77.0 if loss_type == "dapo" else None, return_stats=True)
+    res = []
+    for python_path in (False, True):
+        if python_path:
+            monkeypatch.setattr(grpo_step, "binding", _StepPythonPathOnly)
+        leaf = base.clone().requires_grad_(True)
+        x = leaf[:, :-1, :] if strided else leaf
+        loss, lp, ent, stats = fused_grpo_step(x, t, old, adv, mask, ref, **kw)
+        (loss * scale).backward()
+        res.append((loss.detach(), lp, ent, stats, leaf.grad, loss.grad_fn.name()))
+    for a, b in zip(res[0][:5], res[1][:5]):
+        assert torch.equal(a, b)
+    assert "CppNode" in res[0][5] and "FusedGrpoStep" in res[0][5], res[0][5]
+    assert "CppNode" not in res[1][5], res[1][5]
+
+
+def test_compiled_grpo_step_backward_once_and_fallback():
+    from kernel_opt import fused_grpo_step
+    x = seeded_logits((2, 5, 4096), torch.bfloat16, seed=3).to(DEV).requires_grad_(True)
+    t = seeded_targets((2, 5), 4096, seed=3).to(DEV)
+    old = torch.zeros(2, 5, device=DEV)
+    adv = torch.ones(2, device=DEV)
+    loss, _, _ = fused_grpo_step(x, t, old, adv)
+    loss.backward(retain_graph=True)
+    with pytest.raises(RuntimeError, match="only once per forward"):
+        loss.backward()
+    # rows that are not whole 16-byte vectors: the unfused composition
+    y = seeded_logits((2, 5, 4099), torch.bfloat16, seed=4).to(DEV).requires_grad_(True)
+    t2 = seeded_targets((2, 5), 4099, seed=4).to(DEV)
+    loss2, lp2, _ = fused_grpo_step(y, t2, old, adv)
+    assert lp2.requires_grad and "FusedGrpoStep" not in loss2.grad_fn.name()
+    loss2.backward()
+    assert y.grad is not None and torch.isfinite(y.grad.float()).all()
