@@ -595,14 +595,56 @@ def grpo_step_timing(dev, K, logits, targets):
     tbps = nbytes / (res["fused"] * 1e-6) / 1e12
     del d
     torch.cuda.empty_cache()
+
+    # The same step through the public entry points, from Python: the fused
+    # step + loss.backward(), against fused_logprob_entropy + fused_grpo_loss
+    # + loss.backward(); issued back to back (host-paced) and queued behind a
+    # spin kernel (GPU time).
+    from kernel_opt import fused_grpo_loss, fused_grpo_step, fused_logprob_entropy
+    x = logits.detach().clone().requires_grad_(True)
+    kw = dict(eps_low=eps_low, eps_high=eps_high, beta=beta, loss_type="grpo")
+
+    def step_fused():
+        loss_, _, _ = fused_grpo_step(x, targets, old, adv, mask, ref, **kw)
+        loss_.backward()
+        x.grad = None
+
+    def step_unfused():
+        lp_, _, _ = fused_logprob_entropy(x, targets)
+        loss_, _ = fused_grpo_loss(lp_, old, adv, mask, ref, **kw)
+        loss_.backward()
+        x.grad = None
+
+    e2e = {}
+    for name, fn in (("fused", step_fused), ("unfused", step_unfused)):
+        for _ in range(3):
+            fn()
+        for queued in (False, True):
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            if queued:  # long enough to hold K host-issued steps
+                torch.cuda._sleep(max(Timer.QUEUE_SPIN_CYCLES, K * 500_000))
+            a.record()
+            for _ in range(K):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            e2e[name + ("_queued" if queued else "")] = round(a.elapsed_time(b) / K * 1e3, 2)
+    del x
+    torch.cuda.empty_cache()
     return {"shape": [B, S, V], "loss_type": "grpo", "beta": beta,
             "fused_us": round(res["fused"], 2), "unfused_us": round(res["unfused"], 2),
             "speedup": round(res["unfused"] / res["fused"], 3),
             "fused_algorithmic_bytes": nbytes, "fused_tbps": round(tbps, 4),
             "fused_pct_peak": round(100 * tbps / HBM_PEAK_TBPS, 2),
+            "end_to_end_us": e2e,
             "note": "fused = klp_grpo_step (logits read once, d_logits written once); "
                     "unfused = klp_fwd, klp_grpo_fwd, klp_grpo_bwd, klp_bwd (logits read "
-                    "twice); both kernel time through the C ABI, outputs preallocated"}
+                    "twice); both kernel time through the C ABI, outputs preallocated; "
+                    "end_to_end_us: the step through the public entry points from Python "
+                    "(fused_grpo_step vs fused_logprob_entropy + fused_grpo_loss, loss + "
+                    "backward), host-paced and *_queued (GPU time)"}
 
 
 def shard_timing(dev, K, N=32768, V=151936, P=8):

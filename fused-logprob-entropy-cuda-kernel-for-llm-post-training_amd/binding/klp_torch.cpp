@@ -573,16 +573,20 @@ at::Tensor sched_counter(int device, hipStream_t stream) {
     return g_sched.front().buf;
 }
 
-// grpo_step.grpo_token_weights on a float32 mask, the same torch operations
-// in the same order (so the same bits): kind 0 "grpo" (B * max(row sum, 1)),
-// 1 "bnpo" (max(mask sum, 1)), 2 a fixed normaliser whose float32 reciprocal
-// the caller passes as `scale` ("dr_grpo", "dapo").
+// grpo_step.grpo_token_weights: kind 0 "grpo" (B * max(row sum, 1)), 1 "bnpo"
+// (max(mask sum, 1)), 2 a fixed normaliser whose float32 reciprocal the
+// caller passes as `scale` ("dr_grpo", "dapo").  The same values bit for bit
+// in fewer launches: a bool or integer mask is summed in float32 and
+// multiplied with float32 promotion instead of being converted first (its
+// 0 / 1 sums are exact either way), and the Python statement's `* 1.0` after
+// the reciprocal changes no value.
 at::Tensor token_weights(const at::Tensor& m, int64_t kind, double scale) {
     if (kind == 0) {
-        const at::Tensor den = m.sum({1}, true).clamp_min(1.0) * static_cast<double>(m.size(0));
-        return m * (den.reciprocal() * 1.0);
+        const at::Tensor den =
+            m.sum({1}, true, at::kFloat).clamp_min(1.0) * static_cast<double>(m.size(0));
+        return m * den.reciprocal();
     }
-    if (kind == 1) return m * (m.sum().clamp_min(1.0).reciprocal() * 1.0);
+    if (kind == 1) return m * m.sum(at::kFloat).clamp_min(1.0).reciprocal();
     return m * scale;
 }
 
@@ -676,8 +680,18 @@ std::optional<std::vector<at::Tensor>> fused_grpo_step(
     const bool per_token = advantages.dim() != 1;
     const at::Tensor adv = per_token ? grpo_operand(advantages, "advantages", {B, S}, dev)
                                      : grpo_operand(advantages, "advantages", {B}, dev);
-    at::Tensor m = grpo_operand(mask, "mask", {B, S}, dev);
-    if (!m.defined()) m = at::ones({B, S}, at::TensorOptions().dtype(at::kFloat).device(dev));
+    // The mask is checked as grpo_operand checks it and used in its own dtype
+    // (token_weights).
+    at::Tensor m;
+    if (mask.has_value() && mask->defined()) {
+        if (mask->device() != dev) throw std::runtime_error("mask must be on " + dev.str());
+        if (mask->sizes() != at::IntArrayRef({B, S}))
+            throw std::runtime_error("mask has shape " + tuple_str(mask->sizes()) +
+                                     ", expected " + tuple_str({B, S}));
+        m = mask->detach();
+    } else {
+        m = at::ones({B, S}, at::TensorOptions().dtype(at::kFloat).device(dev));
+    }
     const at::Tensor ref = (beta != 0.0 && ref_logp.has_value() && ref_logp->defined())
                                ? grpo_operand(ref_logp, "ref_logp", {B, S}, dev)
                                : at::Tensor();
