@@ -1,12 +1,13 @@
 """GPU checks of the compiled binding (binding/klp_torch.cpp), which the
-public logprob entry points go through: its autograd function against the
-Python statement of the same op (ops._FusedLogprobEntropy over the same
-launchers), bit for bit, forward and backward; its split-row workspaces (one
-per stream, at most 16 kept); its error behaviour on GPU tensors.  Under
-graph capture the binding declines every call before it allocates or
-launches anything (binding.CaptureDeclined) and the Python path runs: the
-capture tests of test_logprob_gpu.py and test_grpo_step_gpu.py go through
-that fallback."""
+public logprob, GRPO loss and fused GRPO step entry points go through: each
+autograd function against the Python statement of the same op
+(ops._FusedLogprobEntropy, grpo._FusedGrpoLoss, grpo_step._FusedGrpoStep over
+the same launchers), bit for bit, forward and backward; the split-row
+workspaces (one per stream, at most 16 kept); the error behaviour on GPU
+tensors.  Under graph capture the binding declines every call before it
+allocates or launches anything (binding.CaptureDeclined) and the Python path
+runs: the capture tests of test_logprob_gpu.py and test_grpo_step_gpu.py go
+through that fallback."""
 from __future__ import annotations
 
 import pytest
