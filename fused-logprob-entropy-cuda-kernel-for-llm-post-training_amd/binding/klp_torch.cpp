@@ -680,8 +680,18 @@ std::optional<std::vector<at::Tensor>> fused_grpo_step(
     const bool per_token = advantages.dim() != 1;
     const at::Tensor adv = per_token ? grpo_operand(advantages, "advantages", {B, S}, dev)
                                      : grpo_operand(advantages, "advantages", {B}, dev);
-    // The mask is checked as grpo_operand checks it and used in its own dtype
-    // (token_weights).
+    if (targets.device() != dev)
+        throw std::runtime_error("targets must be on " + dev.str() + ", got " +
+                                 targets.device().str());
+    require(targets.scalar_type() == at::kLong, "targets must be int64");
+    require(targets.is_contiguous(), "targets must be contiguous");
+    if (targets.sizes() != at::IntArrayRef({B, S}))
+        throw std::runtime_error("targets has shape " + tuple_str(targets.sizes()) +
+                                 ", expected " + tuple_str({B, S}));
+    // The mask is checked as grpo_operand checks it.  A floating mask is
+    // taken in float32, as the Python statement takes every mask; a bool or
+    // integer mask stays as it is (token_weights promotes it to float32, and
+    // its 0 / 1 sums are exact either way, so the weights are the same bits).
     at::Tensor m;
     if (mask.has_value() && mask->defined()) {
         if (mask->device() != dev) throw std::runtime_error("mask must be on " + dev.str());
@@ -689,6 +699,8 @@ std::optional<std::vector<at::Tensor>> fused_grpo_step(
             throw std::runtime_error("mask has shape " + tuple_str(mask->sizes()) +
                                      ", expected " + tuple_str({B, S}));
         m = mask->detach();
+        if (at::isFloatingType(m.scalar_type()) && m.scalar_type() != at::kFloat)
+            m = m.to(at::kFloat);
     } else {
         m = at::ones({B, S}, at::TensorOptions().dtype(at::kFloat).device(dev));
     }
@@ -696,6 +708,9 @@ std::optional<std::vector<at::Tensor>> fused_grpo_step(
                                ? grpo_operand(ref_logp, "ref_logp", {B, S}, dev)
                                : at::Tensor();
     const at::Tensor weight = token_weights(m, weight_kind, weight_scale).contiguous();
+    // klp_grpo_step reads the weights as float32 [B, S].
+    require(weight.scalar_type() == at::kFloat,
+            "mask must be bool, integer or floating point (token weights are float32)");
     auto out = FusedGrpoStep::apply(logits, targets, old,
                                     ref.defined() ? std::optional<at::Tensor>(ref) : std::nullopt,
                                     adv, weight, temperature, eps_low, eps_high, beta,

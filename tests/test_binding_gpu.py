@@ -207,8 +207,9 @@ def test_compiled_grpo_loss_equals_python_function(monkeypatch, loss_type, level
     ref = (lp0.cpu() + torch.randn(B, S, generator=g) * 0.2).to(DEV)
     adv = torch.randn((B, S) if per_token else (B,), generator=g).to(DEV)
     m = torch.rand(B, S, generator=g) < 0.8
-    mask = None if mask_kind is None else {"float": m.float(), "bool": m,
-                                           "int": m.to(torch.int32)}[mask_kind].to(DEV)
+    mask = None if mask_kind is None else {
+        "float": m.float(), "bool": m, "int": m.to(torch.int32), "bf16": m.to(torch.bfloat16),
+        "fp16": m.to(torch.float16), "f64": m.to(torch.float64)}[mask_kind].to(DEV)
     kw = dict(beta=beta, loss_type=loss_type, importance_level=level, eps_high=0.28,
               max_completion_length=48 if loss_type == "dr_grpo" else None,
               normalizer=123.0 if loss_type == "dapo" else None)
@@ -259,6 +260,16 @@ STEP_CASES = [  # dtype, (B, S, V), strided rows, loss_type, beta, per-token adv
     (torch.float16, (4, 17, 8200), False, "dr_grpo", 0.04, False, "float", None, 2.5),
     (torch.float32, (2, 9, 32000), True, "dapo", 0.0, True, "int", 1.3, -0.5),
     (torch.bfloat16, (8, 300, 40960), False, "grpo", 0.04, False, "bool", None, 1.0),  # persistent
+    # Floating masks other than float32 are taken in float32 (the token
+    # weights the kernel reads are float32), for every loss type.
+    (torch.bfloat16, (3, 40, 4096), False, "grpo", 0.0, False, "bf16", None, 1.0),
+    (torch.bfloat16, (2, 33, 8192), False, "bnpo", 0.04, False, "fp16", None, 1.0),
+    (torch.float16, (4, 17, 8200), False, "dr_grpo", 0.04, False, "f64", None, 2.5),
+    (torch.bfloat16, (2, 9, 4096), True, "dapo", 0.0, True, "bf16", 1.3, -0.5),
+    (torch.float32, (2, 9, 32000), False, "grpo", 0.04, False, "f64", None, 1.0),
+    (torch.float16, (3, 12, 4096), False, "bnpo", 0.0, True, "f64", 0.9, 1.0),
+    (torch.bfloat16, (2, 21, 4096), False, "dr_grpo", 0.0, False, "bf16", None, 1.0),
+    (torch.float32, (2, 9, 4096), False, "dapo", 0.04, False, "fp16", None, 1.0),
 ]
 
 
@@ -279,8 +290,9 @@ def test_compiled_grpo_step_equals_python_function(monkeypatch, dtype, shape, st
     ref = (-torch.rand(B, S, generator=g) * 3).to(DEV)
     adv = torch.randn((B, S) if per_token else (B,), generator=g).to(DEV)
     m = torch.rand(B, S, generator=g) < 0.8
-    mask = None if mask_kind is None else {"float": m.float(), "bool": m,
-                                           "int": m.to(torch.int32)}[mask_kind].to(DEV)
+    mask = None if mask_kind is None else {
+        "float": m.float(), "bool": m, "int": m.to(torch.int32), "bf16": m.to(torch.bfloat16),
+        "fp16": m.to(torch.float16), "f64": m.to(torch.float64)}[mask_kind].to(DEV)
     kw = dict(beta=beta, loss_type=loss_type, eps_high=0.28, temperature=T,
               normalizer=77.0 if loss_type == "dapo" else None, return_stats=True)
     res = []
@@ -315,3 +327,25 @@ def test_compiled_grpo_step_backward_once_and_fallback():
     assert lp2.requires_grad and "FusedGrpoStep" not in loss2.grad_fn.name()
     loss2.backward()
     assert y.grad is not None and torch.isfinite(y.grad.float()).all()
+
+
+def test_compiled_grpo_step_checks_targets_itself():
+    """binding.fused_grpo_step checks targets (device, dtype, layout, shape)
+    before any launch, without the Python wrapper's checks in front of it."""
+    from kernel_opt._library import binding
+    B, S, V = 2, 5, 4096
+    x = seeded_logits((B, S, V), torch.bfloat16, seed=11).to(DEV)
+    t = seeded_targets((B, S), V, seed=11).to(DEV)
+    old = torch.zeros(B, S, device=DEV)
+    adv = torch.ones(B, device=DEV)
+    args = (old, adv, None, None, 1.0, 0.2, 0.28, 0.0, 1, 1.0)
+    assert binding.fused_grpo_step(x, t, *args) is not None
+    bad = [
+        (t.cpu(), "targets must be on"),
+        (t.to(torch.int32), "targets must be int64"),
+        (seeded_targets((S, B), V, seed=1).to(DEV).t(), "targets must be contiguous"),
+        (t.reshape(-1), "targets has shape"),
+    ]
+    for tt, msg in bad:
+        with pytest.raises(RuntimeError, match=msg):
+            binding.fused_grpo_step(x, tt, *args)
