@@ -51,7 +51,7 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
         for (int64_t v = b + tid; v < e; v += NTHREADS) {
             float x = to_f32<DT>(rp[v]);
             if (kScaled) x *= p.scale;
-            float d = grad_one(x, g);
+            float d = grad_elem<DT>(x, g);
             if (v == tgt) d += g.g_logp;
             if (kScaled) d *= p.scale;
             dp[v] = from_f32<DT>(d);
@@ -70,7 +70,7 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
             const int64_t v = (tid < head) ? tid : tail_begin + (tid - head);
             float x = to_f32<DT>(rp[v]);
             if (kScaled) x *= p.scale;
-            float d = grad_one(x, g);
+            float d = grad_elem<DT>(x, g);
             if (v == tgt) d += g.g_logp;
             if (kScaled) d *= p.scale;
             dp[v] = from_f32<DT>(d);
@@ -118,7 +118,8 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
                 float x[EPV];
                 unpack<DT>(v[u], x);
 #pragma unroll
-                for (int j = 0; j < EPV; ++j) x[j] = grad_one(kScaled ? x[j] * p.scale : x[j], g);
+                for (int j = 0; j < EPV; ++j)
+                    x[j] = grad_elem<DT>(kScaled ? x[j] * p.scale : x[j], g);
                 if (idx == t_vec) {
 #pragma unroll
                     for (int j = 0; j < EPV; ++j)

@@ -199,7 +199,7 @@ __device__ __forceinline__ RowGrad row_results(const GrpoStepParams& p, int64_t 
 }
 
 // Pass 2 for one vector (the row's vector i): klp_bwd's gradient with
-// g_ent = g_lse = 0 (grad_one_logp_only), plus the one-hot term at the
+// g_ent = g_lse = 0 (grad_elem_logp_only), plus the one-hot term at the
 // target (element t_elem of vector t_vec), times 1/T, packed to the dtype.
 template <int DT, bool kScaled>
 __device__ __forceinline__ u32x4 grad_vec(u32x4 v, uint32_t i, const RowGrad& g,
@@ -208,7 +208,8 @@ __device__ __forceinline__ u32x4 grad_vec(u32x4 v, uint32_t i, const RowGrad& g,
     float x[EPV];
     unpack<DT>(v, x);
 #pragma unroll
-    for (int j = 0; j < EPV; ++j) x[j] = grad_one_logp_only(kScaled ? x[j] * scale : x[j], g);
+    for (int j = 0; j < EPV; ++j)
+        x[j] = grad_elem_logp_only<DT>(kScaled ? x[j] * scale : x[j], g);
     if (i == t_vec) {
 #pragma unroll
         for (int j = 0; j < EPV; ++j)
