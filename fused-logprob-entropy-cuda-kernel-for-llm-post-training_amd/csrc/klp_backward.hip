@@ -20,6 +20,55 @@
 
 namespace klp {
 
+// The piece's 16-byte vectors [vb, ve) (the body of klp_bwd_kernel).
+template <int DT, int WAVES, int U, bool kNtStore, bool kScaled, bool kLseNonNeg>
+__device__ __forceinline__ void bwd_vectors(const BwdParams& p, const u32x4* vin, u32x4* vout,
+                                            int64_t vb, int64_t ve, int64_t t_vec,
+                                            int t_lane_elem, const RowGrad& g) {
+    constexpr int NTHREADS = WAVES * 64;
+    constexpr int EPV = Traits<DT>::kPerVec;
+    const int tid = threadIdx.x;
+    // Buffer loads through a descriptor over the piece, with 32-bit offsets
+    // (the caller keeps pieces under 2 GiB): C4 3113-3132 us against
+    // 3166-3195 us for global loads of the same policy, C2 equal.  Temporal
+    // loads here (non-temporal in the forward): measured best for a forward
+    // followed by a backward over the same logits.
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<u32x4*>(vin + vb), 0, static_cast<int>((ve - vb) * 16), 0x00020000);
+    for (int64_t i0 = vb; i0 < ve; i0 += static_cast<int64_t>(NTHREADS) * U) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t idx = i0 + tid + u * NTHREADS;
+            if (idx < ve)
+                v[u] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rs, static_cast<int>((idx - vb) * 16), 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t idx = i0 + tid + u * NTHREADS;
+            if (idx < ve) {
+                float x[EPV];
+                unpack<DT>(v[u], x);
+#pragma unroll
+                for (int j = 0; j < EPV; ++j)
+                    x[j] = grad_elem<DT, kLseNonNeg>(kScaled ? x[j] * p.scale : x[j], g);
+                if (idx == t_vec) {
+#pragma unroll
+                    for (int j = 0; j < EPV; ++j)
+                        if (j == t_lane_elem) x[j] += g.g_logp;
+                }
+                if (kScaled) {
+#pragma unroll
+                    for (int j = 0; j < EPV; ++j) x[j] *= p.scale;
+                }
+                if constexpr (kNtStore) __builtin_nontemporal_store(pack<DT>(x), vout + idx);
+                else vout[idx] = pack<DT>(x);
+            }
+        }
+    }
+}
+
 template <int DT, int WAVES, int U, bool kNtStore, bool kScaled>
 __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
     typedef typename Traits<DT>::elem elem;
@@ -51,7 +100,7 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
         for (int64_t v = b + tid; v < e; v += NTHREADS) {
             float x = to_f32<DT>(rp[v]);
             if (kScaled) x *= p.scale;
-            float d = grad_elem<DT>(x, g);
+            float d = g.lse >= 0.0f ? grad_elem<DT, true>(x, g) : grad_elem<DT, false>(x, g);
             if (v == tgt) d += g.g_logp;
             if (kScaled) d *= p.scale;
             dp[v] = from_f32<DT>(d);
@@ -70,7 +119,7 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
             const int64_t v = (tid < head) ? tid : tail_begin + (tid - head);
             float x = to_f32<DT>(rp[v]);
             if (kScaled) x *= p.scale;
-            float d = grad_elem<DT>(x, g);
+            float d = g.lse >= 0.0f ? grad_elem<DT, true>(x, g) : grad_elem<DT, false>(x, g);
             if (v == tgt) d += g.g_logp;
             if (kScaled) d *= p.scale;
             dp[v] = from_f32<DT>(d);
@@ -95,44 +144,18 @@ __global__ __launch_bounds__(WAVES * 64) void klp_bwd_kernel(BwdParams p) {
     const int64_t t_vec = (tgt >= head && tgt < tail_begin) ? t_rel / EPV : -1;
     const int t_lane_elem = (t_vec >= 0) ? static_cast<int>(t_rel - t_vec * EPV) : 0;
 
-    // Buffer loads through a descriptor over the piece, with 32-bit offsets
-    // (the caller keeps pieces under 2 GiB): C4 3113-3132 us against
-    // 3166-3195 us for global loads of the same policy, C2 equal.  Temporal
-    // loads here (non-temporal in the forward): measured best for a forward
-    // followed by a backward over the same logits.
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<u32x4*>(vin + vb), 0, static_cast<int>((ve - vb) * 16), 0x00020000);
-    for (int64_t i0 = vb; i0 < ve; i0 += static_cast<int64_t>(NTHREADS) * U) {
-        u32x4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t idx = i0 + tid + u * NTHREADS;
-            if (idx < ve)
-                v[u] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rs, static_cast<int>((idx - vb) * 16), 0, 0);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t idx = i0 + tid + u * NTHREADS;
-            if (idx < ve) {
-                float x[EPV];
-                unpack<DT>(v[u], x);
-#pragma unroll
-                for (int j = 0; j < EPV; ++j)
-                    x[j] = grad_elem<DT>(kScaled ? x[j] * p.scale : x[j], g);
-                if (idx == t_vec) {
-#pragma unroll
-                    for (int j = 0; j < EPV; ++j)
-                        if (j == t_lane_elem) x[j] += g.g_logp;
-                }
-                if (kScaled) {
-#pragma unroll
-                    for (int j = 0; j < EPV; ++j) x[j] *= p.scale;
-                }
-                if constexpr (kNtStore) __builtin_nontemporal_store(pack<DT>(x), vout + idx);
-                else vout[idx] = pack<DT>(x);
-            }
-        }
+    // fp32 rows take their Fast2Sum operand order from the sign of lse
+    // (grad_one_fp32): one branch per row, outside the element loop.
+    if constexpr (DT == kFP32) {
+        if (g.lse >= 0.0f)
+            bwd_vectors<DT, WAVES, U, kNtStore, kScaled, true>(p, vin, vout, vb, ve, t_vec,
+                                                               t_lane_elem, g);
+        else
+            bwd_vectors<DT, WAVES, U, kNtStore, kScaled, false>(p, vin, vout, vb, ve, t_vec,
+                                                                t_lane_elem, g);
+    } else {
+        bwd_vectors<DT, WAVES, U, kNtStore, kScaled, true>(p, vin, vout, vb, ve, t_vec,
+                                                           t_lane_elem, g);
     }
 }
 

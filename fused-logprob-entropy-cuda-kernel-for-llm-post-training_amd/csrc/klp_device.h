@@ -412,52 +412,65 @@ __device__ __forceinline__ float grad_one_logp_only(float x, const RowGrad& g) {
 }
 
 // fp32 gradients.  An fp32 output resolves the exponent's rounding: the
-// argument above (|arg| ~ 20 for typical rows, one rounding of ulp(20) /
-// 2 ~ 1e-6) moves p by several ulps.  Here the argument is carried exactly
-// to well below one ulp of p:
-//   x - lse          as dh + dl (TwoSum: dh = RN(x - lse), dl its exact error),
-//   (dh + dl) log2e  as ah + al (ah = RN(dh * log2e), al the fma remainder
-//                    plus dl * log2e and dh times log2e's own fp32 tail),
-//   p = 2^ah (1 + al ln2),
+// argument above (|arg| ~ 20 for typical rows, two roundings of ulp(20) / 2
+// ~ 1e-6) moves p by several ulps.  Here the argument is carried exactly to
+// well below one ulp of p:
+//   x - lse          as dh + dl: dh = RN(x - lse) and dl its exact error by
+//                    Fast2Sum, the larger operand first.  lse >= x for every
+//                    logit of the row, so a row with lse >= 0 takes (-lse, x)
+//                    (exact for every x >= -lse, i.e. all logits but those
+//                    below -lse, whose p < e^(-2 lse) keeps the error of one
+//                    rounding), and a row with lse < 0 takes (x, -lse), exact
+//                    for every logit.  The order is a row-level choice
+//                    (kLseNonNeg), not a per-element one;
+//   (dh + dl) log2e  as ah = RN(dh log2e) and, in nats, the remainder
+//                    c = (dh log2e - ah) ln2 + dl + dh (log2e's fp32 tail) ln2
+//                    (log2e ln2 = 1 to within that tail);
+//   p = 2^ah (1 + c),
 // so p carries v_exp_f32's error and the saved lse's rounding only, and
 // lp = dh + dl enters the entropy term with its remainder too.  -inf logits
-// are clamped to kNegBig first (p = 0 exactly, every term finite).  About
-// ten more operations per element, against the ~50 issue slots an fp32
-// element has at the backward's HBM rate.
-constexpr float kLog2eTail = 1.92596299e-08f;  // log2(e) - fp32(log2(e))
+// are clamped to kNegBig first (p = 0 exactly, every term finite).  Six more
+// operations per element than grad_one.
+constexpr float kLog2eTailLn2 = 1.3349758e-08f;  // (log2(e) - fp32(log2(e))) * ln 2
 
+template <bool kLseNonNeg>
 __device__ __forceinline__ float p_exact_arg(float x, float lse, float& dh, float& dl) {
     const float xc = fmax_nan(x, kNegBig);
     dh = xc - lse;
-    const float bb = dh - xc;
-    dl = (xc - (dh - bb)) + (-lse - bb);
+    if constexpr (kLseNonNeg) dl = xc - (dh + lse);
+    else dl = -lse - (dh - xc);
     const float ah = dh * kLog2e;
-    const float al = fmaf(dh, kLog2e, -ah) + fmaf(dl, kLog2e, dh * kLog2eTail);
+    float c = fmaf(dh, kLog2e, -ah);
+    c = fmaf(c, kLn2, dl);
+    c = fmaf(dh, kLog2eTailLn2, c);
     const float e = exp2_hw(ah);
-    return fmaf(e, al * kLn2, e);
+    return fmaf(e, c, e);
 }
 
+template <bool kLseNonNeg>
 __device__ __forceinline__ float grad_one_fp32(float x, const RowGrad& g) {
     float dh, dl;
-    const float p = p_exact_arg(x, g.lse, dh, dl);
-    return p * (fmaf(-g.g_ent, dh, g.c0) - g.g_ent * dl);
+    const float p = p_exact_arg<kLseNonNeg>(x, g.lse, dh, dl);
+    return p * fmaf(-g.g_ent, dl, fmaf(-g.g_ent, dh, g.c0));
 }
 
+template <bool kLseNonNeg>
 __device__ __forceinline__ float grad_one_fp32_logp_only(float x, const RowGrad& g) {
     float dh, dl;
-    return p_exact_arg(x, g.lse, dh, dl) * g.c0;
+    return p_exact_arg<kLseNonNeg>(x, g.lse, dh, dl) * g.c0;
 }
 
-// The gradient of one logit of dtype DT (fp32 rows take the exact-argument
-// form above, bf16 / fp16 rows, whose outputs do not resolve it, grad_one).
-template <int DT>
+// The gradient of one logit of dtype DT: fp32 rows take the exact-argument
+// form above, with the row's operand order kLseNonNeg (= lse >= 0); bf16 /
+// fp16 rows, whose outputs do not resolve it, take grad_one.
+template <int DT, bool kLseNonNeg>
 __device__ __forceinline__ float grad_elem(float x, const RowGrad& g) {
-    if constexpr (DT == kFP32) return grad_one_fp32(x, g);
+    if constexpr (DT == kFP32) return grad_one_fp32<kLseNonNeg>(x, g);
     else return grad_one(x, g);
 }
-template <int DT>
+template <int DT, bool kLseNonNeg>
 __device__ __forceinline__ float grad_elem_logp_only(float x, const RowGrad& g) {
-    if constexpr (DT == kFP32) return grad_one_fp32_logp_only(x, g);
+    if constexpr (DT == kFP32) return grad_one_fp32_logp_only<kLseNonNeg>(x, g);
     else return grad_one_logp_only(x, g);
 }
 

@@ -207,9 +207,17 @@ __device__ __forceinline__ u32x4 grad_vec(u32x4 v, uint32_t i, const RowGrad& g,
     constexpr int EPV = Traits<DT>::kPerVec;
     float x[EPV];
     unpack<DT>(v, x);
+    // fp32 rows: the operand order of klp_bwd's exact argument (the sign of
+    // lse), so that the gradient is klp_bwd's bit for bit.
+    if (DT != kFP32 || g.lse >= 0.0f) {
 #pragma unroll
-    for (int j = 0; j < EPV; ++j)
-        x[j] = grad_elem_logp_only<DT>(kScaled ? x[j] * scale : x[j], g);
+        for (int j = 0; j < EPV; ++j)
+            x[j] = grad_elem_logp_only<DT, true>(kScaled ? x[j] * scale : x[j], g);
+    } else {
+#pragma unroll
+        for (int j = 0; j < EPV; ++j)
+            x[j] = grad_elem_logp_only<DT, false>(kScaled ? x[j] * scale : x[j], g);
+    }
     if (i == t_vec) {
 #pragma unroll
         for (int j = 0; j < EPV; ++j)
