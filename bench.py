@@ -18,22 +18,31 @@ Algorithmic bytes per launch (s = bytes per logit, N rows, V vocab):
     backward = 2*N*V*s + 8N (targets) + 16N (lse, entropy, g_logp, g_ent)
 (g_lse is None in these workloads, so it is not read.)
 
-Timing, all with HIP events on the stream the kernels run on:
-  * `ms_per_step`: one event pair around K interleaved forward+backward steps
-    (the backward re-reads logits the forward has just streamed through the
-    256 MB Infinity Cache, so the step can beat the per-kernel rates);
-  * `fwd_ms` / `bwd_ms`: one event pair around max(K, 50) back-to-back
+Timing, on the stream the kernels run on:
+  * `ms_per_step`: one HIP-event pair around K interleaved forward+backward
+    steps (the backward re-reads logits the forward has just streamed
+    through the 256 MB Infinity Cache, so the step can beat the per-kernel
+    rates);
+  * `fwd_ms` / `bwd_ms`: one HIP-event pair around max(K, 50) back-to-back
     launches;
-  * `fwd_ms_flushed` / `bwd_ms_flushed`: max(K, 50) launches, each right
-    after a 1 GiB buffer was read (which evicts the logits from the cache):
-    one event pair around the (flush, launch) pairs minus one around the
-    flushes alone (`*_flushed_each` times every launch with its own event
-    pair instead, which adds the dispatch gap after the flush);
-  * `ceilings`: in the same process, at the same size and launch shape, the
-    library's calibration kernels (klp_ceiling_read: the forward's loads
-    without arithmetic; klp_ceiling_copy: the backward's loads and stores)
-    and torch's device copy, warm and flushed; `fwd_over_read` and
-    `bwd_over_copy` are the kernels' times over them.
+  * `fwd_ms_flushed` / `bwd_ms_flushed`: kernel durations from the device's
+    own timestamps (torch.profiler over ROCm's tracer, the figures
+    rocprofv3 --kernel-trace reports), the median over 24 launches each
+    right after a 1 GiB buffer was read (which evicts the logits from the
+    cache); `device_timed` gives these and the warm medians with their
+    interquartile spread.  Where the profiler sees no GPU (or with
+    --no-device-timer) HIP events time them instead: one pair around
+    (flush, launch) pairs minus one around the flushes alone;
+  * `ceilings`: in the same process, at the same size and launch shapes,
+    the library's calibration kernels, warm and flushed: klp_ceiling_read
+    (the forward's ring of loads without arithmetic), klp_ceiling_copy (the
+    backward's loop of loads and stores), klp_ceiling_read_pieces and
+    klp_ceiling_write (that loop's loads alone, its stores alone: their sum
+    is the time of a read+write stream whose reads and writes do not
+    overlap on the HBM bus), and torch's device copy; `fwd_over_read`,
+    `bwd_over_copy` and `bwd_over_read_plus_write` are the kernels' times
+    over them;
+  * `configs`: C3, C4 and C5 measured the same way at their own sizes.
 `roofline` reports the dominant kernel, the backward (it moves twice the
 forward's bytes), at the lower of its warm and flushed rates.  `traffic` is
 the HBM bytes per launch from a committed rocprofv3 counter summary under
@@ -258,7 +267,7 @@ def kernel_bytes(short: str, config: str):
         return fb
     if short.startswith("klp_bwd_kernel"):
         return bb
-    if short.startswith("klp_ceiling_read"):
+    if short.startswith("klp_ceiling_read") or short.startswith("klp_ceiling_write"):
         return rb
     if short.startswith("klp_ceiling_copy"):
         return 2 * rb
@@ -983,18 +992,81 @@ class Timer:
         return diffs[len(diffs) // 2], sum(ts) / len(ts)
 
 
+class DeviceTimer:
+    """Kernel durations from the device's own timestamps: torch.profiler over
+    ROCm's tracer, i.e. the begin and end of each dispatch, the figures
+    rocprofv3 --kernel-trace reports.  Each figure is the median over
+    `n` launches back to back ("warm") or each right after a flush
+    ("flushed"), with the interquartile range as the spread.  Unlike a pair
+    of HIP events around (flush + launch) minus one around the flush alone,
+    it is not the difference of two large, separately noisy times.
+
+    `available` is False where the profiler sees no GPU activity, or when
+    disabled (under rocprofv3, whose tracer must not share the process
+    with torch's); callers then fall back to HIP events."""
+
+    def __init__(self, timer, enabled=True):
+        self.timer = timer
+        self.available = False
+        if enabled:
+            try:
+                from torch.profiler import ProfilerActivity
+                self.available = ProfilerActivity.CUDA in torch.profiler.supported_activities()
+            except Exception:
+                self.available = False
+
+    def _durations(self, body, match, n, flushed):
+        from torch.profiler import ProfilerActivity, profile
+        torch.cuda.synchronize()
+        with profile(activities=[ProfilerActivity.CUDA]) as pf:
+            for k in range(n):
+                if flushed:
+                    self.timer.flush(k)
+                body()
+            torch.cuda.synchronize()
+        out = []
+        for e in pf.events():
+            if e.device_type == torch.autograd.DeviceType.CUDA and match in e.name:
+                t = getattr(e, "device_time", None)
+                out.append(float(t if t is not None else e.cuda_time))
+        return out
+
+    @staticmethod
+    def _summary(us):
+        us = sorted(us)
+        n = len(us)
+        med = statistics.median(us)
+        q1, q3 = us[n // 4], us[(3 * n) // 4]
+        return {"ms": round(med / 1e3, 5), "n": n, "spread_pct": round(100 * (q3 - q1) / med, 2),
+                "min_ms": round(us[0] / 1e3, 5), "max_ms": round(us[-1] / 1e3, 5)}
+
+    def stats(self, body, match, n=24):
+        """{"warm": {...}, "flushed": {...}} of the kernels named `match` in
+        `body` (one such launch per call); the first warm launch, right
+        after a flush, is dropped."""
+        warm = self._durations(body, match, n + 1, False)[1:]
+        flushed = self._durations(body, match, n, True)
+        if not warm or not flushed:
+            raise RuntimeError(f"profiler saw no kernel named {match!r}")
+        return {"warm": self._summary(warm), "flushed": self._summary(flushed)}
+
+
 def _tbps(nbytes, ms):
     return nbytes / (ms * 1e-3) / 1e12
 
 
-def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None):
+def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None, dtimer=None):
     """Forward / backward of workload `name` through the C ABI: the timed
     step loop, back-to-back and flushed per-kernel times, and the same-run
-    read / copy ceilings at the kernels' size and launch shapes."""
+    ceilings at the kernels' size and launch shapes: the forward's ring read
+    (klp_ceiling_read), the backward's copy (klp_ceiling_copy) and its loads
+    and stores alone (klp_ceiling_read_pieces, klp_ceiling_write).  With a
+    DeviceTimer the flushed figures (and a warm one beside the events' b2b
+    figure) are kernel durations from the device's timestamps; without one,
+    HIP events (Timer.flushed)."""
     from kernel_opt import _C
     from kernel_opt._library import check_status, lib
 
-    cfg = CONFIGS[name]
     inp = make_inputs(name, dev)
     logits, targets = inp["logits"], inp["targets"]
     g_logp, g_ent = inp["g_logp"].contiguous(), inp["g_ent"].contiguous()
@@ -1033,15 +1105,13 @@ def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None):
     kt = Timer(dev, max(K, KERNEL_LAUNCHES), timer.flush_mode, timer.buf)
     fwd_ms = kt.b2b(fwd)
     bwd_ms = kt.b2b(bwd)
-    fwd_fl, fwd_fl_each = kt.flushed(fwd)
-    bwd_fl, bwd_fl_each = kt.flushed(bwd)
 
     fwd_used = tuple(fcfg) if fcfg else _C.default_config("fwd", logits.dtype, N, V)
     bwd_used = tuple(bcfg) if bcfg else _C.default_config("bwd", logits.dtype, N, V)
 
     # Calibration kernels over a buffer of the logits' size (the logits
     # themselves when their rows are whole contiguous 16-byte vectors), with
-    # the kernels' launch shapes; the copy writes into d_logits.
+    # the kernels' launch shapes; the copy and the write go into d_logits.
     rb = ceiling_row_bytes(V, esz)
     if logits.is_contiguous() and (V * esz) % 16 == 0:
         src = logits
@@ -1049,18 +1119,26 @@ def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None):
         src = torch.empty(N * rb, dtype=torch.uint8, device=dev)
     dst = d_logits if d_logits.numel() * esz >= N * rb else torch.empty(N * rb, dtype=torch.uint8,
                                                                         device=dev)
-    sink = torch.zeros(N * max(fwd_used[2], 1), dtype=torch.int32, device=dev)
+    sink = torch.zeros(N * max(fwd_used[2], bwd_used[2], 1), dtype=torch.int32, device=dev)
     st = timer.stream.cuda_stream
     fw, fu, fs, _ = fwd_used
     bw, bu, bs, _ = bwd_used
+    magic = 0x9E3779B9
 
     def ceil_read():
         check_status(lib.klp_ceiling_read(src.data_ptr(), N, rb, fw, fu, fs, sink.data_ptr(),
-                                          0x9E3779B9, st))
+                                          magic, st))
 
     def ceil_copy():
         check_status(lib.klp_ceiling_copy(src.data_ptr(), dst.data_ptr(), N, rb, bw, bu, bs,
                                           st))
+
+    def ceil_read_pieces():
+        check_status(lib.klp_ceiling_read_pieces(src.data_ptr(), N, rb, bw, bu, bs,
+                                                 sink.data_ptr(), magic, st))
+
+    def ceil_write():
+        check_status(lib.klp_ceiling_write(dst.data_ptr(), N, rb, bw, bu, bs, st))
 
     tsrc = src.view(-1)[:N * rb // src.element_size()] if src is logits else src
     tdst = dst.view(-1)[:tsrc.numel()] if dst.dtype == tsrc.dtype else None
@@ -1068,38 +1146,126 @@ def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None):
     def torch_copy():
         tdst.copy_(tsrc)
 
-    for fn in (ceil_read, ceil_copy):
-        fn()
-    ceil = {"read_ms": kt.b2b(ceil_read), "copy_ms": kt.b2b(ceil_copy)}
-    ceil["read_ms_flushed"], _ = kt.flushed(ceil_read)
-    ceil["copy_ms_flushed"], _ = kt.flushed(ceil_copy)
+    kernels = {"fwd": (fwd, "klp_fwd_kernel"), "bwd": (bwd, "klp_bwd_kernel"),
+               "read": (ceil_read, "klp_ceiling_read_kernel"),
+               "copy": (ceil_copy, "klp_ceiling_copy_kernel"),
+               "read_pieces": (ceil_read_pieces, "klp_ceiling_read_pieces_kernel"),
+               "write": (ceil_write, "klp_ceiling_write_kernel")}
+    for key in ("read", "copy", "read_pieces", "write"):
+        kernels[key][0]()
+    warm = {k: (fwd_ms if k == "fwd" else bwd_ms if k == "bwd" else kt.b2b(fn))
+            for k, (fn, _) in kernels.items()}
+    device = {}
+    if dtimer is not None and dtimer.available:
+        for k, (fn, match) in kernels.items():
+            device[k] = dtimer.stats(fn, match)
+        flushed = {k: device[k]["flushed"]["ms"] for k in kernels}
+        flushed_each = {}
+        method = "device timestamps (torch.profiler): median over the launches, each right " \
+                 "after a flush"
+    else:
+        flushed, flushed_each = {}, {}
+        for k, (fn, _) in kernels.items():
+            flushed[k], flushed_each[k] = kt.flushed(fn)
+        method = "HIP events: (flush + launch) pairs minus flushes alone, median of rounds"
+    # The backward's writes restore d_logits for the callers below.
+    bwd()
     if tdst is not None:
         torch_copy()
-        ceil["torch_copy_ms"] = kt.b2b(torch_copy)
-        ceil["torch_copy_ms_flushed"], _ = kt.flushed(torch_copy)
+        warm["torch_copy"] = kt.b2b(torch_copy)
+        flushed["torch_copy"], _ = kt.flushed(torch_copy)
+    bwd()
     del sink
     if dst is not d_logits:
         del dst
     fb, bb = algorithmic_bytes(N, V, esz)
     rbytes = N * rb
+    nbytes = {"read": rbytes, "copy": 2 * rbytes, "read_pieces": rbytes, "write": rbytes,
+              "torch_copy": 2 * rbytes}
     out_ceil = {
-        "read_kernel": f"klp_ceiling_read, launch {dict(zip(('waves', 'unroll', 'splits'), fwd_used[:3]))}",
-        "copy_kernel": f"klp_ceiling_copy, launch {dict(zip(('waves', 'unroll', 'splits'), bwd_used[:3]))}",
+        "read_kernel": f"klp_ceiling_read (the forward's ring), launch "
+                       f"{dict(zip(('waves', 'unroll', 'splits'), fwd_used[:3]))}",
+        "copy_kernel": f"klp_ceiling_copy, klp_ceiling_read_pieces, klp_ceiling_write (the "
+                       f"backward's loop: copy, loads alone, stores alone), launch "
+                       f"{dict(zip(('waves', 'unroll', 'splits'), bwd_used[:3]))}",
         "buffer_bytes": rbytes,
+        "flushed_method": method,
     }
-    for k, v in ceil.items():
-        out_ceil[k] = round(v, 5)
-        nbytes = rbytes if k.startswith("read") else 2 * rbytes
-        out_ceil[k.replace("_ms", "_tbps")] = round(_tbps(nbytes, v), 4)
-    out_ceil["fwd_over_read"] = round(fwd_ms / ceil["read_ms"], 4)
-    out_ceil["bwd_over_copy"] = round(bwd_ms / ceil["copy_ms"], 4)
-    out_ceil["fwd_over_read_flushed"] = round(fwd_fl / ceil["read_ms_flushed"], 4)
-    out_ceil["bwd_over_copy_flushed"] = round(bwd_fl / ceil["copy_ms_flushed"], 4)
+    for k in nbytes:
+        if k not in warm:
+            continue
+        out_ceil[f"{k}_ms"] = round(warm[k], 5)
+        out_ceil[f"{k}_tbps"] = round(_tbps(nbytes[k], warm[k]), 4)
+        out_ceil[f"{k}_ms_flushed"] = round(flushed[k], 5)
+        out_ceil[f"{k}_tbps_flushed"] = round(_tbps(nbytes[k], flushed[k]), 4)
+    out_ceil["fwd_over_read"] = round(fwd_ms / warm["read"], 4)
+    out_ceil["bwd_over_copy"] = round(bwd_ms / warm["copy"], 4)
+    out_ceil["fwd_over_read_flushed"] = round(flushed["fwd"] / flushed["read"], 4)
+    out_ceil["bwd_over_copy_flushed"] = round(flushed["bwd"] / flushed["copy"], 4)
+    # A read+write stream whose reads and writes cannot overlap on the HBM
+    # bus takes the read-only plus the write-only time.
+    out_ceil["read_plus_write_ms"] = round(warm["read_pieces"] + warm["write"], 5)
+    out_ceil["read_plus_write_ms_flushed"] = round(flushed["read_pieces"] + flushed["write"], 5)
+    out_ceil["read_plus_write_pct_peak"] = round(
+        100 * _tbps(2 * rbytes, warm["read_pieces"] + warm["write"]) / HBM_PEAK_TBPS, 2)
+    out_ceil["bwd_over_read_plus_write"] = round(bwd_ms / (warm["read_pieces"] + warm["write"]), 4)
+    out_ceil["bwd_over_read_plus_write_flushed"] = round(
+        flushed["bwd"] / (flushed["read_pieces"] + flushed["write"]), 4)
     return dict(inputs=inp, logits=logits, targets=targets, g_logp=g_logp, g_ent=g_ent,
                 N=N, V=V, esz=esz, fb=fb, bb=bb, step_ms=step_ms, wall=t_wall, fwd_ms=fwd_ms,
-                bwd_ms=bwd_ms, fwd_fl=fwd_fl, fwd_fl_each=fwd_fl_each, bwd_fl=bwd_fl,
-                bwd_fl_each=bwd_fl_each, fwd_used=fwd_used, bwd_used=bwd_used, ceilings=out_ceil,
-                d_logits=d_logits)
+                bwd_ms=bwd_ms, fwd_fl=flushed["fwd"], fwd_fl_each=flushed_each.get("fwd"),
+                bwd_fl=flushed["bwd"], bwd_fl_each=flushed_each.get("bwd"), fwd_used=fwd_used,
+                bwd_used=bwd_used, ceilings=out_ceil, device_timed=device, d_logits=d_logits)
+
+
+def _device_summary(device):
+    """The DeviceTimer figures of core_timing in microseconds: median, the
+    interquartile spread in percent, and the count, warm and flushed."""
+    if not device:
+        return None
+    out = {}
+    for k, v in device.items():
+        out[k] = {mode: {"us": round(v[mode]["ms"] * 1e3, 2), "spread_pct": v[mode]["spread_pct"],
+                         "n": v[mode]["n"]} for mode in ("warm", "flushed")}
+    return out
+
+
+def config_legs(names, dev, K, warmup, timer, dtimer):
+    """The other BASELINE configs beside the headline, each through
+    core_timing at its own size and default launch shapes: forward and
+    backward, warm and flushed, with the read / copy / read-only / write-only
+    ceilings at that shape.  Inputs are freed before the next config."""
+    out = {}
+    for name in names:
+        print(f"bench.py: config {name}", file=sys.stderr, flush=True)
+        core = core_timing(name, dev, min(K, 20), min(warmup, 3), timer, dtimer=dtimer)
+        cfg = CONFIGS[name]
+        B, S, V = cfg["shape"]
+        fb, bb = core["fb"], core["bb"]
+        c = core["ceilings"]
+        r = {
+            "workload": f"{name}: logits [{B},{S},{V}] {str(cfg['dtype']).replace('torch.', '')}"
+                        + (", rows strided (parent[:, :-1, :])" if "parent_len" in cfg else ""),
+            "fwd_us": round(core["fwd_ms"] * 1e3, 2),
+            "bwd_us": round(core["bwd_ms"] * 1e3, 2),
+            "step_us": round(core["step_ms"] * 1e3, 2),
+            "fwd_us_flushed": round(core["fwd_fl"] * 1e3, 2),
+            "bwd_us_flushed": round(core["bwd_fl"] * 1e3, 2),
+            "fwd_pct_peak": round(100 * _tbps(fb, core["fwd_ms"]) / HBM_PEAK_TBPS, 2),
+            "bwd_pct_peak": round(100 * _tbps(bb, core["bwd_ms"]) / HBM_PEAK_TBPS, 2),
+            "fwd_pct_peak_flushed": round(100 * _tbps(fb, core["fwd_fl"]) / HBM_PEAK_TBPS, 2),
+            "bwd_pct_peak_flushed": round(100 * _tbps(bb, core["bwd_fl"]) / HBM_PEAK_TBPS, 2),
+            "step_tbps": round(_tbps(fb + bb, core["step_ms"]), 4),
+            "fwd_launch": dict(zip(("waves", "unroll", "splits", "flags"), core["fwd_used"])),
+            "bwd_launch": dict(zip(("waves", "unroll", "splits", "flags"), core["bwd_used"])),
+            "ceilings": {k: v for k, v in c.items() if not k.endswith("_kernel")},
+            "device_timed": _device_summary(core["device_timed"]),
+        }
+        out[name] = r
+        del core
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
 
 
 def autograd_timing(dev, K, logits, targets, g_logp, g_ent):
@@ -1395,6 +1561,11 @@ def main(argv=None):
     ap.add_argument("--command", default="",
                     help="the profiling command, quoted in the --trace-from / --traffic-from "
                          "summary")
+    ap.add_argument("--no-device-timer", action="store_true",
+                    help="time flushed launches with HIP events instead of the device's "
+                         "timestamps through torch.profiler (for runs under rocprofv3)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config legs (C3, C4, C5 beside the headline C2)")
     ap.add_argument("--label", default=None,
                     help="tag of a --trace-from summary other than the config name (a run "
                          "that is not --core-only)")
@@ -1427,7 +1598,8 @@ def main(argv=None):
 
     fcfg = tuple(int(v) for v in args.fwd_config.split(",")) if args.fwd_config else None
     bcfg = tuple(int(v) for v in args.bwd_config.split(",")) if args.bwd_config else None
-    core = core_timing(name, dev, K, args.warmup, timer, fcfg, bcfg)
+    dtimer = DeviceTimer(timer, enabled=not args.no_device_timer)
+    core = core_timing(name, dev, K, args.warmup, timer, fcfg, bcfg, dtimer)
     N, V, fb, bb = core["N"], core["V"], core["fb"], core["bb"]
     step_ms, fwd_ms, bwd_ms = core["step_ms"], core["fwd_ms"], core["bwd_ms"]
     fwd_fl, bwd_fl = core["fwd_fl"], core["bwd_fl"]
@@ -1461,6 +1633,10 @@ def main(argv=None):
         if c1 is not None and "cpu_fwd_bwd_ms" in c1:
             cpu["C1"] = {"fwd_ms": c1["cpu_fwd_ms"], "fwd_bwd_ms": c1["cpu_fwd_bwd_ms"],
                          "cores": c1["cpu_threads"]}
+
+    per_config = None
+    if extra and not args.no_configs and name == "C2":
+        per_config = config_legs(("C3", "C4", "C5"), dev, K, args.warmup, timer, dtimer)
 
     grpo = step = lmhead = shard = None
     if extra:
@@ -1519,8 +1695,7 @@ def main(argv=None):
         "bwd_ms": round(bwd_ms, 5),
         "fwd_ms_flushed": round(fwd_fl, 5),
         "bwd_ms_flushed": round(bwd_fl, 5),
-        "fwd_ms_flushed_each": round(core["fwd_fl_each"], 5),
-        "bwd_ms_flushed_each": round(core["bwd_fl_each"], 5),
+        "device_timed": _device_summary(core["device_timed"]),
         "fwd_tbps": round(fwd_tbps, 4),
         "bwd_tbps": round(bwd_tbps, 4),
         "fwd_pct_peak": round(100 * fwd_tbps / HBM_PEAK_TBPS, 2),
@@ -1550,6 +1725,7 @@ def main(argv=None):
         },
         "autograd": autograd,
         "C1": c1,
+        "configs": per_config,
         "small_batch": small,
         "cpu_baseline": cpu,
         "grpo_loss": grpo,

@@ -459,28 +459,40 @@ size_t lmh_workspace_bytes(int64_t n_tokens, int64_t vocab) {
     return static_cast<size_t>(nc) * static_cast<size_t>(n_tokens) * 4 * sizeof(float);
 }
 
-int ceiling_impl(bool copy, const void* src, void* dst, int64_t n_rows, int64_t row_bytes,
+int ceiling_impl(int mode, const void* src, void* dst, int64_t n_rows, int64_t row_bytes,
                  int waves, int unroll, int splits, uint32_t* sink, uint32_t magic,
                  void* stream) {
-    const char* what = copy ? "ceiling copy" : "ceiling read";
+    static const char* const kWhat[] = {"ceiling read", "ceiling copy", "ceiling read pieces",
+                                        "ceiling write"};
+    const char* what = kWhat[mode];
+    const bool reads = mode != klp::kCeilWrite;
+    const bool writes = mode == klp::kCeilCopy || mode == klp::kCeilWrite;
+    const bool folds = mode == klp::kCeilRead || mode == klp::kCeilReadPieces;
     if (n_rows < 0) return fail(KLP_EINVAL, "n_rows must be >= 0");
     if (row_bytes < 16 || row_bytes % 16 != 0)
         return fail(KLP_EINVAL, "row_bytes must be a positive multiple of 16, got %lld",
                     static_cast<long long>(row_bytes));
     if (n_rows == 0) return ok();
-    if (src == nullptr || !aligned(src, 16))
+    if (reads && (src == nullptr || !aligned(src, 16)))
         return fail(KLP_EINVAL, "src must be non-null and 16-byte aligned");
-    if (copy && (dst == nullptr || !aligned(dst, 16)))
+    if (writes && (dst == nullptr || !aligned(dst, 16)))
         return fail(KLP_EINVAL, "dst must be non-null and 16-byte aligned");
-    if (!copy && (sink == nullptr || !aligned(sink, 4)))
+    if (folds && (sink == nullptr || !aligned(sink, 4)))
         return fail(KLP_EINVAL, "sink must be non-null and 4-byte aligned");
     const bool w = (waves == 1 || waves == 2 || waves == 4 || waves == 8 || waves == 16);
     if (!w || (unroll != 2 && unroll != 4) || splits < 1 || splits > 1024)
         return fail(KLP_EINVAL, "unsupported launch shape (waves=%d unroll=%d splits=%d)", waves,
                     unroll, splits);
-    const int64_t per = ((row_bytes / 16 + splits - 1) / splits + 7) / 8 * 8 * 16;
-    if (copy && per > int64_t{INT32_MAX})
+    const int64_t nvec = row_bytes / 16;
+    if (mode == klp::kCeilRead) {
+        // the ring's buffer offsets: the piece plus the prefetched chunks
+        const int64_t per = (nvec + splits - 1) / splits;
+        const int64_t ahead = int64_t{klp::kFwdRing} * unroll * waves * 64;
+        if ((per + ahead) * 16 > int64_t{INT32_MAX})
+            return fail(KLP_EINVAL, "row pieces must be under 2 GiB: use more splits");
+    } else if (((nvec + splits - 1) / splits + 7) / 8 * 8 * 16 > int64_t{INT32_MAX}) {
         return fail(KLP_EINVAL, "row pieces must be under 2 GiB: use more splits");
+    }
     int rc;
     if ((rc = check_grid(n_rows, splits, waves * 64)) != KLP_OK) return rc;
     klp::CeilingParams p;
@@ -493,7 +505,7 @@ int ceiling_impl(bool copy, const void* src, void* dst, int64_t n_rows, int64_t 
     p.magic = magic;
     if (injected_failure(what)) return KLP_ELAUNCH;
     return after_launch(
-        klp::launch_ceiling(copy, p, waves, unroll, static_cast<hipStream_t>(stream)), what);
+        klp::launch_ceiling(mode, p, waves, unroll, static_cast<hipStream_t>(stream)), what);
 }
 
 // Device address of `scratch` on the current device, looked up once per
@@ -1035,14 +1047,27 @@ int klp_lmh_fwd(const void* hidden, int64_t ld_hidden, const void* weight, int64
 
 int klp_ceiling_read(const void* src, int64_t n_rows, int64_t row_bytes, int waves, int unroll,
                      int splits, uint32_t* sink, uint32_t magic, void* stream) {
-    return ceiling_impl(false, src, nullptr, n_rows, row_bytes, waves, unroll, splits, sink,
-                        magic, stream);
+    return ceiling_impl(klp::kCeilRead, src, nullptr, n_rows, row_bytes, waves, unroll, splits,
+                        sink, magic, stream);
 }
 
 int klp_ceiling_copy(const void* src, void* dst, int64_t n_rows, int64_t row_bytes, int waves,
                      int unroll, int splits, void* stream) {
-    return ceiling_impl(true, src, dst, n_rows, row_bytes, waves, unroll, splits, nullptr, 0,
-                        stream);
+    return ceiling_impl(klp::kCeilCopy, src, dst, n_rows, row_bytes, waves, unroll, splits,
+                        nullptr, 0, stream);
+}
+
+int klp_ceiling_read_pieces(const void* src, int64_t n_rows, int64_t row_bytes, int waves,
+                            int unroll, int splits, uint32_t* sink, uint32_t magic,
+                            void* stream) {
+    return ceiling_impl(klp::kCeilReadPieces, src, nullptr, n_rows, row_bytes, waves, unroll,
+                        splits, sink, magic, stream);
+}
+
+int klp_ceiling_write(void* dst, int64_t n_rows, int64_t row_bytes, int waves, int unroll,
+                      int splits, void* stream) {
+    return ceiling_impl(klp::kCeilWrite, nullptr, dst, n_rows, row_bytes, waves, unroll, splits,
+                        nullptr, 0, stream);
 }
 
 int klp_fwd_noalloc(const void* logits, int dtype, int64_t n_rows, int64_t vocab,

@@ -219,17 +219,19 @@ hipError_t launch_lmh_dlogits(const LmhParams& p, hipStream_t stream);
 
 // Calibration kernels (klp_ceiling.hip): rows of `row_bytes` (a multiple of
 // 16) at `src` (and `dst`), 16-byte aligned and contiguous; `splits`
-// workgroups per row.
+// workgroups per row.  Modes: the forward's ring read, and the backward's
+// loop as a copy, its loads alone and its stores alone.
+enum : int { kCeilRead = 0, kCeilCopy = 1, kCeilReadPieces = 2, kCeilWrite = 3 };
 struct CeilingParams {
-    const void* src;
-    void* dst;           // copy only
+    const void* src;     // all modes but kCeilWrite
+    void* dst;           // kCeilCopy, kCeilWrite
     int64_t n_rows;
     int64_t row_bytes;
     int64_t splits;
-    uint32_t* sink;      // read only: [n_rows * splits], written when fold == magic
+    uint32_t* sink;      // reads: [n_rows * splits], written when fold == magic
     uint32_t magic;
 };
-hipError_t launch_ceiling(bool copy, const CeilingParams& p, int waves, int unroll,
+hipError_t launch_ceiling(int mode, const CeilingParams& p, int waves, int unroll,
                           hipStream_t stream);
 
 hipError_t launch_fwd(int dtype, const FwdParams& p, const FwdConfig& c, hipStream_t stream);

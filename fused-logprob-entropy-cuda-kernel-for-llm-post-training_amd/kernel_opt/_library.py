@@ -84,6 +84,9 @@ SIGNATURES = {
     "klp_default_config": (None, [_i32, _i32, _i64, _i64] + [ctypes.POINTER(_i32)] * 4),
     "klp_ceiling_read": (_i32, [_vp, _i64, _i64, _i32, _i32, _i32, _vp, ctypes.c_uint32, _vp]),
     "klp_ceiling_copy": (_i32, [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp]),
+    "klp_ceiling_read_pieces": (_i32, [_vp, _i64, _i64, _i32, _i32, _i32, _vp, ctypes.c_uint32,
+                                       _vp]),
+    "klp_ceiling_write": (_i32, [_vp, _i64, _i64, _i32, _i32, _i32, _vp]),
 }
 
 

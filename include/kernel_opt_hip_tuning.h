@@ -65,27 +65,41 @@ int64_t klp_grpo_step_persistent_min_rows(int dtype, int64_t vocab, int scaled);
 
 /*
  * Calibration kernels: the memory access of klp_fwd (klp_ceiling_read) and
- * of klp_bwd (klp_ceiling_copy) without their arithmetic, for measuring the
- * read and copy rates this device reaches at the same size and launch shape.
- * No counterpart in the reference, whose roofline is priced against the
- * device's nominal peak (bench/plot_roofline.py, bench/ncu_parse.py:183-212).
+ * of klp_bwd (klp_ceiling_copy; its loads alone, klp_ceiling_read_pieces;
+ * its stores alone, klp_ceiling_write) without their arithmetic, for
+ * measuring the read, copy, read-only and write-only rates this device
+ * reaches at the same size and launch shape.  No counterpart in the
+ * reference, whose roofline is priced against the device's nominal peak
+ * (bench/plot_roofline.py, bench/ncu_parse.py:183-212).
  *
  * `src` (and `dst`) hold n_rows contiguous rows of `row_bytes` bytes (a
  * positive multiple of 16), 16-byte aligned.  waves in {1, 2, 4, 8, 16},
  * unroll in {2, 4}, splits in [1, 1024] workgroups per row.
  *
- * klp_ceiling_read streams every row piece with non-temporal 16-byte loads
- * (as the forward does) and xor-folds the words; a workgroup writes its fold
- * to sink[workgroup] (n_rows * splits uint32) only when it equals `magic`.
+ * klp_ceiling_read streams every row piece (ceil(row / splits) 16-byte
+ * vectors) through the forward's ring: unroll non-temporal 16-byte buffer
+ * loads per thread per chunk, two chunks in flight ahead of the one being
+ * folded, as klp_fwd loads them.  It xor-folds the words; a workgroup
+ * writes its fold to sink[workgroup] (n_rows * splits uint32) only when it
+ * equals `magic`.
  * klp_ceiling_copy copies src to dst with ordinary 16-byte loads and
- * non-temporal 16-byte stores, pieces rounded up to 8 vectors (as the
- * backward does); pieces must stay under 2 GiB.
+ * non-temporal 16-byte stores, pieces rounded up to 8 vectors, unroll loads
+ * then unroll stores per thread per iteration (as klp_bwd does); pieces
+ * must stay under 2 GiB.
+ * klp_ceiling_read_pieces runs the same loop with the loads alone (folded
+ * into `sink` as klp_ceiling_read does); klp_ceiling_write with the stores
+ * alone (each 16-byte vector of dst gets its index within the row).
  */
 int klp_ceiling_read(const void* src, int64_t n_rows, int64_t row_bytes,
                      int waves, int unroll, int splits,
                      uint32_t* sink, uint32_t magic, void* stream);
 int klp_ceiling_copy(const void* src, void* dst, int64_t n_rows, int64_t row_bytes,
                      int waves, int unroll, int splits, void* stream);
+int klp_ceiling_read_pieces(const void* src, int64_t n_rows, int64_t row_bytes,
+                            int waves, int unroll, int splits,
+                            uint32_t* sink, uint32_t magic, void* stream);
+int klp_ceiling_write(void* dst, int64_t n_rows, int64_t row_bytes,
+                      int waves, int unroll, int splits, void* stream);
 
 #ifdef __cplusplus
 }

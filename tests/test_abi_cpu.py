@@ -433,8 +433,9 @@ def test_scale_inplace_validation_errors():
 
 
 def test_ceiling_validation_errors():
-    """klp_ceiling_read / klp_ceiling_copy reject bad arguments before any
-    launch; n_rows = 0 is a no-op; an injected launch failure is reported."""
+    """klp_ceiling_read / _copy / _read_pieces / _write reject bad arguments
+    before any launch; n_rows = 0 is a no-op; an injected launch failure is
+    reported."""
     from kernel_opt._library import KLP_EINVAL, KLP_ELAUNCH, lib
     A = ctypes.c_void_p(0x100000)
 
@@ -460,6 +461,25 @@ def test_ceiling_validation_errors():
     assert copy(u=8) == KLP_EINVAL and "launch shape" in _err()
     assert copy(sp=0) == KLP_EINVAL and "launch shape" in _err()
     assert copy(n=1, rb=(1 << 31) + 16, sp=1) == KLP_EINVAL and "2 GiB" in _err()
+    assert read(n=1, rb=(1 << 31) - 16, sp=1) == KLP_EINVAL and "2 GiB" in _err()
+
+    def pieces(**kw):
+        a = dict(src=A, n=4, rb=4096, w=8, u=2, sp=16, sink=A)
+        a.update(kw)
+        return lib.klp_ceiling_read_pieces(a["src"], a["n"], a["rb"], a["w"], a["u"], a["sp"],
+                                           a["sink"], 7, None)
+
+    def write(**kw):
+        a = dict(dst=A, n=4, rb=4096, w=8, u=2, sp=16)
+        a.update(kw)
+        return lib.klp_ceiling_write(a["dst"], a["n"], a["rb"], a["w"], a["u"], a["sp"], None)
+    assert pieces(n=0, src=None, sink=None) == 0 and write(n=0, dst=None) == 0
+    assert pieces(src=None) == KLP_EINVAL and "src" in _err()
+    assert pieces(sink=None) == KLP_EINVAL and "sink" in _err()
+    assert write(dst=ctypes.c_void_p(0x100004)) == KLP_EINVAL and "dst" in _err()
+    assert write(rb=8) == KLP_EINVAL and "multiple of 16" in _err()
+    assert write(w=32) == KLP_EINVAL and "launch shape" in _err()
+    assert pieces(n=1, rb=(1 << 31) + 16, sp=1) == KLP_EINVAL and "2 GiB" in _err()
     lib.klp_debug_fail_next_launches(1)
     try:
         assert copy() == KLP_ELAUNCH and "ceiling copy" in _err()
