@@ -1523,6 +1523,295 @@ def sweep(name, dev, K, timer, out_md):
         fh.write("\n".join(lines) + "\n")
 
 
+# ---------------------------------------------------------------------------
+# The reference's comparison matrix on this device (bench/bench_micro.py:
+# 95-122, shapes of docs/FINAL_REPORT.md:298-314; bench/bench_backward.py;
+# traffic multiples of REPORT.md:157-177).  The eager baselines are the
+# reference's own, restated here as GPU baselines to be timed (the restatement
+# in oracle/eager_ref.py is test infrastructure, used as a checker and by the
+# CPU baseline leg only).
+# ---------------------------------------------------------------------------
+def _trl_selective_log_softmax(logits, index):
+    """TRL 1.4's selective_log_softmax as the reference describes it
+    (REPORT.md:19-30): gather minus a per-row logsumexp for fp32 / fp64, a
+    per-batch-element log_softmax + gather loop otherwise."""
+    import torch.nn.functional as F
+    if logits.dtype in (torch.float32, torch.float64):
+        sel = torch.gather(logits, dim=-1, index=index.unsqueeze(-1)).squeeze(-1)
+        return sel - torch.stack([torch.logsumexp(lg, dim=-1) for lg in logits])
+    out = []
+    for row_logits, row_labels in zip(logits, index):
+        lp = F.log_softmax(row_logits, dim=-1)
+        out.append(lp.gather(dim=-1, index=row_labels.unsqueeze(-1)).squeeze(-1))
+    return torch.stack(out)
+
+
+def _trl_entropy_from_logits(logits, chunk_size=128):
+    """TRL 1.4's entropy_from_logits: 128-row chunks of log_softmax, exp,
+    multiply, sum (notes/stage1_findings.md:38-60 of the reference)."""
+    import torch.nn.functional as F
+    flat = logits.reshape(-1, logits.shape[-1])
+    ents = []
+    for chunk in flat.split(chunk_size, dim=0):
+        lp = F.log_softmax(chunk, dim=-1)
+        ents.append(-(torch.exp(lp) * lp).sum(-1))
+    return torch.cat(ents, dim=0).reshape(logits.shape[:-1])
+
+
+def _trl_eager(logits, targets):
+    return _trl_selective_log_softmax(logits, targets), _trl_entropy_from_logits(logits)
+
+
+def _pytorch_separate(logits, targets):
+    import torch.nn.functional as F
+    lp = F.log_softmax(logits, dim=-1)
+    logp = lp.gather(-1, targets.unsqueeze(-1)).squeeze(-1)
+    return logp, -(lp.exp() * lp).sum(-1)
+
+
+def _eager_reference(logits, targets):
+    """The differentiable eager forward of the reference's backward bench
+    (bench/bench_backward.py:19-26)."""
+    import torch.nn.functional as F
+    lp = F.log_softmax(logits, dim=-1)
+    logp = lp.gather(-1, targets.unsqueeze(-1)).squeeze(-1)
+    ent = -(lp.exp() * lp).sum(-1)
+    return logp, ent, torch.logsumexp(logits, dim=-1)
+
+
+MATRIX_SHAPES = ((256, 32000), (1024, 32000), (4096, 32000), (256, 128256), (1024, 128256),
+                 (1024, 152064))
+MATRIX_BWD_SHAPES = ((256, 32000), (1024, 128256), (1024, 152064), (4096, 32000))
+MATRIX_TRAFFIC_SHAPE = (1024, 128256)
+
+
+def _matrix_inputs(BS, V, dev, seed=0):
+    g = _gen(dev, seed)
+    x = torch.randn(1, BS, V, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    t = torch.randint(0, V, (1, BS), generator=g, device=dev, dtype=torch.int64)
+    return x, t
+
+
+def _matrix_backends():
+    import kernel_opt
+    return {
+        "ours": lambda x, t: kernel_opt.fused_logprob_entropy(x, t),
+        "ours_naive": lambda x, t: kernel_opt.fused_logprob_entropy_naive(x, t),
+        "trl_eager": _trl_eager,
+        "pytorch_separate": _pytorch_separate,
+    }
+
+
+def _per_call_ms(fn, n_warmup=5, n_iter=30):
+    """The reference's timing (bench/bench_micro.py:56-75): an event pair
+    around each call, median of n_iter after n_warmup; peak allocation
+    during the calls minus before, MB."""
+    for _ in range(n_warmup):
+        out = fn()
+        del out
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    pre = torch.cuda.memory_allocated()
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(n_iter)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(n_iter)]
+    for i in range(n_iter):
+        st[i].record()
+        out = fn()
+        en[i].record()
+    torch.cuda.synchronize()
+    del out
+    ts = sorted(a.elapsed_time(b) for a, b in zip(st, en))
+    return ts[len(ts) // 2], (torch.cuda.max_memory_allocated() - pre) / 2 ** 20
+
+
+def matrix(dev, out_md, dtimer):
+    """Forward latency of the reference's four backends over its six shapes
+    (bf16, B = 1), each the reference's way; our kernels' device time beside
+    it; then the backward against eager autograd (bench/bench_backward.py's
+    method: events around loss.backward(), median of 20 after 5)."""
+    backends = _matrix_backends()
+    rows = {}
+    for BS, V in MATRIX_SHAPES:
+        x, t = _matrix_inputs(BS, V, dev)
+        r = {}
+        for name, fn in backends.items():
+            ms, mb = _per_call_ms(lambda: fn(x, t))
+            r[name] = {"ms": round(ms, 4), "alloc_mb": round(mb, 1),
+                       "gbps": round(x.numel() * 2 / (ms * 1e-3) / 1e9, 1)}
+        if dtimer is not None and dtimer.available:
+            dt = dtimer.stats(lambda: backends["ours"](x, t), "klp_fwd_kernel", n=16)
+            r["ours"]["kernel_us_warm"] = round(dt["warm"]["ms"] * 1e3, 2)
+            r["ours"]["kernel_us_flushed"] = round(dt["flushed"]["ms"] * 1e3, 2)
+            dn = dtimer.stats(lambda: backends["ours_naive"](x, t), "klp_fwd_naive_kernel", n=8)
+            r["ours_naive"]["kernel_us_warm"] = round(dn["warm"]["ms"] * 1e3, 2)
+        rows[(BS, V)] = r
+        print(f"bench.py: matrix forward {BS}x{V}: " +
+              ", ".join(f"{k} {v['ms']:.3f} ms" for k, v in r.items()), file=sys.stderr,
+              flush=True)
+        del x, t
+        torch.cuda.empty_cache()
+    bwd = {}
+    import kernel_opt
+    for BS, V in MATRIX_BWD_SHAPES:
+        base, t = _matrix_inputs(BS, V, dev, seed=1)
+        g = _gen(dev, 7)
+        gl, ge, gs = (torch.randn(1, BS, generator=g, device=dev) for _ in range(3))
+        res = {}
+        for name, fwd in (("eager_autograd", _eager_reference),
+                          ("ours", kernel_opt.fused_logprob_entropy)):
+            times = []
+            for i in range(25):
+                x = base.clone().requires_grad_(True)
+                lp, ent, lse = fwd(x, t)
+                loss = (lp * gl + ent * ge + lse * gs).sum()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                a.record()
+                loss.backward()
+                b.record()
+                torch.cuda.synchronize()
+                if i >= 5:
+                    times.append(a.elapsed_time(b))
+                del x, lp, ent, lse, loss
+            res[name] = round(statistics.median(times), 4)
+        bwd[(BS, V)] = res
+        print(f"bench.py: matrix backward {BS}x{V}: {res}", file=sys.stderr, flush=True)
+        del base, t
+        torch.cuda.empty_cache()
+    bid = build_id()
+    md = ["# The reference's comparison matrix on one MI355X", "",
+          f"`python bench.py --matrix {out_md}` (build `{bid}`, git `{_git_head()}`). bf16 "
+          "logits `[1, B*S, V]` ~ N(0, 1), targets uniform, as the reference's "
+          "`bench/bench_micro.py:167-169` draws them. Backends as the reference defines them "
+          "(`bench/bench_micro.py:95-122`): `ours` = `kernel_opt.fused_logprob_entropy`, "
+          "`ours_naive` = `fused_logprob_entropy_naive` (one thread per row), `trl_eager` = "
+          "TRL's `selective_log_softmax` + `entropy_from_logits` (restated in `bench.py`; TRL is "
+          "not installed), `pytorch_separate` = `F.log_softmax` + gather + `-(p log p).sum`. "
+          "Timing as the reference's: a HIP-event pair around each call (host launch "
+          "included), median of 30 after 5 warm-ups; `kernel` = our kernel's own duration "
+          "from the device's timestamps, back to back and after a 1 GiB flush.", "",
+          "Forward, ms (and GB/s of one pass over the logits):", "",
+          "| (B*S, V) | TRL eager | PyTorch sep. | naive | **ours** | ours kernel, warm / "
+          "flushed | speedup vs TRL | peak alloc MB (TRL / ours) |",
+          "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for (BS, V), r in rows.items():
+        md.append(f"| ({BS}, {V}) | {r['trl_eager']['ms']:.3f} | "
+                  f"{r['pytorch_separate']['ms']:.3f} | {r['ours_naive']['ms']:.3f} | "
+                  f"**{r['ours']['ms']:.3f}** ({r['ours']['gbps']:.0f}) | "
+                  f"{r['ours'].get('kernel_us_warm', '-')} / "
+                  f"{r['ours'].get('kernel_us_flushed', '-')} us | "
+                  f"**{r['trl_eager']['ms'] / r['ours']['ms']:.1f}x** | "
+                  f"{r['trl_eager']['alloc_mb']:.0f} / {r['ours']['alloc_mb']:.1f} |")
+    md += ["", "Backward (`loss.backward()` of `(logp*g_logp + ent*g_ent + lse*g_lse).sum()`, "
+           "the reference's `bench/bench_backward.py` method: events around the backward, "
+           "median of 20 after 5), ms:", "",
+           "| (B*S, V) | eager autograd | **ours** | speedup |", "|---|---:|---:|---:|"]
+    for (BS, V), r in bwd.items():
+        md.append(f"| ({BS}, {V}) | {r['eager_autograd']:.3f} | **{r['ours']:.3f}** | "
+                  f"**{r['eager_autograd'] / r['ours']:.1f}x** |")
+    data = {"kind": "matrix", "build_id": bid,
+            "forward": {f"{k[0]}x{k[1]}": v for k, v in rows.items()},
+            "backward": {f"{k[0]}x{k[1]}": v for k, v in bwd.items()}}
+    md += ["", _profile_line(data), ""]
+    with open(out_md, "w") as f:
+        f.write("\n".join(md))
+    print("\n".join(md))
+
+
+MATRIX_TRAFFIC_BACKENDS = ("ours_fwd", "ours_bwd", "ours_naive", "trl_eager", "pytorch_separate")
+
+
+def matrix_run(dev):
+    """One call of each backend at MATRIX_TRAFFIC_SHAPE for rocprofv3 --pmc
+    (FETCH_SIZE, then WRITE_SIZE): first klp_ceiling_copy over the logits'
+    bytes (the counters' calibration), then for backend i a marker,
+    klp_ceiling_write over one row of 16 * (i + 1) bytes, and the backend's
+    call; a last marker closes the sequence.  Warm-up calls run before the
+    first marker."""
+    from kernel_opt import _C
+    from kernel_opt._library import check_status, lib
+    BS, V = MATRIX_TRAFFIC_SHAPE
+    x, t = _matrix_inputs(BS, V, dev)
+    N = BS
+    lp, ent, lse = (torch.empty(N, device=dev) for _ in range(3))
+    d = torch.empty(x.shape, dtype=x.dtype, device=dev)
+    g = torch.full((N,), 1.0 / N, device=dev)
+    mk = torch.empty(4096, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    b = _matrix_backends()
+    calls = {
+        "ours_fwd": lambda: _C.fwd_launch(x, t, lp, ent, lse),
+        "ours_bwd": lambda: _C.bwd_launch(x, t, lse, ent, g, g, None, d),
+        "ours_naive": lambda: b["ours_naive"](x, t),
+        "trl_eager": lambda: b["trl_eager"](x, t),
+        "pytorch_separate": lambda: b["pytorch_separate"](x, t),
+    }
+    for name in MATRIX_TRAFFIC_BACKENDS:
+        calls[name]()
+    torch.cuda.synchronize()
+    check_status(lib.klp_ceiling_copy(x.data_ptr(), d.data_ptr(), N, V * 2, 8, 2, 16, st))
+    for i, name in enumerate(MATRIX_TRAFFIC_BACKENDS):
+        check_status(lib.klp_ceiling_write(mk.data_ptr(), 1, 16 * (i + 1), 1, 2, 1, st))
+        calls[name]()
+    check_status(lib.klp_ceiling_write(mk.data_ptr(), 1, 16 * (len(calls) + 1), 1, 2, 1, st))
+    torch.cuda.synchronize()
+    print(json.dumps({"matrix_run": MATRIX_TRAFFIC_SHAPE, "backends": MATRIX_TRAFFIC_BACKENDS}))
+
+
+def summarize_matrix_traffic(fetch_dir, write_dir, command=""):
+    """Bytes each backend of matrix_run moves: the FETCH_SIZE and WRITE_SIZE
+    of every dispatch between its marker and the next, scaled by the
+    calibration copy's known bytes.  Returns (markdown, data)."""
+    BS, V = MATRIX_TRAFFIC_SHAPE
+    logits_bytes = BS * V * 2
+    totals, counts, factor = {}, {}, {}
+    for counter, directory in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        recs = [r for r in _rocprof_csv(directory, "counter_collection.csv")
+                if r["Counter_Name"] == counter]
+        recs.sort(key=lambda r: int(r.get("Dispatch_Id") or r.get("Correlation_Id") or 0))
+        cal = [r for r in recs if "klp_ceiling_copy_kernel" in r["Kernel_Name"]]
+        if not cal:
+            raise RuntimeError("no calibration copy in " + directory)
+        factor[counter] = logits_bytes / (1024 * float(cal[-1]["Counter_Value"]))
+        start = recs.index(cal[-1]) + 1
+        cur = None
+        for r in recs[start:]:
+            if "klp_ceiling_write_kernel" in r["Kernel_Name"]:
+                cur = len([k for k in totals if k[0] == counter])
+                cur = MATRIX_TRAFFIC_BACKENDS[cur] if cur < len(MATRIX_TRAFFIC_BACKENDS) else None
+                if cur is not None:
+                    totals[(counter, cur)] = 0.0
+                    counts[(counter, cur)] = 0
+                continue
+            if cur is not None:
+                totals[(counter, cur)] += float(r["Counter_Value"]) * 1024 * factor[counter]
+                counts[(counter, cur)] += 1
+    rows, data = [], {}
+    for name in MATRIX_TRAFFIC_BACKENDS:
+        fe, wr = totals[("FETCH_SIZE", name)], totals[("WRITE_SIZE", name)]
+        need = 2 * logits_bytes if name == "ours_bwd" else logits_bytes
+        data[name] = {"dispatches": counts[("FETCH_SIZE", name)], "read_bytes": int(fe),
+                      "write_bytes": int(wr), "required_bytes": need,
+                      "amplification": round((fe + wr) / need, 3)}
+        rows.append(f"| {name} | {counts[('FETCH_SIZE', name)]} | {need / 1e6:.1f} MB | "
+                    f"{(fe + wr) / 1e6:.1f} MB (read {fe / 1e6:.1f}, write {wr / 1e6:.1f}) | "
+                    f"**{(fe + wr) / need:.2f}x** |")
+    md = [f"# Bytes moved per call, (B*S, V) = ({BS}, {V}) bf16, one MI355X", "",
+          "rocprofv3 FETCH_SIZE and WRITE_SIZE of every dispatch of each backend "
+          "(`bench.py --matrix-run`, dispatches grouped between marker launches), scaled by "
+          f"the counters' reading for a copy of known size (FETCH x{factor['FETCH_SIZE']:.5f}, "
+          f"WRITE x{factor['WRITE_SIZE']:.5f}); summarised by `python bench.py "
+          f"--matrix-traffic-from {fetch_dir} {write_dir}`. The reference's table: "
+          "`REPORT.md:157-177` (RTX 4060, ncu).", ""]
+    if command:
+        md += ["Commands (MI355X):", "```", command, "```", ""]
+    md += ["| backend | dispatches | bytes required | bytes moved | amplification |",
+           "|---|---:|---:|---:|---:|"] + rows
+    data = {"kind": "matrix_traffic", "build_id": build_id(), "backends": data}
+    md += ["", _profile_line(data), ""]
+    return "\n".join(md), data
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -1566,6 +1855,15 @@ def main(argv=None):
                          "timestamps through torch.profiler (for runs under rocprofv3)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-config legs (C3, C4, C5 beside the headline C2)")
+    ap.add_argument("--matrix", metavar="OUT_MD", default=None,
+                    help="the reference's comparison matrix (forward backends over its six "
+                         "shapes, backward against eager autograd) into OUT_MD")
+    ap.add_argument("--matrix-run", action="store_true",
+                    help="one call of each matrix backend between markers, for rocprofv3 "
+                         "--pmc runs")
+    ap.add_argument("--matrix-traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    default=None, help="bytes moved per backend from two rocprofv3 --pmc runs "
+                                       "of --matrix-run (markdown to stdout; no GPU needed)")
     ap.add_argument("--label", default=None,
                     help="tag of a --trace-from summary other than the config name (a run "
                          "that is not --core-only)")
@@ -1577,6 +1875,10 @@ def main(argv=None):
         return 0
     if args.traffic_from:
         md, _ = summarize_traffic(*args.traffic_from, args.config, args.command)
+        print(md)
+        return 0
+    if args.matrix_traffic_from:
+        md, _ = summarize_matrix_traffic(*args.matrix_traffic_from, args.command)
         print(md)
         return 0
 
@@ -1594,6 +1896,12 @@ def main(argv=None):
     timer = Timer(dev, K, args.flush_mode)
     if args.sweep:
         sweep(name, dev, K, timer, args.sweep)
+        return 0
+    if args.matrix:
+        matrix(dev, args.matrix, DeviceTimer(timer, enabled=not args.no_device_timer))
+        return 0
+    if args.matrix_run:
+        matrix_run(dev)
         return 0
 
     fcfg = tuple(int(v) for v in args.fwd_config.split(",")) if args.fwd_config else None

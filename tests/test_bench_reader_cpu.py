@@ -156,3 +156,43 @@ def test_labelled_trace_is_not_the_configs(tmp_path, monkeypatch):
     monkeypatch.setattr(bench, "PROFILES_DIR", str(prof))
     assert bench.load_profiles("trace", "C2", bench.build_id()) == []
     assert len(bench.load_profiles("trace", "C2-grpo-run", bench.build_id())) == 1
+
+
+def test_matrix_traffic_groups_dispatches_between_markers(tmp_path):
+    """--matrix-traffic-from: the calibration copy scales each counter; the
+    dispatches after marker i (klp_ceiling_write) and before marker i + 1
+    are backend i's; dispatches before the copy (warm-up) and after the last
+    marker are not counted."""
+    BS, V = bench.MATRIX_TRAFFIC_SHAPE
+    lb = BS * V * 2
+    MARK = "void klp::klp_ceiling_write_kernel<1, 2>(klp::CeilingParams)"
+    NAIVE = "void klp::klp_fwd_naive_kernel<0>(klp::NaiveParams)"
+    SOFT = "void at::native::softmax_kernel(...)"
+    kib = lb / 1024
+
+    def seq(fetch):
+        # warm-up, calibration copy, then per backend: marker + its kernels
+        f = 0.5 if fetch else 1.0
+        s = [(FWD, 1e9), (COPY, kib * f),
+             (MARK, 0.0), (FWD, kib * f),
+             (MARK, 0.0), (BWD, kib * f) if fetch else (BWD, kib * f),
+             (MARK, 0.0), (NAIVE, kib * f),
+             (MARK, 0.0)] + [(SOFT, kib * f)] * 9 + [
+             (MARK, 0.0), (SOFT, kib * f), (SOFT, 2 * kib * f),
+             (MARK, 0.0), (FWD, 1e9)]
+        return s
+    fetch = _counter_dir(tmp_path, "f", "FETCH_SIZE", seq(True))
+    write = _counter_dir(tmp_path, "w", "WRITE_SIZE", seq(False))
+    md, data = bench.summarize_matrix_traffic(fetch, write)
+    b = data["backends"]
+    assert list(b) == list(bench.MATRIX_TRAFFIC_BACKENDS)
+    assert b["ours_fwd"]["dispatches"] == 1
+    assert b["ours_fwd"]["read_bytes"] == pytest.approx(lb, rel=1e-9)
+    assert b["ours_fwd"]["amplification"] == pytest.approx(2.0)      # read + write of lb
+    assert b["ours_bwd"]["required_bytes"] == 2 * lb
+    assert b["ours_bwd"]["amplification"] == pytest.approx(1.0)
+    assert b["trl_eager"]["dispatches"] == 9
+    assert b["trl_eager"]["amplification"] == pytest.approx(18.0)
+    assert b["pytorch_separate"]["dispatches"] == 2
+    assert b["pytorch_separate"]["amplification"] == pytest.approx(6.0)
+    assert "klp-profile" in md
