@@ -26,13 +26,20 @@ epilogue, logits kept as fp32 MFMA sums (never rounded), bf16 inputs, hidden
 size a multiple of 64.  Its backward recomputes chunks of logits with the
 same MFMA order (klp_lmh_bwd_logits on a slice of the weight) and runs the
 same two library GEMMs per chunk.  It is slower than the library GEMM at
-these shapes (measured at 1024 tokens of Qwen2.5-7B's head: forward 1.30 ms
-against 0.91-0.92 chunked and 0.91-0.93 unfused).
+these shapes (1024 tokens of Qwen2.5-7B's head, bench.py's lm_head leg:
+forward 1.30-1.32 ms, 34% of the bf16 MFMA peak, against 0.93 ms for the
+library GEMM) and is kept as a correct alternative, not tuned further.
+
+At 1024 tokens the chunked forward runs within ~1.5% of the unfused one, on
+either side from box to box (bench.py's lm_head leg: 0.9356 against 0.9279 ms
+on one box, 0.9143 against 0.9278 on another), while it holds 64 MiB of
+extra memory where the unfused path holds 297 MiB of logits; at 8192 tokens
+6.33 against 6.42 ms, 131 against 2376 MiB.
 
 The backward of either head recomputes the logits, one GEMM more than the
 unfused path's backward: that is the price of not holding them (measured
-forward + backward at 1024 tokens: 4.72 ms chunked, 3.87 ms unfused, with
-135 MiB against 297 MiB beyond the inputs and gradients).  When the loss is
+forward + backward at 1024 tokens: 4.64-4.72 ms chunked, 3.83-3.87 ms
+unfused, with 135 MiB against 297 MiB beyond the inputs and gradients).  When the loss is
 known in the forward, :func:`kernel_opt.fused_linear_grpo_step` computes the
 gradients there and needs no recompute.
 
