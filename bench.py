@@ -1977,6 +1977,16 @@ def main(argv=None):
             if k.startswith("klp_bwd_kernel") or k.startswith("klp_fwd_kernel"):
                 trace_check = trace_check or {"file": prof["file"]}
                 trace_check[k] = {ph: round(d["avg_ns"] / 1e3, 3) for ph, d in v.items()}
+                # This run's device-timed medians over the trace's medians of
+                # the same phase (another run, usually another box).
+                role = "bwd" if k.startswith("klp_bwd_kernel") else "fwd"
+                dev_t = (core.get("device_timed") or {}).get(role)
+                if dev_t:
+                    ratio = trace_check.setdefault("bench_over_trace_median", {})
+                    ratio[role] = {
+                        mode: round(dev_t[mode]["ms"] * 1e6 / v[ph]["median_ns"], 4)
+                        for mode, ph in (("warm", "back to back"), ("flushed", "flushed"))
+                        if ph in v}
     dt = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[logits.dtype]
     out = {
         "metric": "fwd/bwd ms + HBM TB/s (% of peak) at B*S=1024, V=152064 bf16",
