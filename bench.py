@@ -1218,6 +1218,30 @@ def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None, dtimer=None):
                 bwd_used=bwd_used, ceilings=out_ceil, device_timed=device, d_logits=d_logits)
 
 
+def trace_agreement(profiles, device_timed):
+    """The committed kernel-trace summaries' figures for klp_fwd / klp_bwd
+    (average us per phase), and this run's device-timed medians divided by
+    the trace's medians of the same phase ("back to back" for warm,
+    "flushed" for flushed): `bench_over_trace_median`.  The trace is another
+    run, usually on another box.  None without a summary of this build."""
+    out = None
+    for prof in profiles:
+        for k, v in prof["kernels"].items():
+            if not (k.startswith("klp_bwd_kernel") or k.startswith("klp_fwd_kernel")):
+                continue
+            out = out or {"file": prof["file"]}
+            out[k] = {ph: round(d["avg_ns"] / 1e3, 3) for ph, d in v.items()}
+            role = "bwd" if k.startswith("klp_bwd_kernel") else "fwd"
+            dev_t = (device_timed or {}).get(role)
+            if dev_t:
+                ratio = out.setdefault("bench_over_trace_median", {})
+                ratio[role] = {
+                    mode: round(dev_t[mode]["ms"] * 1e6 / v[ph]["median_ns"], 4)
+                    for mode, ph in (("warm", "back to back"), ("flushed", "flushed"))
+                    if ph in v and v[ph].get("median_ns")}
+    return out
+
+
 def _device_summary(device):
     """The DeviceTimer figures of core_timing in microseconds: median, the
     interquartile spread in percent, and the count, warm and flushed."""
@@ -1971,22 +1995,7 @@ def main(argv=None):
             elif k.startswith("klp_fwd_kernel"):
                 fwd_traffic = v["traffic_bytes"]
         traffic_src = prof["file"]
-    trace_check = None
-    for prof in load_profiles("trace", name, bid):
-        for k, v in prof["kernels"].items():
-            if k.startswith("klp_bwd_kernel") or k.startswith("klp_fwd_kernel"):
-                trace_check = trace_check or {"file": prof["file"]}
-                trace_check[k] = {ph: round(d["avg_ns"] / 1e3, 3) for ph, d in v.items()}
-                # This run's device-timed medians over the trace's medians of
-                # the same phase (another run, usually another box).
-                role = "bwd" if k.startswith("klp_bwd_kernel") else "fwd"
-                dev_t = (core.get("device_timed") or {}).get(role)
-                if dev_t:
-                    ratio = trace_check.setdefault("bench_over_trace_median", {})
-                    ratio[role] = {
-                        mode: round(dev_t[mode]["ms"] * 1e6 / v[ph]["median_ns"], 4)
-                        for mode, ph in (("warm", "back to back"), ("flushed", "flushed"))
-                        if ph in v}
+    trace_check = trace_agreement(load_profiles("trace", name, bid), core.get("device_timed"))
     dt = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[logits.dtype]
     out = {
         "metric": "fwd/bwd ms + HBM TB/s (% of peak) at B*S=1024, V=152064 bf16",

@@ -196,3 +196,26 @@ def test_matrix_traffic_groups_dispatches_between_markers(tmp_path):
     assert b["pytorch_separate"]["dispatches"] == 2
     assert b["pytorch_separate"]["amplification"] == pytest.approx(6.0)
     assert "klp-profile" in md
+
+
+def test_trace_agreement_divides_device_medians_by_the_trace():
+    prof = {"file": "profiles/x.md", "kernels": {
+        "klp_fwd_kernel<0, 8, 2, false, false>": {
+            "back to back": {"avg_ns": 48600.0, "median_ns": 48500.0},
+            "flushed": {"avg_ns": 48900.0, "median_ns": 48800.0}},
+        "klp_bwd_kernel<0, 8, 2, true, false>": {
+            "back to back": {"avg_ns": 102000.0, "median_ns": 102000.0}},
+        "klp_ceiling_copy_kernel<8, 2>": {
+            "back to back": {"avg_ns": 101000.0, "median_ns": 101000.0}}}}
+    dev = {"fwd": {"warm": {"ms": 0.0485}, "flushed": {"ms": 0.0500}},
+           "bwd": {"warm": {"ms": 0.0969}, "flushed": {"ms": 0.1}}}
+    tc = bench.trace_agreement([prof], dev)
+    assert tc["file"] == "profiles/x.md"
+    assert tc["klp_fwd_kernel<0, 8, 2, false, false>"]["flushed"] == 48.9
+    assert "klp_ceiling_copy_kernel<8, 2>" not in tc
+    r = tc["bench_over_trace_median"]
+    assert r["fwd"] == {"warm": 1.0, "flushed": round(50000 / 48800, 4)}
+    assert r["bwd"] == {"warm": 0.95}  # no flushed phase in that trace
+    assert bench.trace_agreement([], dev) is None
+    no_dev = bench.trace_agreement([prof], None)
+    assert "bench_over_trace_median" not in no_dev
