@@ -1836,6 +1836,94 @@ def summarize_matrix_traffic(fetch_dir, write_dir, command=""):
     return "\n".join(md), data
 
 
+def _rng(vals, nd):
+    """'a' or 'a–b' (min–max) of the non-None values, nd decimals."""
+    v = [x for x in vals if x is not None]
+    if not v:
+        return "—"
+    lo, hi = min(v), max(v)
+    return f"{lo:.{nd}f}" if round(lo, nd) == round(hi, nd) else f"{lo:.{nd}f}–{hi:.{nd}f}"
+
+
+def configs_table(paths, command=""):
+    """Markdown table of C1-C5 from bench.py output lines (the default
+    command's: the C2 headline, its C1 leg and its C3-C5 `configs` legs),
+    one range per cell over the files given."""
+    runs = []
+    for path in paths:
+        with open(path) as f:
+            lines = [ln for ln in f.read().splitlines() if ln.strip().startswith("{")]
+        runs.append(json.loads(lines[-1]))
+    bids = sorted({r.get("build_id") for r in runs})
+    per = {c: [] for c in ("C1", "C2", "C3", "C4", "C5")}
+    for r in runs:
+        c = r["ceilings"]
+        per["C2"].append({
+            "fwd": r["fwd_ms"] * 1e3, "fwd_fl": r["fwd_ms_flushed"] * 1e3,
+            "fwd_pct": r["fwd_pct_peak"], "fwd_pct_fl": r["fwd_pct_peak_flushed"],
+            "f_read": c["fwd_over_read"], "f_read_fl": c.get("fwd_over_read_flushed"),
+            "bwd": r["bwd_ms"] * 1e3, "bwd_fl": r["bwd_ms_flushed"] * 1e3,
+            "bwd_pct": r["bwd_pct_peak"], "bwd_pct_fl": r["bwd_pct_peak_flushed"],
+            "b_copy": c["bwd_over_copy"], "b_rw": c.get("bwd_over_read_plus_write"),
+            "b_rw_fl": c.get("bwd_over_read_plus_write_flushed"),
+            "step": r["ms_per_step"] * 1e3})
+        for name, leg in (r.get("configs") or {}).items():
+            lc = leg["ceilings"]
+            per[name].append({
+                "fwd": leg["fwd_us"], "fwd_fl": leg["fwd_us_flushed"],
+                "fwd_pct": leg["fwd_pct_peak"], "fwd_pct_fl": leg["fwd_pct_peak_flushed"],
+                "f_read": lc["fwd_over_read"], "f_read_fl": lc.get("fwd_over_read_flushed"),
+                "bwd": leg["bwd_us"], "bwd_fl": leg["bwd_us_flushed"],
+                "bwd_pct": leg["bwd_pct_peak"], "bwd_pct_fl": leg["bwd_pct_peak_flushed"],
+                "b_copy": lc["bwd_over_copy"], "b_rw": lc.get("bwd_over_read_plus_write"),
+                "b_rw_fl": lc.get("bwd_over_read_plus_write_flushed"), "step": leg["step_us"]})
+        c1 = r.get("C1")
+        if c1:
+            B, S, V = CONFIGS["C1"]["shape"]
+            fb = B * S * V * 4 + 20 * B * S
+            per["C1"].append({
+                "fwd": c1["fwd_us"], "fwd_pct": c1["fwd_tbps"] / 8 * 100,
+                "bwd": c1["bwd_us"], "bwd_pct": c1["bwd_tbps"] / 8 * 100,
+                "step": None, "fwd_bytes": fb})
+    lines = [
+        "# Forward / backward at C1–C5 with same-run ceilings (bench.py)", "",
+        f"{len(runs)} run(s) of `python bench.py` (the driver's command) on one MI355X each, "
+        f"build {', '.join(f'`{b}`' for b in bids)}; each cell is the range over the runs. "
+        "C2 is the line's headline, C1 its `C1` leg, C3–C5 its `configs` legs.", "",
+        "Warm: launches queued back to back behind a spin kernel (HIP events). Flushed: each "
+        "launch's own device duration right after a 1 GiB read (torch.profiler, median of "
+        "24). Ceilings, same run, same launch shapes: the forward's ring of loads without "
+        "arithmetic (read), the backward's loop as a copy, and that loop's loads alone plus "
+        "its stores alone (read-only + write-only). % of 8 TB/s of algorithmic bytes.", ""]
+    if command:
+        lines += ["Command:", "```", command, "```", ""]
+    lines += [
+        "| config | fwd µs warm / flushed | fwd % warm / flushed | fwd / read warm, flushed "
+        "| bwd µs warm / flushed | bwd % warm / flushed | bwd / copy "
+        "| bwd / (read-only + write-only) warm, flushed | step µs |",
+        "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    label = {"C1": "C1 fp32 [2,128,32000]", "C2": "C2 bf16 [4,256,152064]",
+             "C3": "C3 fp16 [8,1024,128256]", "C4": "C4 bf16 [16,2048,151936]",
+             "C5": "C5 fp32 [4,2048,262144], strided"}
+    for name in ("C1", "C2", "C3", "C4", "C5"):
+        rs = per[name]
+        if not rs:
+            continue
+        g = lambda k: [x.get(k) for x in rs]  # noqa: E731
+        lines.append(
+            f"| {label[name]} | {_rng(g('fwd'), 2)} / {_rng(g('fwd_fl'), 2)} "
+            f"| {_rng(g('fwd_pct'), 1)} / {_rng(g('fwd_pct_fl'), 1)} "
+            f"| {_rng(g('f_read'), 3)}, {_rng(g('f_read_fl'), 3)} "
+            f"| {_rng(g('bwd'), 2)} / {_rng(g('bwd_fl'), 2)} "
+            f"| {_rng(g('bwd_pct'), 1)} / {_rng(g('bwd_pct_fl'), 1)} "
+            f"| {_rng(g('b_copy'), 3)} | {_rng(g('b_rw'), 3)}, {_rng(g('b_rw_fl'), 3)} "
+            f"| {_rng(g('step'), 1)} |")
+    lines += ["", "C1's figures are GPU time per launch with launches queued (the C1 leg); "
+              "at 33 MB it is launch-latency bound and Infinity-Cache resident, and the "
+              "leg times no ceilings or flushed launches."]
+    return "\n".join(lines) + "\n"
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -1888,6 +1976,9 @@ def main(argv=None):
     ap.add_argument("--matrix-traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     default=None, help="bytes moved per backend from two rocprofv3 --pmc runs "
                                        "of --matrix-run (markdown to stdout; no GPU needed)")
+    ap.add_argument("--configs-table", nargs="+", metavar="BENCH_JSON", default=None,
+                    help="C1-C5 table (markdown to stdout) from the output lines of one or "
+                         "more default bench.py runs; no GPU needed")
     ap.add_argument("--label", default=None,
                     help="tag of a --trace-from summary other than the config name (a run "
                          "that is not --core-only)")
@@ -1904,6 +1995,9 @@ def main(argv=None):
     if args.matrix_traffic_from:
         md, _ = summarize_matrix_traffic(*args.matrix_traffic_from, args.command)
         print(md)
+        return 0
+    if args.configs_table:
+        print(configs_table(args.configs_table, args.command), end="")
         return 0
 
     if args.gpus != 1:
