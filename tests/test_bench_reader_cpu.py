@@ -219,3 +219,34 @@ def test_trace_agreement_divides_device_medians_by_the_trace():
     assert bench.trace_agreement([], dev) is None
     no_dev = bench.trace_agreement([prof], None)
     assert "bench_over_trace_median" not in no_dev
+
+
+def test_configs_table_ranges_over_runs(tmp_path):
+    import json
+
+    def line(f, b):
+        ceil = {"fwd_over_read": 1.07, "fwd_over_read_flushed": 1.075, "bwd_over_copy": 1.01,
+                "bwd_over_read_plus_write": 1.02, "bwd_over_read_plus_write_flushed": 0.96}
+        leg = {"fwd_us": f * 10, "fwd_us_flushed": f * 10, "fwd_pct_peak": 85.0,
+               "fwd_pct_peak_flushed": 86.0, "bwd_us": b * 10, "bwd_us_flushed": b * 10,
+               "bwd_pct_peak": 79.0, "bwd_pct_peak_flushed": 80.0, "step_us": (f + b) * 10,
+               "ceilings": ceil}
+        return {"build_id": "abc", "fwd_ms": f / 1e3, "fwd_ms_flushed": f / 1e3,
+                "fwd_pct_peak": 80.0, "fwd_pct_peak_flushed": 79.0, "bwd_ms": b / 1e3,
+                "bwd_ms_flushed": b / 1e3, "bwd_pct_peak": 76.0, "bwd_pct_peak_flushed": 77.0,
+                "ms_per_step": (f + b) / 1e3, "ceilings": ceil, "configs": {"C3": leg},
+                "C1": {"fwd_us": 7.0, "bwd_us": 11.5, "fwd_tbps": 4.8, "bwd_tbps": 5.7}}
+    paths = []
+    for i, (f, b) in enumerate(((48.1, 102.6), (48.5, 101.4))):
+        p = tmp_path / f"b{i}.json"
+        p.write_text("bench.py: noise\n" + json.dumps(line(f, b)) + "\n")
+        paths.append(str(p))
+    md = bench.configs_table(paths, "python bench.py")
+    rows = {ln.split("|")[1].strip().split()[0]: ln for ln in md.splitlines()
+            if ln.startswith("| C")}
+    assert set(rows) == {"C1", "C2", "C3"}
+    assert "48.10–48.50 / 48.10–48.50" in rows["C2"]
+    assert "101.40–102.60" in rows["C2"]
+    assert "481.00–485.00" in rows["C3"]
+    assert "| 1.070, 1.075 |" in rows["C2"]
+    assert "`abc`" in md and "python bench.py" in md
