@@ -304,6 +304,54 @@ def _git_head() -> str | None:
         return None
 
 
+def summarize_counters(directory: str, config: str, command: str = ""):
+    """Per-dispatch averages of every counter in a rocprofv3 --pmc run, for the
+    klp forward / backward and calibration kernels (rows of one dispatch and
+    counter summed), with SQ_INSTS_* also per element of the workload (x 64
+    lanes / N*V: wave instructions times lanes over logits).  Returns
+    (markdown, data)."""
+    N, V, _ = _workload_sizes(config)
+    elems = N * V
+    per = {}
+    for r in _rocprof_csv(directory, "counter_collection.csv"):
+        if not _is_klp(r["Kernel_Name"]):
+            continue
+        k = short_kernel(r["Kernel_Name"])
+        d = per.setdefault(k, {}).setdefault(r["Counter_Name"], {})
+        d[r["Dispatch_Id"]] = d.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    names = sorted({c for d in per.values() for c in d})
+    kernels = {}
+    rows = []
+    for k in sorted(per):
+        vals = {c: sum(v.values()) / len(v) for c, v in per[k].items()}
+        n = max(len(v) for v in per[k].values())
+        kernels[k] = {"dispatches": n, "mean": {c: round(v, 2) for c, v in vals.items()}}
+        cells = []
+        for c in names:
+            v = vals.get(c)
+            if v is None:
+                cells.append("-")
+            elif c.startswith("SQ_INSTS_"):
+                cells.append(f"{v:.4g} ({v * 64 / elems:.2f}/elem)")
+            else:
+                cells.append(f"{v:.4g}")
+        rows.append(f"| `{k}` | {n} | " + " | ".join(cells) + " |")
+    data = {"kind": "counters", "config": config, "build_id": build_id(),
+            "git_head": _git_head(), "kernels": kernels}
+    md = [f"# rocprofv3 counters: klp kernels, workload {config}", "",
+          f"Build id `{data['build_id']}`; summarised by `python bench.py --counters-from DIR "
+          f"--config {config}`. Means per dispatch (a dispatch's rows summed over shader "
+          f"engines and XCDs); SQ_INSTS_* also per logit element (wave instructions x 64 / "
+          f"{elems}).", ""]
+    if command:
+        md += ["Command (MI355X):", "```", command, "```", ""]
+    md += ["| kernel | dispatches | " + " | ".join(names) + " |",
+           "|---|---:|" + "---:|" * len(names)]
+    md += rows
+    md += ["", "<!-- klp-profile " + json.dumps(data, sort_keys=True) + " -->"]
+    return "\n".join(md) + "\n", data
+
+
 def summarize_traffic(fetch_dir: str, write_dir: str, config: str, command: str = ""):
     """Per-dispatch HBM bytes of the klp kernels from two rocprofv3 --pmc
     runs (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by what the
@@ -1976,6 +2024,9 @@ def main(argv=None):
     ap.add_argument("--matrix-traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     default=None, help="bytes moved per backend from two rocprofv3 --pmc runs "
                                        "of --matrix-run (markdown to stdout; no GPU needed)")
+    ap.add_argument("--counters-from", metavar="DIR", default=None,
+                    help="summarise any rocprofv3 --pmc run's counters per klp kernel "
+                         "(markdown to stdout; no GPU needed)")
     ap.add_argument("--configs-table", nargs="+", metavar="BENCH_JSON", default=None,
                     help="C1-C5 table (markdown to stdout) from the output lines of one or "
                          "more default bench.py runs; no GPU needed")
@@ -1995,6 +2046,10 @@ def main(argv=None):
     if args.matrix_traffic_from:
         md, _ = summarize_matrix_traffic(*args.matrix_traffic_from, args.command)
         print(md)
+        return 0
+    if args.counters_from:
+        md, _ = summarize_counters(args.counters_from, args.config, args.command)
+        print(md, end="")
         return 0
     if args.configs_table:
         print(configs_table(args.configs_table, args.command), end="")
