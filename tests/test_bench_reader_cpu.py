@@ -250,3 +250,26 @@ def test_configs_table_ranges_over_runs(tmp_path):
     assert "481.00–485.00" in rows["C3"]
     assert "| 1.070, 1.075 |" in rows["C2"]
     assert "`abc`" in md and "python bench.py" in md
+
+
+def test_counters_summed_per_dispatch_and_per_element(tmp_path):
+    N, V, _ = bench._workload_sizes("C2")
+    rows = []
+    # Two dispatches of the forward, each reported as two shader-engine rows.
+    for disp, (a, b) in ((1, (100.0, 300.0)), (2, (200.0, 200.0))):
+        for v in (a, b):
+            rows.append({"Dispatch_Id": disp, "Kernel_Name": FWD, "Counter_Name": "SQ_INSTS_VALU",
+                         "Counter_Value": v})
+        rows.append({"Dispatch_Id": disp, "Kernel_Name": FWD, "Counter_Name": "VALUBusy",
+                     "Counter_Value": 50.0 + disp})
+    rows.append({"Dispatch_Id": 3, "Kernel_Name": FLUSH, "Counter_Name": "SQ_INSTS_VALU",
+                 "Counter_Value": 1e9})
+    d = tmp_path / "cnt"
+    _write(str(d / "host" / "1" / "x_counter_collection.csv"), COUNTER_COLS, rows)
+    md, data = bench.summarize_counters(str(d), "C2", "rocprofv3 --pmc ...")
+    k = bench.short_kernel(FWD)
+    assert list(data["kernels"]) == [k]  # the non-klp kernel is left out
+    assert data["kernels"][k]["dispatches"] == 2
+    assert data["kernels"][k]["mean"] == {"SQ_INSTS_VALU": 400.0, "VALUBusy": 51.5}
+    assert f"({400.0 * 64 / (N * V):.2f}/elem)" in md
+    assert data["kind"] == "counters" and "rocprofv3 --pmc" in md
