@@ -65,6 +65,11 @@ constexpr int64_t kBwdSmallGrid = 16384;
 constexpr int kMaxSplits = 64;
 // fp32 backward rows of 4-wave workgroups (C5: 128 pieces of one iteration).
 constexpr int kMaxSplitsFp32 = 256;
+// MI355X's Infinity Cache (256 MB, memory-side, shared by the XCDs).
+constexpr int64_t kInfinityCacheBytes = int64_t{256} << 20;
+// Backward grids of this many row pieces and more (512 per CU) take pieces
+// of up to 33/32 of an iteration rather than at most one.
+constexpr int64_t kBwdManyPieces = 131072;
 
 // Shared checks of the row-addressed logits operand.
 int check_rows(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t rows_inner,
@@ -239,6 +244,42 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
         if (dtype == KLP_FP32 && 2 * s <= kMaxSplitsFp32) {
             c.waves = 4;
             s *= 2;
+        }
+    }
+    // bf16 / fp16 logits larger than the Infinity Cache: 4-wave workgroups
+    // over pieces of about one iteration (512 vectors): the fewest pieces of
+    // at most one iteration, or on grids of kBwdManyPieces pieces and more of
+    // at most 33/32 of one (fewer workgroups to dispatch), if each fills 7/8
+    // of an iteration.  The rules above leave Qwen's vocabularies at 1.16
+    // iterations a piece.  Measured back to back / flushed / after a forward:
+    //  - C2 [1024, 152064], 38 pieces of 504 vectors: 96.0-98.5 / 98.0-98.7 /
+    //    97.2-98.3 us against 99.7-100.1 / 100.8-101.3 / 100.0-101.2 for 8
+    //    waves x 16 (four boxes); 36 pieces of 528 ~1% slower than 38;
+    //  - C4 [32768, 151936], 36 pieces of 528: 3007-3010 / 2997-2998 /
+    //    2998-3001 us against 3185-3231 / 3094-3111 / 3155-3173 for 16 waves
+    //    x 10 (two boxes); 38 pieces of 504 3085-3239 / 3143-3317 / 3109-3154;
+    //  - C3 [8192, 128256] fp16, 31 pieces of 520: 642 / 653 / 648 us
+    //    against 660 / 654 / 673 for 32 pieces and 663 / 679 / 668 for 16
+    //    waves x 8;
+    //  - against the previous shapes: [32768, 18992] 0.95-0.97x,
+    //    [4096, 152064] 0.94-0.97x, [16384, 65536] 0.88-0.90x,
+    //    [2048, 262144] 0.86-0.88x, fp16 [4096, 128256] 0.95-0.96x,
+    //    [8192, 32000] 0.98-0.99x; [1024, 256000] 1.00-1.02x (at 63 pieces
+    //    of at most one iteration).
+    // Logits the cache holds keep the shapes above: their back-to-back
+    // re-reads hit it, and smaller pieces measured up to 12% slower there
+    // ([1024, 100352]: 13 pieces of 8 waves 66.8 against 59.6 us).
+    if (dtype != KLP_FP32 && n_rows * vocab * elem_bytes(dtype) >= kInfinityCacheBytes) {
+        const int64_t tile4 = int64_t{4} * 64 * 2;
+        int64_t e = (nvec + tile4 - 1) / tile4;
+        if (n_rows * e >= kBwdManyPieces) {
+            const int64_t cap = tile4 + tile4 / 32;
+            e = (nvec + cap - 1) / cap;
+        }
+        if (e <= kMaxSplits && nvec / e >= tile4 - tile4 / 8) {
+            c.waves = 4;
+            c.unroll = 2;
+            s = e;
         }
     }
     // Rows of more than 2 GiB per 64 pieces (never a real vocabulary) take

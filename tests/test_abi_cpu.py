@@ -155,12 +155,22 @@ def test_default_launch_shapes():
     assert lib.klp_fwd_workspace_bytes(0, 16, 152064) == 16 * s * 16 + 64
     # backward splits rows freely (no second pass)
     assert _C.default_config("bwd", torch.bfloat16, 1024, 152064)[2] >= 2
-    # small bf16 / fp16 grids: 8-wave workgroups over twice the pieces (C2);
-    # larger grids 16 waves (C3, C4); fp32 rows 4 waves over four times (C1)
-    assert _C.default_config("bwd", torch.bfloat16, 1024, 152064)[:3] == (8, 2, 16)
+    # bf16 / fp16 logits over the Infinity Cache's size: 4-wave workgroups
+    # over pieces of about one iteration (512 vectors): at most one on
+    # smaller grids (C2: 19008 vectors in 38 pieces of 504), at most 33/32
+    # from 131072 pieces on (C3: 31 of 520, C4: 36 of 528)
+    assert _C.default_config("bwd", torch.bfloat16, 1024, 152064)[:3] == (4, 2, 38)
+    assert _C.default_config("bwd", torch.float16, 2048, 152064)[:3] == (4, 2, 38)
+    assert _C.default_config("bwd", torch.bfloat16, 1536, 128000)[:3] == (4, 2, 32)
+    assert _C.default_config("bwd", torch.float16, 8192, 128256)[:3] == (4, 2, 31)
+    assert _C.default_config("bwd", torch.bfloat16, 32768, 151936)[:3] == (4, 2, 36)
+    assert _C.default_config("bwd", torch.bfloat16, 4096, 152064)[:3] == (4, 2, 36)
+    # logits the cache holds: small bf16 / fp16 grids 8-wave workgroups over
+    # twice the power-of-two pieces of 16 waves; fp32 rows 4 waves over four
+    # times (C1)
+    assert _C.default_config("bwd", torch.bfloat16, 256, 152064)[:3] == (8, 2, 16)
+    assert _C.default_config("bwd", torch.bfloat16, 1024, 100352)[:3] == (8, 2, 8)
     assert _C.default_config("bwd", torch.float32, 256, 32000)[:3] == (4, 2, 16)
-    assert _C.default_config("bwd", torch.float16, 8192, 128256)[:3] == (16, 2, 8)
-    assert _C.default_config("bwd", torch.bfloat16, 32768, 151936)[:3] == (16, 2, 10)
     # fp32 rows: 4 waves at every grid size (C5)
     assert _C.default_config("bwd", torch.float32, 8192, 262144)[:3] == (4, 2, 128)
 

@@ -29,7 +29,8 @@ def _lib():
 
 
 @pytest.mark.parametrize("n_rows,row_bytes,waves,unroll,splits", [
-    (7, 304128, 16, 2, 8),      # C2 rows, the backward's default shape
+    (7, 304128, 4, 2, 38),      # C2 rows, the backward's default shape
+    (7, 304128, 16, 2, 8),
     (5, 4096, 4, 4, 3),         # pieces that are not whole 8-vector groups
     (3, 16 * 1000 + 16, 8, 2, 16),
     (2, 16, 1, 2, 1),           # one vector per row
@@ -100,7 +101,8 @@ def test_ceiling_read_reads_every_word(n_rows, row_bytes, waves, unroll, splits)
 
 
 @pytest.mark.parametrize("n_rows,row_bytes,waves,unroll,splits", [
-    (4, 304128, 8, 2, 16),      # C2 rows, the backward's default shape
+    (4, 304128, 4, 2, 38),      # C2 rows, the backward's default shape
+    (4, 304128, 8, 2, 16),
     (5, 4096 + 16 * 7, 4, 4, 3),
     (3, 16 * 300, 1, 2, 5),
 ])
@@ -127,7 +129,8 @@ def test_ceiling_read_pieces_reads_every_word(n_rows, row_bytes, waves, unroll, 
 
 
 @pytest.mark.parametrize("n_rows,row_bytes,waves,unroll,splits", [
-    (7, 304128, 8, 2, 16),      # C2 rows, the backward's default shape
+    (7, 304128, 4, 2, 38),      # C2 rows, the backward's default shape
+    (7, 304128, 8, 2, 16),
     (5, 4096, 4, 4, 3),
     (2, 16, 1, 2, 1),
 ])
