@@ -1534,9 +1534,13 @@ def small_batch_leg(dev, timer):
                     "of the same bytes bounds it from below"}
 
 
-def sweep(name, dev, K, timer, out_md):
+def sweep(name, dev, K, timer, out_md, dtimer=None):
     """Launch-shape sweep of the forward and backward at workload `name`,
-    back to back and flushed, written as a markdown table."""
+    back to back and flushed, written as a markdown table: the forward over
+    waves x unroll x 1-2 pieces, the backward over waves x unroll x
+    power-of-two pieces plus, at 4 and 8 waves, the piece counts of about
+    one iteration (the fewest within one, and one on either side).  With a
+    DeviceTimer both columns are device-timed medians."""
     from kernel_opt import _C
     inp = make_inputs(name, dev)
     x, t = inp["logits"], inp["targets"]
@@ -1550,17 +1554,27 @@ def sweep(name, dev, K, timer, out_md):
     bdef = _C.default_config("bwd", x.dtype, N, V)
     timer = Timer(dev, max(K, KERNEL_LAUNCHES), timer.flush_mode, timer.buf)
     n = timer.K
+
+    def _sweep_times(fn, match):
+        if dtimer is not None and dtimer.available:
+            st = dtimer.stats(fn, match, n=16)
+            return st["warm"]["ms"], st["flushed"]["ms"]
+        return timer.b2b(fn), timer.flushed(fn)[0]
     t_spin = time.perf_counter() + SETTLE_S
     while time.perf_counter() < t_spin:
         _C.fwd_launch(x, t, lp, ent, lse)
         _C.bwd_launch(x, t, lse, ent, gl, ge, None, d)
         torch.cuda.synchronize()
+    use_dev = dtimer is not None and dtimer.available
+    how = ("each shape's kernel duration from the device's timestamps (torch.profiler), the "
+           "median over 16 launches back to back and over 16 each right after a 1 GiB read"
+           if use_dev else
+           f"each shape timed over {n} back-to-back launches queued behind a spin kernel (one "
+           "event pair), and right after a 1 GiB read (the median over 9 rounds of one event "
+           "pair around K / 9 (read, launch) pairs minus one around as many reads alone, per "
+           "launch)")
     lines = [f"# Launch-shape sweep, workload {name} (build `{build_id()}`)", "",
-             f"`python bench.py --config {name} --sweep OUT.md --steps {K}`: each shape timed "
-             f"over {n} back-to-back launches queued behind a spin kernel (one event pair), "
-             "and right after a 1 GiB read (the median over 9 rounds of one event pair "
-             "around K / 9 (read, launch) pairs minus one around as many reads alone, per "
-             "launch). "
+             f"`python bench.py --config {name} --sweep OUT.md --steps {K}`: {how}. "
              "Defaults marked *.", "",
              "| kernel | waves | unroll | splits | b2b us | b2b % of 8 TB/s | flushed us | "
              "flushed % |", "|---|---:|---:|---:|---:|---:|---:|---:|"]
@@ -1571,26 +1585,33 @@ def sweep(name, dev, K, timer, out_md):
                 c = (w, u, sp, 0)
                 fn = (lambda c=c: _C.fwd_launch(x, t, lp, ent, lse, config=c))
                 fn()
-                a = timer.b2b(fn)
-                f, _ = timer.flushed(fn)
+                a, f = _sweep_times(fn, "klp_fwd_kernel")
                 mark = "*" if c == tuple(fdef) else ""
                 lines.append(f"| fwd{mark} | {w} | {u} | {sp} | {a * 1e3:.2f} | "
                              f"{100 * _tbps(fb, a) / HBM_PEAK_TBPS:.1f} | {f * 1e3:.2f} | "
                              f"{100 * _tbps(fb, f) / HBM_PEAK_TBPS:.1f} |")
                 print(lines[-1], file=sys.stderr, flush=True)
-    for w in (4, 8, 16):
-        for u in (2, 4):
-            for sp in (4, 8, 16):
-                c = (w, u, sp, 1)
-                fn = (lambda c=c: _C.bwd_launch(x, t, lse, ent, gl, ge, None, d, config=c))
-                fn()
-                a = timer.b2b(fn)
-                f, _ = timer.flushed(fn)
-                mark = "*" if c == tuple(bdef) else ""
-                lines.append(f"| bwd{mark} | {w} | {u} | {sp} | {a * 1e3:.2f} | "
-                             f"{100 * _tbps(bb, a) / HBM_PEAK_TBPS:.1f} | {f * 1e3:.2f} | "
-                             f"{100 * _tbps(bb, f) / HBM_PEAK_TBPS:.1f} |")
-                print(lines[-1], file=sys.stderr, flush=True)
+    nvec = V * x.element_size() // 16
+    bcfgs = [(w, u, sp, 1) for w in (4, 8, 16) for u in (2, 4) for sp in (4, 8, 16)]
+    for w in (4, 8):
+        e = -(-nvec // (w * 64 * 2))
+        bcfgs += [(w, 2, sp, 1) for sp in (e - 1, e, e + 1) if 1 <= sp <= 1024]
+    if tuple(bdef) not in bcfgs:
+        bcfgs.append(tuple(bdef))
+    seen = set()
+    for c in bcfgs:
+        if c in seen:
+            continue
+        seen.add(c)
+        w, u, sp = c[:3]
+        fn = (lambda c=c: _C.bwd_launch(x, t, lse, ent, gl, ge, None, d, config=c))
+        fn()
+        a, f = _sweep_times(fn, "klp_bwd_kernel")
+        mark = "*" if c == tuple(bdef) else ""
+        lines.append(f"| bwd{mark} | {w} | {u} | {sp} | {a * 1e3:.2f} | "
+                     f"{100 * _tbps(bb, a) / HBM_PEAK_TBPS:.1f} | {f * 1e3:.2f} | "
+                     f"{100 * _tbps(bb, f) / HBM_PEAK_TBPS:.1f} |")
+        print(lines[-1], file=sys.stderr, flush=True)
     with open(out_md, "w") as fh:
         fh.write("\n".join(lines) + "\n")
 
@@ -2068,7 +2089,8 @@ def main(argv=None):
     K = args.steps
     timer = Timer(dev, K, args.flush_mode)
     if args.sweep:
-        sweep(name, dev, K, timer, args.sweep)
+        sweep(name, dev, K, timer, args.sweep,
+              DeviceTimer(timer, enabled=not args.no_device_timer))
         return 0
     if args.matrix:
         matrix(dev, args.matrix, DeviceTimer(timer, enabled=not args.no_device_timer))
