@@ -296,6 +296,36 @@ def test_backward_small_pieces_bitwise(dtype, oracle):
         assert np.array_equal(storage_bits(d), storage_bits(ref)), f"backward differs for {cfg}"
 
 
+@pytest.mark.parametrize("dtype,V,shapes", [
+    (torch.bfloat16, 152064, [(4, 2, 38, 1), (4, 2, 36, 1), (4, 2, 39, 1), (8, 2, 16, 1)]),
+    (torch.bfloat16, 151936, [(4, 2, 36, 1), (4, 2, 37, 1), (16, 2, 10, 1)]),
+    (torch.float16, 128256, [(4, 2, 31, 1), (4, 2, 32, 1), (16, 2, 8, 1)]),
+])
+def test_backward_pieces_of_one_iteration_bitwise(dtype, V, shapes, oracle):
+    """The backward's shapes for logits beyond the Infinity Cache (4-wave
+    workgroups over pieces of about one iteration: C2 38, C4 36, C3 31) write
+    the same gradient bits as their neighbours and as the shapes before them
+    (8 waves x 16, 16 x 10, 16 x 8), on rows of Qwen's and Llama 3's
+    vocabularies; the first shape is checked against the oracle."""
+    from kernel_opt import _C
+    N = 6
+    x = seeded_logits((N, V), dtype, seed=91).to(DEV)
+    t = seeded_targets((N,), V, seed=91).to(DEV)
+    t[0], t[1] = 0, V - 1
+    outs = [torch.empty(N, device=DEV) for _ in range(3)]
+    _C.fwd_launch(x, t, *outs)
+    g = torch.Generator().manual_seed(92)
+    gl, ge, gs = [(torch.randn(N, generator=g) * 0.5).to(DEV) for _ in range(3)]
+    ref = torch.empty_like(x)
+    _C.bwd_launch(x, t, outs[2], outs[1], gl, ge, gs, ref, config=shapes[0])
+    ulps, kind = _grad_ulps(oracle, x.cpu(), t.cpu(), outs[2], outs[1], ref, gl, ge, gs)
+    assert ulps <= 1.0, f"{kind}: {ulps}"
+    for cfg in shapes[1:]:
+        d = torch.empty_like(ref)
+        _C.bwd_launch(x, t, outs[2], outs[1], gl, ge, gs, d, config=cfg)
+        assert np.array_equal(storage_bits(d), storage_bits(ref)), f"backward differs for {cfg}"
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("V", [1, 2, 3, 7, 8, 9, 15, 16, 17, 63, 64, 65, 1000, 4097])
 @pytest.mark.parametrize("offset", [0, 1, 3])
