@@ -276,7 +276,7 @@ klp::BwdConfig default_bwd_config(int dtype, int64_t n_rows, int64_t vocab) {
             const int64_t cap = tile4 + tile4 / 32;
             e = (nvec + cap - 1) / cap;
         }
-        if (e <= kMaxSplits && nvec / e >= tile4 - tile4 / 8) {
+        if (e >= 1 && e <= kMaxSplits && nvec / e >= tile4 - tile4 / 8) {
             c.waves = 4;
             c.unroll = 2;
             s = e;

@@ -171,6 +171,9 @@ def test_default_launch_shapes():
     assert _C.default_config("bwd", torch.bfloat16, 256, 152064)[:3] == (8, 2, 16)
     assert _C.default_config("bwd", torch.bfloat16, 1024, 100352)[:3] == (8, 2, 8)
     assert _C.default_config("bwd", torch.float32, 256, 32000)[:3] == (4, 2, 16)
+    # rows of fewer than 8 elements (no 16-byte body) over the cache's size:
+    # the piece rule has no vectors to cut and leaves the row whole
+    assert _C.default_config("bwd", torch.bfloat16, 40_000_000, 4)[2] == 1
     # fp32 rows: 4 waves at every grid size (C5)
     assert _C.default_config("bwd", torch.float32, 8192, 262144)[:3] == (4, 2, 128)
 
