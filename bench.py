@@ -295,6 +295,13 @@ def load_profiles(kind: str, config: str, bid: str):
     return out
 
 
+def _git_note() -> str:
+    """', git `<head>`' where the tree is a git checkout, else '' (a copy of
+    the tree without its .git, as on a remote GPU box)."""
+    h = _git_head()
+    return f", git `{h}`" if h else ""
+
+
 def _git_head() -> str | None:
     try:
         import subprocess
@@ -1773,7 +1780,7 @@ def matrix(dev, out_md, dtimer):
         torch.cuda.empty_cache()
     bid = build_id()
     md = ["# The reference's comparison matrix on one MI355X", "",
-          f"`python bench.py --matrix {out_md}` (build `{bid}`, git `{_git_head()}`). bf16 "
+          f"`python bench.py --matrix {out_md}` (build `{bid}`{_git_note()}). bf16 "
           "logits `[1, B*S, V]` ~ N(0, 1), targets uniform, as the reference's "
           "`bench/bench_micro.py:167-169` draws them. Backends as the reference defines them "
           "(`bench/bench_micro.py:95-122`): `ours` = `kernel_opt.fused_logprob_entropy`, "
