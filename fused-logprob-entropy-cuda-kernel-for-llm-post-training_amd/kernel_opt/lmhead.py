@@ -30,9 +30,9 @@ these shapes (1024 tokens of Qwen2.5-7B's head, bench.py's lm_head leg:
 forward 1.30-1.32 ms, 34% of the bf16 MFMA peak, against 0.93 ms for the
 library GEMM) and is kept as a correct alternative, not tuned further.
 
-At 1024 tokens the chunked forward runs within ~1.5% of the unfused one, on
+At 1024 tokens the chunked forward runs within ~2% of the unfused one, on
 either side from box to box (bench.py's lm_head leg: 0.9356 against 0.9279 ms
-on one box, 0.9143 against 0.9278 on another), while it holds 64 MiB of
+on one box, 0.901-0.954 against 0.911-0.948 ms on three others), while it holds 64 MiB of
 extra memory where the unfused path holds 297 MiB of logits; at 8192 tokens
 6.33 against 6.42 ms, 131 against 2376 MiB.
 
