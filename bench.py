@@ -673,6 +673,13 @@ def grpo_step_timing(dev, K, logits, targets):
         loss_.backward()
         x.grad = None
 
+    mask_i32 = mask.to(torch.int32)
+
+    def step_fused_int32_mask():
+        loss_, _, _ = fused_grpo_step(x, targets, old, adv, mask_i32, ref, **kw)
+        loss_.backward()
+        x.grad = None
+
     def step_unfused():
         lp_, _, _ = fused_logprob_entropy(x, targets)
         loss_, _ = fused_grpo_loss(lp_, old, adv, mask, ref, **kw)
@@ -680,7 +687,8 @@ def grpo_step_timing(dev, K, logits, targets):
         x.grad = None
 
     e2e = {}
-    for name, fn in (("fused", step_fused), ("unfused", step_unfused)):
+    for name, fn in (("fused", step_fused), ("fused_int32_mask", step_fused_int32_mask),
+                     ("unfused", step_unfused)):
         for _ in range(3):
             fn()
         for queued in (False, True):
@@ -708,7 +716,10 @@ def grpo_step_timing(dev, K, logits, targets):
                     "twice); both kernel time through the C ABI, outputs preallocated; "
                     "end_to_end_us: the step through the public entry points from Python "
                     "(fused_grpo_step vs fused_logprob_entropy + fused_grpo_loss, loss + "
-                    "backward), host-paced and *_queued (GPU time)"}
+                    "backward), host-paced and *_queued (GPU time), with a float32 mask "
+                    "(token weights in eager torch) and fused_int32_mask with the same mask "
+                    "as int32, as TRL's completion_mask comes (token weights in one "
+                    "klp_grpo_token_weights launch)"}
 
 
 def shard_timing(dev, K, N=32768, V=151936, P=8):

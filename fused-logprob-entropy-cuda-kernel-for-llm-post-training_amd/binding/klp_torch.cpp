@@ -693,7 +693,8 @@ std::optional<std::vector<at::Tensor>> fused_grpo_step(
     // integer mask stays as it is (token_weights promotes it to float32, and
     // its 0 / 1 sums are exact either way, so the weights are the same bits).
     at::Tensor m;
-    if (mask.has_value() && mask->defined()) {
+    const bool has_mask = mask.has_value() && mask->defined();
+    if (has_mask) {
         if (mask->device() != dev) throw std::runtime_error("mask must be on " + dev.str());
         if (mask->sizes() != at::IntArrayRef({B, S}))
             throw std::runtime_error("mask has shape " + tuple_str(mask->sizes()) +
@@ -701,13 +702,44 @@ std::optional<std::vector<at::Tensor>> fused_grpo_step(
         m = mask->detach();
         if (at::isFloatingType(m.scalar_type()) && m.scalar_type() != at::kFloat)
             m = m.to(at::kFloat);
-    } else {
-        m = at::ones({B, S}, at::TensorOptions().dtype(at::kFloat).device(dev));
     }
     const at::Tensor ref = (beta != 0.0 && ref_logp.has_value() && ref_logp->defined())
                                ? grpo_operand(ref_logp, "ref_logp", {B, S}, dev)
                                : at::Tensor();
-    const at::Tensor weight = token_weights(m, weight_kind, weight_scale).contiguous();
+    // No mask, or a bool / uint8 / int32 / int64 one: klp_grpo_token_weights
+    // computes the weights in one launch, the same bits as token_weights
+    // (its integer sums are exact, as the eager float32 sums of a 0 / 1 mask
+    // are).  A floating mask takes token_weights, and so does a fixed
+    // normaliser whose float32 reciprocal is not finite and > 0 (a zero or
+    // negative normaliser: the entry point rejects such a scale, the eager
+    // statement gives inf / negative weights).
+    int mask_code = -1;
+    if (has_mask) {
+        const auto st = m.scalar_type();
+        mask_code = (st == at::kBool || st == at::kByte) ? KLP_MASK_U8
+                    : st == at::kInt                     ? KLP_MASK_I32
+                    : st == at::kLong                    ? KLP_MASK_I64
+                                                         : -1;
+    }
+    const float fixed_scale = static_cast<float>(weight_scale);
+    const bool scale_ok = weight_kind != KLP_GRPO_LOSS_FIXED ||
+                          (fixed_scale > 0.0f && fixed_scale < INFINITY);
+    at::Tensor weight;
+    if ((!has_mask || mask_code >= 0) && scale_ok) {
+        const at::Tensor mc = has_mask ? m.contiguous() : at::Tensor();
+        weight = at::empty({B, S}, at::TensorOptions().dtype(at::kFloat).device(dev));
+        const c10::hip::HIPGuard guard(static_cast<c10::DeviceIndex>(dev.index()));
+        hipStream_t stream =
+            c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev.index())).stream();
+        check_status(klp_grpo_token_weights(has_mask ? mc.data_ptr() : nullptr,
+                                            has_mask ? mask_code : KLP_MASK_U8, B, S,
+                                            static_cast<int>(weight_kind), fixed_scale,
+                                            weight.data_ptr<float>(), stream));
+    } else {
+        const at::Tensor mf =
+            has_mask ? m : at::ones({B, S}, at::TensorOptions().dtype(at::kFloat).device(dev));
+        weight = token_weights(mf, weight_kind, weight_scale).contiguous();
+    }
     // klp_grpo_step reads the weights as float32 [B, S].
     require(weight.scalar_type() == at::kFloat,
             "mask must be bool, integer or floating point (token weights are float32)");

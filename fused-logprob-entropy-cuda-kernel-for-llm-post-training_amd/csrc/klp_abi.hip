@@ -7,6 +7,7 @@
 // caller's stream, and a hipGetLastError() check after every launch (the
 // reference has none).  Nothing here allocates, frees or synchronises.
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <math.h>
 #include <string.h>
@@ -899,6 +900,40 @@ int klp_scale_inplace(void* data, int dtype, int64_t n, const float* scale, void
     p.scale = scale;
     if (injected_failure("scale")) return KLP_ELAUNCH;
     return after_launch(klp::launch_scale(dtype, p, static_cast<hipStream_t>(stream)), "scale");
+}
+
+int klp_grpo_token_weights(const void* mask, int mask_dtype, int64_t n_seqs, int64_t seq_len,
+                           int loss_type, float scale, float* weights, void* stream) {
+    if (n_seqs < 0 || seq_len < 0) return fail(KLP_EINVAL, "n_seqs and seq_len must be >= 0");
+    if (loss_type != KLP_GRPO_LOSS_GRPO && loss_type != KLP_GRPO_LOSS_BNPO &&
+        loss_type != KLP_GRPO_LOSS_FIXED)
+        return fail(KLP_EINVAL, "unknown loss_type %d", loss_type);
+    if (mask != nullptr && mask_dtype != KLP_MASK_U8 && mask_dtype != KLP_MASK_I32 &&
+        mask_dtype != KLP_MASK_I64)
+        return fail(KLP_EDTYPE, "mask must be bool / uint8, int32 or int64");
+    if (n_seqs > 0 && seq_len > INT64_MAX / n_seqs)
+        return fail(KLP_EINVAL, "n_seqs * seq_len overflows");
+    if (n_seqs * seq_len == 0) return ok();
+    if (weights == nullptr || !aligned(weights, 4))
+        return fail(KLP_EINVAL, "weights must be non-null and 4-byte aligned");
+    if (mask != nullptr) {
+        const size_t a = mask_dtype == KLP_MASK_I64 ? 8 : mask_dtype == KLP_MASK_I32 ? 4 : 1;
+        if (!aligned(mask, a)) return fail(KLP_EINVAL, "mask must be aligned to its element size");
+    }
+    if (loss_type == KLP_GRPO_LOSS_FIXED && !(scale > 0.0f && scale < INFINITY))
+        return fail(KLP_EINVAL, "scale (1 / normaliser) must be finite and > 0, got %g",
+                    static_cast<double>(scale));
+    klp::TokenWeightsParams p;
+    p.mask = mask;
+    p.mask_dtype = mask_dtype;
+    p.kind = loss_type;
+    p.B = n_seqs;
+    p.S = seq_len;
+    p.scale = scale;
+    p.weights = weights;
+    if (injected_failure("grpo_token_weights")) return KLP_ELAUNCH;
+    return after_launch(klp::launch_grpo_token_weights(p, static_cast<hipStream_t>(stream)),
+                        "grpo_token_weights");
 }
 
 int64_t klp_grpo_step_max_vocab(int dtype) {

@@ -22,6 +22,8 @@
 // fixed order, the loss and statistics), klp_grpo_bwd_kernel (one workgroup
 // per row: the gradient, scaled by the upstream gradient of the loss).  All
 // reductions have a fixed order, so results do not depend on timing.
+#include <type_traits>
+
 #include "klp_grpo_terms.h"
 #include "klp_launch.h"
 
@@ -204,6 +206,120 @@ __global__ __launch_bounds__(kGrpoThreads) void klp_grpo_bwd_kernel(GrpoParams p
         const TokenLoss t = token_loss(p, lp - p.old_logp[i], adv_at(p, b, i), lp,
                                        has_ref ? p.ref_logp[i] : 0.0f, has_ref);
         p.d_logp[i] = (t.dw + t.dlp) * m * scale;
+    }
+}
+
+namespace {
+
+constexpr int kWeightThreads = 1024;
+constexpr int kWeightWaves = kWeightThreads / 64;
+
+// Mask element i as an integer: M is the mask's element type, void for no
+// mask (all ones).
+template <typename M>
+__device__ __forceinline__ int64_t mask_value(const void* mask, int64_t i) {
+    if constexpr (std::is_void_v<M>) {
+        return 1;
+    } else {
+        return static_cast<int64_t>(static_cast<const M*>(mask)[i]);
+    }
+}
+
+// 64-bit integer sum over a wave (xor tree on the two 32-bit halves).
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const int lo = __shfl_xor(static_cast<int>(static_cast<uint64_t>(v)), off, 64);
+        const int hi = __shfl_xor(static_cast<int>(static_cast<uint64_t>(v) >> 32), off, 64);
+        v += static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                  static_cast<uint32_t>(lo));
+    }
+    return v;
+}
+
+}  // namespace
+
+// The GRPO step's token weights w = m / normaliser in one workgroup:
+//   Kind 0 ("grpo"): m * (1 / (max(row sum of m, 1) * B)), row by row,
+//   Kind 1 ("bnpo"): m * (1 / max(sum of m, 1)),
+//   Kind 2 (fixed):  m * scale.
+// The mask's sums are taken exactly in 64-bit integers and rounded once to
+// float32, then the same float32 operations as the eager statement
+// (grpo_step.grpo_token_weights) follow: the weights are its bits whenever
+// those sums are below 2^24, as the sums of any 0 / 1 mask of fewer than
+// 2^24 tokens are (the eager float32 sums of integers are exact there, in
+// any order).  One wave per row for kind 0; a fixed-order block sum for
+// kind 1.  One instance per (kind, mask element type): each is a single
+// straight loop nest, and every 64-bit index starts from the zero-extended
+// thread id.
+template <int Kind, typename M>
+__global__ __launch_bounds__(kWeightThreads) void klp_grpo_token_weights_kernel(
+    TokenWeightsParams p) {
+    const uint32_t tid = threadIdx.x;
+    const int64_t lane = static_cast<int64_t>(tid & 63u);
+    const int64_t wave = static_cast<int64_t>(tid >> 6);
+    if constexpr (Kind == 0) {
+        for (int64_t b = wave; b < p.B; b += kWeightWaves) {
+            const int64_t base = b * p.S;
+            int64_t v = 0;
+            for (int64_t s = lane; s < p.S; s += 64) v += mask_value<M>(p.mask, base + s);
+            v = wave_sum_i64(v);
+            const float den = fmaxf(static_cast<float>(v), 1.0f) * static_cast<float>(p.B);
+            const float r = 1.0f / den;
+            for (int64_t s = lane; s < p.S; s += 64)
+                p.weights[base + s] = static_cast<float>(mask_value<M>(p.mask, base + s)) * r;
+        }
+    } else {
+        const int64_t n = p.B * p.S;
+        const int64_t first = static_cast<int64_t>(tid);
+        float r = p.scale;
+        if constexpr (Kind == 1) {
+            __shared__ int64_t part[kWeightWaves];
+            int64_t v = 0;
+            for (int64_t i = first; i < n; i += kWeightThreads) v += mask_value<M>(p.mask, i);
+            v = wave_sum_i64(v);
+            if (lane == 0) part[wave] = v;
+            __syncthreads();
+            int64_t tot = 0;
+#pragma unroll
+            for (int w = 0; w < kWeightWaves; ++w) tot += part[w];
+            r = 1.0f / fmaxf(static_cast<float>(tot), 1.0f);
+        }
+        for (int64_t i = first; i < n; i += kWeightThreads)
+            p.weights[i] = static_cast<float>(mask_value<M>(p.mask, i)) * r;
+    }
+}
+
+namespace {
+
+template <int Kind>
+hipError_t launch_token_weights_kind(const TokenWeightsParams& p, hipStream_t stream) {
+    const dim3 grid(1), block(kWeightThreads);
+    if (p.mask == nullptr)
+        return launch_kernel(klp_grpo_token_weights_kernel<Kind, void>, grid, block, stream, p);
+    switch (p.mask_dtype) {
+        case KLP_MASK_U8:
+            return launch_kernel(klp_grpo_token_weights_kernel<Kind, uint8_t>, grid, block,
+                                 stream, p);
+        case KLP_MASK_I32:
+            return launch_kernel(klp_grpo_token_weights_kernel<Kind, int32_t>, grid, block,
+                                 stream, p);
+        case KLP_MASK_I64:
+            return launch_kernel(klp_grpo_token_weights_kernel<Kind, int64_t>, grid, block,
+                                 stream, p);
+        default:
+            return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_grpo_token_weights(const TokenWeightsParams& p, hipStream_t stream) {
+    switch (p.kind) {
+        case 0: return launch_token_weights_kind<0>(p, stream);
+        case 1: return launch_token_weights_kind<1>(p, stream);
+        case 2: return launch_token_weights_kind<2>(p, stream);
+        default: return hipErrorInvalidValue;
     }
 }
 

@@ -130,6 +130,19 @@ struct GrpoParams {
 // Workspace words per row of the GRPO loss (5 used, padded).
 constexpr int kGrpoRowWords = 8;
 
+// Token weights of the GRPO step (klp_grpo_token_weights): a bool / uint8,
+// int32 or int64 mask (or none: all ones) divided by the loss type's
+// normaliser.
+struct TokenWeightsParams {
+    const void* mask;  // nullable (all ones)
+    int mask_dtype;    // KLP_MASK_U8 / KLP_MASK_I32 / KLP_MASK_I64
+    int kind;          // 0 "grpo", 1 "bnpo", 2 fixed (scale)
+    int64_t B;
+    int64_t S;
+    float scale;       // kind 2: the normaliser's float32 reciprocal
+    float* weights;    // [B, S]
+};
+
 // Row counter of the persistent GRPO step kernel (klp_grpo_step's `sched`):
 // zero before a launch, and left zero by it.
 struct StepSched {
@@ -240,6 +253,7 @@ hipError_t launch_fwd_naive(int dtype, const NaiveParams& p, hipStream_t stream)
 hipError_t launch_bwd(int dtype, const BwdParams& p, const BwdConfig& c, hipStream_t stream);
 hipError_t launch_grpo_fwd(const GrpoParams& p, hipStream_t stream);
 hipError_t launch_grpo_bwd(const GrpoParams& p, hipStream_t stream);
+hipError_t launch_grpo_token_weights(const TokenWeightsParams& p, hipStream_t stream);
 bool fwd_config_supported(const FwdConfig& c);
 bool bwd_config_supported(const BwdConfig& c);
 

@@ -354,6 +354,31 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                   void* d_logits, void* sched, void* stream);
 
 /*
+ * The fused GRPO step's token weights from a mask, in one launch: weights
+ * [n_seqs, seq_len] float32 = m / normaliser with m the mask (NULL: all
+ * ones) and the normaliser of `loss_type` (KLP_GRPO_LOSS_GRPO: n_seqs *
+ * max(row sum of m, 1), row by row; KLP_GRPO_LOSS_BNPO: max(sum of m, 1);
+ * KLP_GRPO_LOSS_FIXED: `scale` is the normaliser's float32 reciprocal), as
+ * weights = m * (1 / normaliser).  No counterpart in the reference, whose
+ * loss divides by the normaliser in eager PyTorch
+ * (examples/compare_one_step.py:232-236); it replaces the chain of small
+ * launches (row sums, clamp, scale, reciprocal, product) that computes
+ * klp_grpo_step's tok_weight from the mask.  mask_dtype: KLP_MASK_U8 (bool
+ * or uint8), KLP_MASK_I32, KLP_MASK_I64; the mask's sums are exact 64-bit
+ * integer sums rounded once to float32, so the weights equal the float32
+ * eager computation's bits whenever those sums are below 2^24 (any 0 / 1
+ * mask of fewer than 2^24 tokens).  Floating-point masks are not taken.
+ */
+enum klp_mask_dtype {
+    KLP_MASK_U8 = 0,
+    KLP_MASK_I32 = 1,
+    KLP_MASK_I64 = 2
+};
+
+int klp_grpo_token_weights(const void* mask, int mask_dtype, int64_t n_seqs, int64_t seq_len,
+                           int loss_type, float scale, float* weights, void* stream);
+
+/*
  * data[i] *= *scale for i in [0, n), in place, on the stream: each element is
  * multiplied in fp32 and rounded once to `dtype` (RNE), as torch's
  * `tensor * float` computes it.  `scale` is a device pointer read by the

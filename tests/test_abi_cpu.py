@@ -445,6 +445,35 @@ def test_scale_inplace_validation_errors():
         lib.klp_debug_fail_next_launches(0)
 
 
+def test_grpo_token_weights_validation_errors():
+    """klp_grpo_token_weights rejects bad arguments before any launch; an
+    empty batch is a no-op; an injected launch failure is reported."""
+    from kernel_opt._library import KLP_EDTYPE, KLP_EINVAL, KLP_ELAUNCH, lib
+    A = ctypes.c_void_p(0x100000)
+
+    def tw(**kw):
+        a = dict(m=A, md=1, B=4, S=8, kind=0, scale=1.0, w=A)
+        a.update(kw)
+        return lib.klp_grpo_token_weights(a["m"], a["md"], a["B"], a["S"], a["kind"],
+                                          a["scale"], a["w"], None)
+    assert tw(B=0) == 0 and tw(S=0, m=None, w=None) == 0
+    assert tw(B=-1) == KLP_EINVAL and "n_seqs" in _err()
+    assert tw(kind=3) == KLP_EINVAL and "loss_type" in _err()
+    assert tw(md=3) == KLP_EDTYPE and "mask" in _err()
+    assert tw(w=None) == KLP_EINVAL and "weights" in _err()
+    assert tw(w=ctypes.c_void_p(0x100002)) == KLP_EINVAL and "weights" in _err()
+    assert tw(m=ctypes.c_void_p(0x100002)) == KLP_EINVAL and "mask" in _err()       # int32
+    assert tw(md=2, m=ctypes.c_void_p(0x100004)) == KLP_EINVAL and "mask" in _err()  # int64
+    assert tw(kind=2, scale=0.0) == KLP_EINVAL and "scale" in _err()
+    assert tw(kind=2, scale=float("inf")) == KLP_EINVAL and "scale" in _err()
+    assert tw(B=1 << 62, S=8) == KLP_EINVAL and "overflows" in _err()
+    lib.klp_debug_fail_next_launches(1)
+    try:
+        assert tw(md=0, m=ctypes.c_void_p(0x100001)) == KLP_ELAUNCH and "token_weights" in _err()
+    finally:
+        lib.klp_debug_fail_next_launches(0)
+
+
 def test_ceiling_validation_errors():
     """klp_ceiling_read / _copy / _read_pieces / _write reject bad arguments
     before any launch; n_rows = 0 is a no-op; an injected launch failure is

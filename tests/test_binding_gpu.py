@@ -310,6 +310,42 @@ def test_compiled_grpo_step_equals_python_function(monkeypatch, dtype, shape, st
     assert "CppNode" not in res[1][5], res[1][5]
 
 
+@pytest.mark.parametrize("normalizer", [-4.0, 0.0])
+@pytest.mark.parametrize("mask_kind", ["bool", "int64", None])
+def test_compiled_grpo_step_nonpositive_normalizer(monkeypatch, normalizer, mask_kind):
+    """A zero or negative "dapo" normaliser: the binding keeps the eager
+    statement's weights (negative, or inf / nan), the Python path's bits in
+    the loss, logp, entropy and d_logits."""
+    from kernel_opt import fused_grpo_step, grpo_step
+    B, S, V = 3, 20, 4096
+    base = seeded_logits((B, S, V), torch.bfloat16, seed=11).to(DEV)
+    t = seeded_targets((B, S), V, seed=12).to(DEV)
+    g = torch.Generator().manual_seed(13)
+    old = (-torch.rand(B, S, generator=g) * 3).to(DEV)
+    adv = torch.randn(B, generator=g).to(DEV)
+    m = torch.rand(B, S, generator=g) < 0.8
+    mask = None if mask_kind is None else m.to(getattr(torch, mask_kind)).to(DEV)
+
+    def bits(x):
+        x = x.detach().contiguous()
+        return x.view({4: torch.int32, 2: torch.int16}[x.element_size()])
+
+    res = []
+    for python_path in (False, True):
+        if python_path:
+            monkeypatch.setattr(grpo_step, "binding", _StepPythonPathOnly)
+        leaf = base.clone().requires_grad_(True)
+        loss, lp, ent = fused_grpo_step(leaf, t, old, adv, mask, loss_type="dapo",
+                                        normalizer=normalizer)
+        loss.backward()
+        res.append([bits(loss), bits(lp), bits(ent), bits(leaf.grad), loss.grad_fn.name()])
+    for a, b in zip(res[0][:4], res[1][:4]):
+        assert torch.equal(a, b)
+    assert "FusedGrpoStep" in res[0][4], res[0][4]
+    if normalizer < 0:
+        assert torch.isfinite(res[0][0].view(torch.float32)).all()
+
+
 def test_compiled_grpo_step_backward_once_and_fallback():
     from kernel_opt import fused_grpo_step
     x = seeded_logits((2, 5, 4096), torch.bfloat16, seed=3).to(DEV).requires_grad_(True)

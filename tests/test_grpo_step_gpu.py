@@ -531,3 +531,39 @@ def test_persistent_rows_only_where_they_pay():
                          (KLP_FP32, 16384)):
             assert lib.klp_grpo_step_persistent_min_rows(dtype, V, scaled) == 0, (dtype, V)
         assert lib.klp_grpo_step_persistent_min_rows(KLP_BF16, 155656, scaled) == 0
+
+
+@pytest.mark.parametrize("B,S", [(1, 1), (3, 1000), (4, 256), (16, 2048), (2, 70001)])
+@pytest.mark.parametrize("mask_kind", ["bool", "uint8", "int32", "int64", "none"])
+def test_token_weights_kernel_matches_eager(B, S, mask_kind):
+    """klp_grpo_token_weights (one launch) writes the bits of the eager
+    statement grpo_step.grpo_token_weights for every loss type: bool / uint8
+    / int32 / int64 0 / 1 masks (one all-zero row, whose normaliser clamps
+    to 1) and no mask."""
+    import ctypes
+    from kernel_opt._library import check_status, lib
+    from kernel_opt.grpo_step import grpo_token_weights
+    print(f"token weights B={B} S={S} mask={mask_kind}", flush=True)
+    g = torch.Generator().manual_seed(B * 7919 + S)
+    m01 = (torch.rand(B, S, generator=g) < 0.7)
+    if B > 1:
+        m01[1] = False
+    codes = {"bool": 0, "uint8": 0, "int32": 1, "int64": 2}
+    dt = {"bool": torch.bool, "uint8": torch.uint8, "int32": torch.int32, "int64": torch.int64}
+    mask = None if mask_kind == "none" else m01.to(dt[mask_kind]).to(DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    for kind, loss_type, kw in ((0, "grpo", {}), (1, "bnpo", {}), (2, "dr_grpo", {}),
+                                (2, "dapo", {"normalizer": 777.0})):
+        eager = grpo_token_weights(mask if mask is not None else torch.ones(B, S, device=DEV),
+                                   loss_type, **kw)
+        scale = 0.0
+        if kind == 2:
+            den = float(B * S) if loss_type == "dr_grpo" else kw["normalizer"]
+            scale = float(np.float32(1.0) / np.float32(den))
+        w = torch.full((B, S), -1.0, device=DEV)
+        check_status(lib.klp_grpo_token_weights(
+            mask.data_ptr() if mask is not None else None, codes.get(mask_kind, 0), B, S, kind,
+            ctypes.c_float(scale), w.data_ptr(), st))
+        torch.cuda.synchronize()
+        assert torch.equal(w.view(torch.int32), eager.float().contiguous().view(torch.int32)), \
+            f"{loss_type}: max |diff| {float((w - eager).abs().max()):.3g}"

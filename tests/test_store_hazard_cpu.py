@@ -17,17 +17,12 @@ from __future__ import annotations
 
 import os
 import re
-import shutil
-import subprocess
 
 import pytest
 
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-CSRC = os.path.join(ROOT, "fused-logprob-entropy-cuda-kernel-for-llm-post-training_amd", "csrc")
-HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-         "--cuda-device-only", "-S"]
+import isa_listing
+
+CSRC = isa_listing.CSRC
 WAIT_STATES = 2
 
 STORE = re.compile(r"buffer_store_dwordx[34] v\[(\d+):(\d+)\]")
@@ -105,14 +100,10 @@ def test_detector_flags_the_pattern_that_failed():
     assert len(hazards(late)) == 1  # one wait state passed, two are needed
 
 
-@pytest.mark.skipif(not shutil.which(HIPCC) and not os.path.exists(HIPCC),
-                    reason="hipcc not available")
+@pytest.mark.skipif(not isa_listing.available(), reason="hipcc not available")
 @pytest.mark.parametrize("source", _sources_with_buffer_stores())
-def test_buffer_stores_have_wait_states(source, tmp_path):
-    out = tmp_path / (source + ".s")
-    subprocess.run([HIPCC, *FLAGS, os.path.join(CSRC, source), "-o", str(out)],
-                   check=True, capture_output=True, timeout=600)
-    listing = out.read_text()
+def test_buffer_stores_have_wait_states(source):
+    listing = isa_listing.listing(source)
     n_stores = len(STORE.findall(listing))
     assert n_stores > 0, f"{source}: no buffer stores in the listing"
     found = hazards(listing)
