@@ -240,9 +240,11 @@ def _rocprof_csv(directory: str, suffix: str):
 
 def short_kernel(name: str) -> str:
     """'void klp::klp_bwd_kernel<0, 16, 2, true, false>(klp::BwdParams)' ->
-    'klp_bwd_kernel<0, 16, 2, true, false>'; other names unchanged up to
-    the argument list."""
-    m = re.match(r"(?:void )?(?:klp::)?([A-Za-z_0-9]+(?:<[^()]*>)?)", name)
+    'klp_bwd_kernel<0, 16, 2, true, false>' (also through an anonymous
+    namespace: 'void klp::(anonymous namespace)::klp_scale_kernel(...)' ->
+    'klp_scale_kernel'); other names unchanged up to the argument list."""
+    m = re.match(r"(?:void )?(?:klp::)?(?:\(anonymous namespace\)::)?"
+                 r"([A-Za-z_0-9]+(?:<[^()]*>)?)", name)
     return m.group(1) if m else name
 
 

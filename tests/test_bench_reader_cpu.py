@@ -137,6 +137,11 @@ def test_short_kernel_names():
     assert bench.short_kernel(BWD) == "klp_bwd_kernel<0, 16, 2, true, false>"
     assert bench.short_kernel("void klp::klp_fwd_shard_merge_kernel(klp::ShardMergeParams)") == \
         "klp_fwd_shard_merge_kernel"
+    assert bench.short_kernel("void klp::(anonymous namespace)::klp_scale_kernel"
+                              "(klp::ScaleParams)") == "klp_scale_kernel"
+    assert bench.short_kernel("void klp::klp_grpo_token_weights_kernel<0, unsigned char>"
+                              "(klp::TokenWeightsParams)") == \
+        "klp_grpo_token_weights_kernel<0, unsigned char>"
 
 
 def test_labelled_trace_is_not_the_configs(tmp_path, monkeypatch):
