@@ -633,8 +633,8 @@ def grpo_step_timing(dev, K, logits, targets):
     def fused():
         check_status(lib.klp_grpo_step(P(logits), DTYPE_CODES[logits.dtype], N, V, *rows,
                                        P(targets), 1.0, P(old), P(ref), P(adv), P(w), S,
-                                       eps_low, eps_high, beta, 0, P(lp), P(ent), P(lse),
-                                       P(loss_tok), P(d), P(sched), st))
+                                       eps_low, eps_high, beta, 0, 1.0, P(lp), P(ent),
+                                       P(lse), P(loss_tok), P(d), P(sched), st))
 
     def unfused():
         _C.fwd_launch(logits, targets, lp, ent, lse)
@@ -688,8 +688,24 @@ def grpo_step_timing(dev, K, logits, targets):
         loss_.backward()
         x.grad = None
 
+    # A trainer with 8 gradient-accumulation steps backpropagates loss / 8:
+    # undeclared, the backward multiplies d_logits by 1/8 (a read and a
+    # write of it); declared as grad_scale, the forward applies it.
+    def step_fused_ga8():
+        loss_, _, _ = fused_grpo_step(x, targets, old, adv, mask_i32, ref, **kw)
+        (loss_ / 8).backward()
+        x.grad = None
+
+    def step_fused_ga8_declared():
+        loss_, _, _ = fused_grpo_step(x, targets, old, adv, mask_i32, ref, grad_scale=0.125,
+                                      **kw)
+        (loss_ / 8).backward()
+        x.grad = None
+
     e2e = {}
     for name, fn in (("fused", step_fused), ("fused_int32_mask", step_fused_int32_mask),
+                     ("fused_loss_over_8", step_fused_ga8),
+                     ("fused_loss_over_8_grad_scale", step_fused_ga8_declared),
                      ("unfused", step_unfused)):
         for _ in range(3):
             fn()
@@ -721,7 +737,9 @@ def grpo_step_timing(dev, K, logits, targets):
                     "backward), host-paced and *_queued (GPU time), with a float32 mask "
                     "(token weights in eager torch) and fused_int32_mask with the same mask "
                     "as int32, as TRL's completion_mask comes (token weights in one "
-                    "klp_grpo_token_weights launch)"}
+                    "klp_grpo_token_weights launch); fused_loss_over_8: (loss / 8).backward(), "
+                    "as under 8 gradient-accumulation steps, without and with grad_scale=1/8 "
+                    "declared (undeclared, the backward rescales d_logits)"}
 
 
 def shard_timing(dev, K, N=32768, V=151936, P=8):

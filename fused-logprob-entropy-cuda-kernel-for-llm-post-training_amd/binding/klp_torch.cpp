@@ -607,7 +607,8 @@ class FusedGrpoStep : public torch::autograd::Function<FusedGrpoStep> {
                                  const at::Tensor& targets, const at::Tensor& old,
                                  const std::optional<at::Tensor>& ref, const at::Tensor& adv,
                                  const at::Tensor& weight, double temperature, double eps_low,
-                                 double eps_high, double beta, int64_t per_token) {
+                                 double eps_high, double beta, int64_t per_token,
+                                 double grad_scale) {
         const int64_t B = logits.size(0), S = logits.size(1), V = logits.size(2);
         const auto rows = row_layout(logits);
         require(rows.has_value(), "logits must be contiguous");
@@ -626,15 +627,17 @@ class FusedGrpoStep : public torch::autograd::Function<FusedGrpoStep> {
             logits.data_ptr(), dtype_code(logits.scalar_type()), B * S, V, L[0], L[1], L[2],
             targets.data_ptr<int64_t>(), static_cast<float>(temperature), fptr(old), fptr(r),
             fptr(adv), fptr(weight), S, static_cast<float>(eps_low), static_cast<float>(eps_high),
-            static_cast<float>(beta), static_cast<int>(per_token), out_ptr(logp), out_ptr(ent),
-            out_ptr(lse), out_ptr(loss_tok), d_logits.data_ptr(), sched.data_ptr(), stream));
+            static_cast<float>(beta), static_cast<int>(per_token), static_cast<float>(grad_scale),
+            out_ptr(logp), out_ptr(ent), out_ptr(lse), out_ptr(loss_tok), d_logits.data_ptr(),
+            sched.data_ptr(), stream));
         ctx->saved_data["d_logits"] = d_logits;
+        ctx->saved_data["grad_scale"] = grad_scale;
         ctx->mark_non_differentiable({logp, ent});
         return {loss_tok.sum(), logp, ent};
     }
 
     static variable_list backward(AutogradContext* ctx, variable_list grads) {
-        variable_list none(11);
+        variable_list none(12);
         c10::IValue& held = ctx->saved_data["d_logits"];
         if (!held.isTensor())
             throw std::runtime_error(
@@ -652,12 +655,13 @@ class FusedGrpoStep : public torch::autograd::Function<FusedGrpoStep> {
             throw std::runtime_error(
                 "kernel_opt: this backward belongs to a forward run outside graph capture and "
                 "cannot itself be captured; capture the forward with it");
-        // d *= g on the device (grpo_step.scale_by_upstream): nothing is
-        // written when g is exactly 1.
+        // d *= g / grad_scale on the device (grpo_step.scale_by_upstream):
+        // nothing is written when g equals the declared grad_scale.
+        const float applied = static_cast<float>(ctx->saved_data["grad_scale"].toDouble());
         const at::Tensor g = grads[0].detach().to(d.device(), at::kFloat).reshape({1}).contiguous();
         const c10::hip::HIPGuard guard(static_cast<c10::DeviceIndex>(dev));
-        check_status(klp_scale_inplace(d.data_ptr(), dtype_code(d.scalar_type()), d.numel(),
-                                       fptr(g), stream));
+        check_status(klp_rescale_inplace(d.data_ptr(), dtype_code(d.scalar_type()), d.numel(),
+                                         fptr(g), applied, stream));
         none[0] = d;
         return none;
     }
@@ -670,7 +674,7 @@ std::optional<std::vector<at::Tensor>> fused_grpo_step(
     const at::Tensor& logits, const at::Tensor& targets, const at::Tensor& old_logp,
     const at::Tensor& advantages, const std::optional<at::Tensor>& mask,
     const std::optional<at::Tensor>& ref_logp, double temperature, double eps_low,
-    double eps_high, double beta, int64_t weight_kind, double weight_scale) {
+    double eps_high, double beta, int64_t weight_kind, double weight_scale, double grad_scale) {
     require(logits.is_cuda() && logits.dim() == 3, "logits must be a [B, S, V] GPU tensor");
     decline_under_capture(logits.get_device());
     if (!grpo_step_supported(logits, row_layout(logits))) return std::nullopt;
@@ -746,7 +750,7 @@ std::optional<std::vector<at::Tensor>> fused_grpo_step(
     auto out = FusedGrpoStep::apply(logits, targets, old,
                                     ref.defined() ? std::optional<at::Tensor>(ref) : std::nullopt,
                                     adv, weight, temperature, eps_low, eps_high, beta,
-                                    static_cast<int64_t>(per_token));
+                                    static_cast<int64_t>(per_token), grad_scale);
     return std::vector<at::Tensor>{out[0], out[1], out[2]};
 }
 
@@ -823,7 +827,7 @@ PYBIND11_MODULE(klp_torch, m) {
           pybind11::arg("old_logp"), pybind11::arg("advantages"), pybind11::arg("mask"),
           pybind11::arg("ref_logp"), pybind11::arg("temperature"), pybind11::arg("eps_low"),
           pybind11::arg("eps_high"), pybind11::arg("beta"), pybind11::arg("weight_kind"),
-          pybind11::arg("weight_scale"));
+          pybind11::arg("weight_scale"), pybind11::arg("grad_scale") = 1.0);
     m.def(
         "workspaces_cached",
         []() {

@@ -881,6 +881,14 @@ int klp_fwd_shard_merge(const float* states, int64_t n_shards, int64_t n_rows,
 }
 
 int klp_scale_inplace(void* data, int dtype, int64_t n, const float* scale, void* stream) {
+    return klp_rescale_inplace(data, dtype, n, scale, 1.0f, stream);
+}
+
+int klp_rescale_inplace(void* data, int dtype, int64_t n, const float* scale, float applied,
+                        void* stream) {
+    if (!(applied == applied) || applied == INFINITY || applied == -INFINITY || applied == 0.0f)
+        return fail(KLP_EINVAL, "applied must be finite and non-zero, got %g",
+                    static_cast<double>(applied));
     if (dtype != KLP_BF16 && dtype != KLP_FP16 && dtype != KLP_FP32)
         return fail(KLP_EDTYPE, "dtype must be bf16, fp16, or fp32");
     if (n < 0) return fail(KLP_EINVAL, "n must be >= 0");
@@ -898,6 +906,7 @@ int klp_scale_inplace(void* data, int dtype, int64_t n, const float* scale, void
     if (p.head > n) p.head = n;
     p.nvec = (n - p.head) / (16 / esz);
     p.scale = scale;
+    p.applied = applied;
     if (injected_failure("scale")) return KLP_ELAUNCH;
     return after_launch(klp::launch_scale(dtype, p, static_cast<hipStream_t>(stream)), "scale");
 }
@@ -946,8 +955,8 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                   const int64_t* targets, float temperature, const float* old_logp,
                   const float* ref_logp, const float* advantages, const float* tok_weight,
                   int64_t seq_len, float eps_low, float eps_high, float beta, int adv_per_token,
-                  float* logprob, float* entropy, float* lse, float* loss_tok, void* d_logits,
-                  void* sched, void* stream) {
+                  float grad_scale, float* logprob, float* entropy, float* lse, float* loss_tok,
+                  void* d_logits, void* sched, void* stream) {
     int rc = check_rows(logits, dtype, n_rows, vocab, rows_inner, stride_outer, stride_inner,
                         targets);
     if (rc != KLP_OK) return rc;
@@ -981,6 +990,10 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
         return fail(KLP_EINVAL, "eps_low and eps_high must be finite and >= 0");
     if (!(beta == beta) || beta == INFINITY || beta == -INFINITY)
         return fail(KLP_EINVAL, "beta must be finite");
+    if (!(grad_scale == grad_scale) || grad_scale == INFINITY || grad_scale == -INFINITY ||
+        grad_scale == 0.0f)
+        return fail(KLP_EINVAL, "grad_scale must be finite and non-zero, got %g",
+                    static_cast<double>(grad_scale));
     if (sched != nullptr && !aligned(sched, 8))
         return fail(KLP_EINVAL, "sched must be 8-byte aligned");
     if ((rc = check_grid(n_rows, 1, klp::kGrpoStepThreads)) != KLP_OK) return rc;
@@ -1001,6 +1014,7 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
     p.eps_high = eps_high;
     p.beta = beta;
     p.adv_per_token = adv_per_token != 0;
+    p.grad_scale = grad_scale;
     p.logprob = logprob;
     p.entropy = entropy;
     p.lse = lse;

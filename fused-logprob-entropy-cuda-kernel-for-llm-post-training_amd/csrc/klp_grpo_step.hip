@@ -6,8 +6,12 @@
 // ref_t) with a per-token weight w_t known in advance (mask / normaliser),
 // and the entropy is not differentiated.  So once a row's logsumexp is known,
 // its d_logits can be written at once (klp_bwd's formula with
-// g_logp = w_t * dl_t, g_ent = g_lse = 0):
-//   d[v] = (onehot(v == t) - p_v) * g_logp          (times 1/T).
+// g_logp = w_t * dl_t * c, g_ent = g_lse = 0):
+//   d[v] = (onehot(v == t) - p_v) * g_logp          (times 1/T),
+// where c (grad_scale) is the upstream gradient the caller will send into
+// the loss, declared in advance (1 for loss.backward(); 1 / k when a
+// trainer divides the loss by k gradient-accumulation steps), so that the
+// backward has nothing left to do.
 // The unfused step reads the logits twice (forward, backward) and writes
 // d_logits once; here one workgroup of 1024 threads keeps its whole row in
 // registers, so the logits are read once: 2 passes of HBM traffic instead
@@ -182,7 +186,7 @@ __device__ __forceinline__ RowGrad row_results(const GrpoStepParams& p, int64_t 
         // GRPO terms of this token (token-level importance weight).
         const TokenLoss tl = grpo_token_loss(eps_low, eps_high, beta, o.logp - in.old_lp,
                                              in.adv, o.logp, in.ref_lp, has_ref);
-        const float g_logp = in.wt * (tl.dw + tl.dlp);
+        const float g_logp = in.wt * (tl.dw + tl.dlp) * p.grad_scale;
         if (lane == 0) {
             if (kPublishNext) sh.next_row = next_row;
             sh.row_vals[0] = o.lse;

@@ -169,6 +169,7 @@ struct GrpoStepParams {
     float eps_high;
     float beta;
     int adv_per_token;
+    float grad_scale;         // multiplies every token's gradient (not its loss)
     float* logprob;           // [n_rows]
     float* entropy;           // [n_rows]
     float* lse;               // [n_rows], nullable
@@ -192,7 +193,8 @@ struct ScaleParams {
     int64_t n;
     int64_t head;
     int64_t nvec;
-    const float* scale;
+    const float* scale;       // device scalar g
+    float applied;            // data holds values already scaled by this; factor g / applied
 };
 
 hipError_t launch_scale(int dtype, const ScaleParams& p, hipStream_t stream);

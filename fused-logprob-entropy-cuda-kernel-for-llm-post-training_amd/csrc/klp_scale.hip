@@ -5,10 +5,13 @@
 // forward; the backward only multiplies them by the loss's upstream gradient.
 // That scalar lives on the device; reading it on the host would stall the
 // caller's stream (a synchronisation in every backward).  This kernel reads
-// it itself: when it is exactly 1 (loss.backward() on the loss) every
-// workgroup returns at once and nothing is written; otherwise each element
-// is multiplied in fp32 and rounded once to its dtype (RNE), as torch's
-// `tensor * float` does.
+// it itself.  The buffer may already hold the gradients scaled by the
+// upstream gradient the caller declared in advance (`applied`, 1 when none
+// was): when the scalar equals it (loss.backward() on the loss, or the
+// declared 1 / gradient-accumulation steps) every workgroup returns at once
+// and nothing is written; otherwise each element is multiplied in fp32 by
+// scalar / applied (the scalar itself when applied is 1) and rounded once to
+// its dtype (RNE), as torch's `tensor * float` does.
 #include "klp_launch.h"
 
 namespace klp {
@@ -20,8 +23,9 @@ constexpr int64_t kScaleMaxBlocks = 4096;
 
 template <int DT>
 __global__ __launch_bounds__(kScaleThreads) void klp_scale_kernel(ScaleParams p) {
-    const float s = *p.scale;
-    if (s == 1.0f) return;
+    const float g = *p.scale;
+    if (g == p.applied) return;
+    const float s = g / p.applied;  // g itself when applied is 1
     typedef typename Traits<DT>::elem elem;
     constexpr int EPV = Traits<DT>::kPerVec;
     elem* e = static_cast<elem*>(p.data);

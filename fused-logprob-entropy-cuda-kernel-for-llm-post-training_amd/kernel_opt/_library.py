@@ -73,9 +73,10 @@ SIGNATURES = {
                                      _vp]),
     "klp_grpo_step_max_vocab": (_i64, [_i32]),
     "klp_scale_inplace": (_i32, [_vp, _i32, _i64, _vp, _vp]),
+    "klp_rescale_inplace": (_i32, [_vp, _i32, _i64, _vp, ctypes.c_float, _vp]),
     "klp_grpo_token_weights": (_i32, [_vp, _i32, _i64, _i64, _i32, ctypes.c_float, _vp, _vp]),
     "klp_grpo_step": (_i32, _ROWS + [_vp, ctypes.c_float] + [_vp] * 4 + [_i64]
-                      + [ctypes.c_float] * 3 + [_i32] + [_vp] * 7),
+                      + [ctypes.c_float] * 3 + [_i32, ctypes.c_float] + [_vp] * 7),
     # include/kernel_opt_hip_tuning.h
     "klp_grpo_step_persistent_min_rows": (_i64, [_i32, _i64, _i32]),
     "klp_fwd_workspace_bytes_ex": (_sz, [_i64, _i32]),

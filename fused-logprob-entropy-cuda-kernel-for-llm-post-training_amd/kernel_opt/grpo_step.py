@@ -34,6 +34,7 @@ Restrictions of the fused path, by construction:
 from __future__ import annotations
 
 import collections
+import math
 import threading
 
 import numpy as np
@@ -133,8 +134,9 @@ def grpo_step_launch(logits, targets, old, ref, adv, weight, params):
     ``entropy``, ``lse``, ``loss_tok`` ``[B, S]`` and ``d_logits`` (dense,
     logits dtype).  ``old`` / ``ref`` / ``adv`` / ``weight`` are float32,
     contiguous, on the logits' device; ``params`` = (temperature, eps_low,
-    eps_high, beta, adv_per_token)."""
-    temperature, eps_low, eps_high, beta, per_token = params
+    eps_high, beta, adv_per_token, grad_scale): ``d_logits`` is the loss's
+    gradient times ``grad_scale``."""
+    temperature, eps_low, eps_high, beta, per_token, grad_scale = params
     B, S, V = logits.shape
     dev = logits.device
     rows = _C.row_layout(logits)
@@ -148,24 +150,26 @@ def grpo_step_launch(logits, targets, old, ref, adv, weight, params):
         rc = lib.klp_grpo_step(_ptr(logits), DTYPE_CODES[logits.dtype], B * S, V, *rows,
                                _ptr(targets), float(temperature), _ptr(old), _ptr(ref),
                                _ptr(adv), _ptr(weight), S, eps_low, eps_high, beta, per_token,
-                               _ptr(logp), _ptr(ent), _ptr(lse), _ptr(loss_tok), _ptr(d_logits),
+                               float(grad_scale), _ptr(logp), _ptr(ent), _ptr(lse), _ptr(loss_tok), _ptr(d_logits),
                                _ptr(_sched(dev.index, stream)), stream)
     check_status(rc)
     return logp, ent, lse, loss_tok, d_logits
 
 
-def scale_by_upstream(t: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
-    """``t *= g`` in place (``t`` contiguous, ``g`` a one-element tensor on
-    ``t``'s device) without reading ``g`` on the host: klp_scale_inplace reads
-    it on the device, multiplies in float32 and rounds once to ``t``'s dtype
-    (as ``t * float(g)`` would), and writes nothing when ``g == 1``."""
+def scale_by_upstream(t: torch.Tensor, g: torch.Tensor, applied: float = 1.0) -> torch.Tensor:
+    """``t *= g / applied`` in place (``t`` contiguous, already scaled by the
+    declared upstream gradient ``applied``; ``g`` a one-element tensor on
+    ``t``'s device) without reading ``g`` on the host: klp_rescale_inplace
+    reads it on the device, multiplies in float32 by ``g / applied`` (``g``
+    itself when ``applied`` is 1) and rounds once to ``t``'s dtype (as
+    ``t * float(g)`` would), and writes nothing when ``g == applied``."""
     if not t.is_contiguous():
         raise RuntimeError("scale_by_upstream needs a contiguous tensor")
     g32 = g.detach().to(device=t.device, dtype=torch.float32).reshape(1).contiguous()
     with device_guard(t.device.index):
         stream = stream_handle(t.device.index)
-        rc = lib.klp_scale_inplace(_ptr(t), DTYPE_CODES[t.dtype], t.numel(), _ptr(g32),
-                                   stream)
+        rc = lib.klp_rescale_inplace(_ptr(t), DTYPE_CODES[t.dtype], t.numel(), _ptr(g32),
+                                     float(applied), stream)
     check_status(rc)
     return t
 
@@ -177,6 +181,7 @@ class _FusedGrpoStep(torch.autograd.Function):
         logp, ent, _lse, loss_tok, d_logits = grpo_step_launch(logits, targets, old, ref, adv,
                                                                weight, params)
         ctx.d_logits = d_logits
+        ctx.grad_scale = params[5]
         ctx.mark_non_differentiable(logp, ent)
         return loss_tok.sum(), logp, ent
 
@@ -190,8 +195,9 @@ class _FusedGrpoStep(torch.autograd.Function):
         if g_loss is None or not ctx.needs_input_grad[0]:
             return None, None, None, None, None, None, None
         # The upstream gradient stays on the device (no host synchronisation);
-        # exactly 1 leaves d as it is.
-        return scale_by_upstream(d, g_loss), None, None, None, None, None, None
+        # exactly the declared grad_scale (1 by default) leaves d as it is.
+        return (scale_by_upstream(d, g_loss, ctx.grad_scale), None, None, None, None, None,
+                None)
 
 
 def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch.Tensor,
@@ -200,13 +206,22 @@ def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch
                     eps_high: float | None = None, beta: float = 0.0, loss_type: str = "bnpo",
                     importance_level: str = "token", max_completion_length: int | None = None,
                     normalizer: float | None = None, temperature: float | None = None,
-                    return_stats: bool = False):
+                    return_stats: bool = False, grad_scale: float = 1.0):
     """GRPO loss of ``logits`` ``[B, S, V]`` (the completion window, rows as
     :func:`kernel_opt.fused_logprob_entropy` accepts them) for ``targets``
     ``[B, S]`` (int64), differentiable in ``logits``.
 
     The loss arguments are those of :func:`kernel_opt.fused_grpo_loss`;
     ``temperature`` divides the logits as in ``fused_logprob_entropy``.
+
+    ``grad_scale`` declares the upstream gradient the caller's backward will
+    send into the loss: 1 for ``loss.backward()``, ``1 / k`` when a trainer
+    divides the loss by ``k`` gradient-accumulation steps.  The fused kernel
+    writes d_logits already multiplied by it, so the backward writes nothing
+    when the upstream gradient equals it; any other upstream gradient is
+    still applied (one more pass over d_logits, multiplied by the ratio).
+    It changes no value beyond rounding, and the unfused composition ignores
+    it.
 
     Returns ``(loss, logp, entropy)``, or ``(loss, logp, entropy, stats)``
     with ``return_stats`` (stats as ``fused_grpo_loss`` returns them).
@@ -229,6 +244,7 @@ def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch
     t = 1.0 if temperature is None else float(temperature)
     if not (t > 0.0 and t != float("inf")):
         raise RuntimeError(f"temperature must be finite and > 0, got {t}")
+    gs = _check_grad_scale(grad_scale)
     loss_kw = dict(eps_low=eps_low, eps_high=eps_high, beta=beta, loss_type=loss_type,
                    importance_level=importance_level,
                    max_completion_length=max_completion_length, normalizer=normalizer)
@@ -244,11 +260,11 @@ def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch
         try:
             out = binding.fused_grpo_step(logits, targets, old_logp, advantages, mask,
                                           ref_logp, t, float(eps_low), float(eh), float(beta),
-                                          kind, scale)
+                                          kind, scale, gs)
         except binding.CaptureDeclined:
             out = _fused_python(logits, targets, old_logp, advantages, mask, ref_logp, t,
                                 float(eps_low), float(eh), float(beta), loss_type,
-                                max_completion_length, normalizer)
+                                max_completion_length, normalizer, gs)
         if out is not None:
             loss, logp, ent = out
             if not return_stats:
@@ -263,6 +279,16 @@ def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch
     logp, ent, _ = fused_logprob_entropy(logits, targets, temperature)
     loss, stats = fused_grpo_loss(logp, old_logp, advantages, mask, ref_logp, **loss_kw)
     return (loss, logp, ent, stats) if return_stats else (loss, logp, ent)
+
+
+def _check_grad_scale(grad_scale) -> float:
+    """``grad_scale`` as a float, finite and non-zero in float32 (the
+    kernels take it as float32)."""
+    gs = float(grad_scale)
+    if not (math.isfinite(gs) and abs(gs) <= float(np.finfo(np.float32).max)
+            and np.float32(gs) != 0):
+        raise ValueError(f"grad_scale must be finite and non-zero in float32, got {grad_scale}")
+    return gs
 
 
 def _weight_kind(B, S, loss_type, max_completion_length, normalizer):
@@ -283,7 +309,7 @@ def _weight_kind(B, S, loss_type, max_completion_length, normalizer):
 
 
 def _fused_python(logits, targets, old_logp, advantages, mask, ref_logp, t, eps_low, eps_high,
-                  beta, loss_type, max_completion_length, normalizer):
+                  beta, loss_type, max_completion_length, normalizer, grad_scale=1.0):
     """The fused path in Python (graph capture): (loss, logp, entropy), or
     None when klp_grpo_step does not take these logits."""
     if not _fused_supported(logits, _C.row_layout(logits)):
@@ -306,5 +332,5 @@ def _fused_python(logits, targets, old_logp, advantages, mask, ref_logp, t, eps_
          else torch.ones((B, S), dtype=torch.float32, device=dev))
     ref = f32(ref_logp, "ref_logp", (B, S)) if (beta != 0.0 and ref_logp is not None) else None
     weight = grpo_token_weights(m, loss_type, max_completion_length, normalizer).contiguous()
-    params = (t, eps_low, eps_high, beta, int(per_token))
+    params = (t, eps_low, eps_high, beta, int(per_token), grad_scale)
     return _FusedGrpoStep.apply(logits, targets, old, ref, adv, weight, params)

@@ -31,7 +31,7 @@ import torch
 
 from ._library import DTYPE_CODES, lib
 from .grpo import fused_grpo_loss
-from .grpo_step import grpo_step_launch, grpo_token_weights, scale_by_upstream
+from .grpo_step import _check_grad_scale, grpo_step_launch, grpo_token_weights, scale_by_upstream
 from .ops import fused_logprob_entropy
 
 __all__ = ["fused_linear_grpo_step"]
@@ -75,7 +75,7 @@ class _FusedLinearGrpoStep(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hidden, weight, targets, old, ref, adv, wts, params, chunk):
-        temperature, eps_low, eps_high, beta = params
+        temperature, eps_low, eps_high, beta, grad_scale = params
         D = hidden.size(-1)
         V = weight.size(0)
         h2 = hidden.reshape(-1, D)
@@ -88,7 +88,7 @@ class _FusedLinearGrpoStep(torch.autograd.Function):
         d_hidden = torch.empty_like(h2) if need_h else None
         d_weight = None
         single = chunk >= N
-        step_params = (temperature, eps_low, eps_high, beta, 1)  # per-token advantages
+        step_params = (temperature, eps_low, eps_high, beta, 1, grad_scale)  # per-token adv.
         for n0 in range(0, N, chunk):
             n1 = min(N, n0 + chunk)
             c = n1 - n0
@@ -113,6 +113,7 @@ class _FusedLinearGrpoStep(torch.autograd.Function):
         if need_w and not single and d_weight.dtype != weight.dtype:
             d_weight = d_weight.to(weight.dtype)
         ctx.grads = (d_hidden, d_weight)
+        ctx.grad_scale = grad_scale
         ctx.hidden_shape = hidden.shape
         logp, ent = logp.view(targets.shape), ent.view(targets.shape)
         ctx.mark_non_differentiable(logp, ent)
@@ -129,11 +130,12 @@ class _FusedLinearGrpoStep(torch.autograd.Function):
         if g_loss is None:
             return (None,) * 9
         # The upstream gradient stays on the device (no host synchronisation):
-        # multiplied in float32, one rounding to the dtype; 1 writes nothing.
+        # multiplied in float32 by its ratio to the declared grad_scale, one
+        # rounding to the dtype; equal to it (1 by default) writes nothing.
         if d_hidden is not None:
-            d_hidden = scale_by_upstream(d_hidden, g_loss).view(ctx.hidden_shape)
+            d_hidden = scale_by_upstream(d_hidden, g_loss, ctx.grad_scale).view(ctx.hidden_shape)
         if d_weight is not None:
-            scale_by_upstream(d_weight, g_loss)
+            scale_by_upstream(d_weight, g_loss, ctx.grad_scale)
         return d_hidden, d_weight, None, None, None, None, None, None, None
 
 
@@ -152,7 +154,8 @@ def fused_linear_grpo_step(hidden: torch.Tensor, weight: torch.Tensor, targets: 
                            loss_type: str = "bnpo", importance_level: str = "token",
                            max_completion_length: int | None = None,
                            normalizer: float | None = None, temperature: float | None = None,
-                           chunk_tokens: int | None = None, return_stats: bool = False):
+                           chunk_tokens: int | None = None, return_stats: bool = False,
+                           grad_scale: float = 1.0):
     """GRPO loss of the LM head ``hidden @ weight^T`` over token chunks;
     differentiable in ``hidden`` and ``weight``.
 
@@ -169,6 +172,11 @@ def fused_linear_grpo_step(hidden: torch.Tensor, weight: torch.Tensor, targets: 
             Smaller chunks cost GEMM efficiency.  Default: the fewest equal
             chunks whose ``[chunk, V]`` buffers stay within 4 GiB
             (:data:`DEFAULT_CHUNK_BYTES`).
+        grad_scale: the upstream gradient the caller's backward will send
+            into the loss (``1 / k`` under ``k`` gradient-accumulation steps),
+            as :func:`kernel_opt.fused_grpo_step` takes it: the gradients are
+            computed already multiplied by it, and the backward writes
+            nothing when the upstream gradient equals it.
 
     Returns ``(loss, logp, entropy)`` (``+ stats`` with ``return_stats``);
     ``logp`` and ``entropy`` are float32 ``[B, S]`` constants.
@@ -189,6 +197,7 @@ def fused_linear_grpo_step(hidden: torch.Tensor, weight: torch.Tensor, targets: 
     T = 1.0 if temperature is None else float(temperature)
     if not (T > 0.0 and T != float("inf")):
         raise RuntimeError(f"temperature must be finite and > 0, got {T}")
+    gs = _check_grad_scale(grad_scale)
     V = weight.size(0)
     chunk = (default_chunk_tokens(B * S, V, hidden.element_size()) if chunk_tokens is None
              else int(chunk_tokens))
@@ -222,7 +231,7 @@ def fused_linear_grpo_step(hidden: torch.Tensor, weight: torch.Tensor, targets: 
     ref = f32(ref_logp, "ref_logp", (B, S)) if (beta != 0.0 and ref_logp is not None) else None
     wts = grpo_token_weights(m, loss_type, max_completion_length, normalizer)
     eh = eps_low if eps_high is None else eps_high
-    params = (T, float(eps_low), float(eh), float(beta))
+    params = (T, float(eps_low), float(eh), float(beta), gs)
     flat = lambda x: None if x is None else x.reshape(-1).contiguous()  # noqa: E731
     loss, logp, ent = _FusedLinearGrpoStep.apply(
         hidden, weight, targets.contiguous(), flat(old), flat(ref), flat(adv), flat(wts),

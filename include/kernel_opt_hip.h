@@ -321,11 +321,18 @@ int klp_grpo_bwd(const float* logp, const float* old_logp, const float* ref_logp
  *   tok_weight [n_rows]: the weight of each token's loss in the batch loss,
  *       mask / normaliser (e.g. mask / max(sum mask, 1) for
  *       KLP_GRPO_LOSS_BNPO).
+ *   grad_scale: the upstream gradient the caller will send into the batch
+ *       loss, declared in advance (finite, non-zero): 1 for loss.backward();
+ *       1 / k when a trainer divides the loss by k gradient-accumulation
+ *       steps.  It multiplies the gradient, not loss_tok.
  * Writes logprob, entropy and (unless NULL) lse [n_rows] as klp_fwd;
  * loss_tok [n_rows] = tok_weight * loss_tok (the batch loss is their sum);
  * and d_logits (dense [n_rows, vocab], logits dtype, 16-byte aligned) =
- * d (sum loss_tok) / d logits, exactly klp_bwd's formula with
- * g_logp = tok_weight * d loss_tok / d logp and g_ent = g_lse = 0.
+ * grad_scale * d (sum loss_tok) / d logits, exactly klp_bwd's formula with
+ * g_logp = tok_weight * d loss_tok / d logp * grad_scale (in that order, in
+ * fp32) and g_ent = g_lse = 0.  The backward then applies the actual
+ * upstream gradient with klp_rescale_inplace(d_logits, ..., grad_scale),
+ * which writes nothing when the two are equal.
  * Only rows of at most klp_grpo_step_max_vocab(dtype) elements whose start
  * and length are whole 16-byte vectors are supported (row starts 16-byte
  * aligned, vocab * element size a multiple of 16); anything else returns
@@ -350,7 +357,7 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                   const float* old_logp, const float* ref_logp, const float* advantages,
                   const float* tok_weight, int64_t seq_len,
                   float eps_low, float eps_high, float beta, int adv_per_token,
-                  float* logprob, float* entropy, float* lse, float* loss_tok,
+                  float grad_scale, float* logprob, float* entropy, float* lse, float* loss_tok,
                   void* d_logits, void* sched, void* stream);
 
 /*
@@ -389,6 +396,19 @@ int klp_grpo_token_weights(const void* mask, int mask_dtype, int64_t n_seqs, int
  * no host synchronisation.  data aligned to its element size, n >= 0.
  */
 int klp_scale_inplace(void* data, int dtype, int64_t n, const float* scale, void* stream);
+
+/*
+ * data[i] *= *scale / applied for i in [0, n), in place, on the stream, for
+ * a buffer that already holds its values multiplied by `applied` (the
+ * upstream gradient declared in advance, klp_grpo_step's grad_scale): when
+ * *scale == applied nothing is written; otherwise each element is
+ * multiplied in fp32 by fp32(*scale / applied) and rounded once to `dtype`
+ * (RNE).  klp_scale_inplace is this with applied = 1 (the factor is then
+ * *scale itself).  No counterpart in the reference.  applied finite and
+ * non-zero; the rest as klp_scale_inplace.
+ */
+int klp_rescale_inplace(void* data, int dtype, int64_t n, const float* scale, float applied,
+                        void* stream);
 
 /*
  * Fused LM head + per-token logprob / entropy, forward.  No counterpart in the

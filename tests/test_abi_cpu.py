@@ -310,13 +310,13 @@ def test_grpo_step_validation_errors():
 
     def step(**kw):
         a = dict(logits=A, dtype=0, n=8, v=4096, ri=8, so=0, si=4096, tg=A, temp=1.0, old=A,
-                 ref=None, adv=A, w=A, S=4, el=0.2, eh=0.28, beta=0.0, pt=0, lp=A, ent=A,
-                 lse=None, lt=A, d=A, sched=None)
+                 ref=None, adv=A, w=A, S=4, el=0.2, eh=0.28, beta=0.0, pt=0, gs=1.0, lp=A,
+                 ent=A, lse=None, lt=A, d=A, sched=None)
         a.update(kw)
         return lib.klp_grpo_step(a["logits"], a["dtype"], a["n"], a["v"], a["ri"], a["so"],
                                  a["si"], a["tg"], a["temp"], a["old"], a["ref"], a["adv"],
-                                 a["w"], a["S"], a["el"], a["eh"], a["beta"], a["pt"], a["lp"],
-                                 a["ent"], a["lse"], a["lt"], a["d"], a["sched"], None)
+                                 a["w"], a["S"], a["el"], a["eh"], a["beta"], a["pt"], a["gs"],
+                                 a["lp"], a["ent"], a["lse"], a["lt"], a["d"], a["sched"], None)
     assert step(n=0) == 0
     assert step(dtype=9) == KLP_EDTYPE
     assert step(temp=0.0) == KLP_EINVAL and "temperature" in _err()
@@ -335,6 +335,9 @@ def test_grpo_step_validation_errors():
     assert step(d=ctypes.c_void_p(0x100004)) == KLP_EINVAL and "d_logits" in _err()
     assert step(el=-1.0) == KLP_EINVAL and "eps_low" in _err()
     assert step(beta=float("inf")) == KLP_EINVAL and "beta" in _err()
+    for gs in (0.0, -0.0, float("inf"), float("-inf"), float("nan")):
+        assert step(gs=gs) == KLP_EINVAL and "grad_scale" in _err(), gs
+    assert step(n=0, gs=0.0) == 0  # no rows: nothing checked past the rows
     assert step(sched=ctypes.c_void_p(0x100004)) == KLP_EINVAL and "sched" in _err()
     lib.klp_debug_fail_next_launches(1)
     try:
@@ -441,6 +444,33 @@ def test_scale_inplace_validation_errors():
     lib.klp_debug_fail_next_launches(1)
     try:
         assert scale() == KLP_ELAUNCH and "scale" in _err()
+    finally:
+        lib.klp_debug_fail_next_launches(0)
+
+
+def test_rescale_inplace_validation_errors():
+    """klp_rescale_inplace checks `applied` (finite, non-zero), then the
+    buffer as klp_scale_inplace does; an injected launch failure is
+    reported."""
+    from kernel_opt._library import KLP_EDTYPE, KLP_EINVAL, KLP_ELAUNCH, lib
+    A = ctypes.c_void_p(0x100000)
+
+    def rescale(**kw):
+        a = dict(d=A, dtype=0, n=100, s=A, applied=0.125)
+        a.update(kw)
+        return lib.klp_rescale_inplace(a["d"], a["dtype"], a["n"], a["s"], a["applied"], None)
+    for bad in (0.0, -0.0, float("inf"), float("-inf"), float("nan")):
+        assert rescale(applied=bad) == KLP_EINVAL and "applied" in _err(), bad
+        assert rescale(applied=bad, n=0) == KLP_EINVAL and "applied" in _err(), bad
+    assert rescale(n=0) == 0
+    assert rescale(applied=-3.0, n=0, d=None, s=None) == 0
+    assert rescale(dtype=3) == KLP_EDTYPE
+    assert rescale(n=-1) == KLP_EINVAL and "n must" in _err()
+    assert rescale(d=ctypes.c_void_p(0x100001)) == KLP_EINVAL and "data" in _err()
+    assert rescale(s=None) == KLP_EINVAL and "scale" in _err()
+    lib.klp_debug_fail_next_launches(1)
+    try:
+        assert rescale() == KLP_ELAUNCH and "scale" in _err()
     finally:
         lib.klp_debug_fail_next_launches(0)
 

@@ -346,6 +346,40 @@ def test_compiled_grpo_step_nonpositive_normalizer(monkeypatch, normalizer, mask
         assert torch.isfinite(res[0][0].view(torch.float32)).all()
 
 
+@pytest.mark.parametrize("upstream", [0.25, 1.0, -3.0])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_compiled_grpo_step_grad_scale(monkeypatch, upstream, dtype):
+    """A declared grad_scale of 0.25: the binding's op and the Python
+    statement give the same bits for the loss, logp, entropy and d_logits,
+    whether the upstream gradient equals it (nothing written in the
+    backward) or not (the ratio applied)."""
+    from kernel_opt import fused_grpo_step, grpo_step
+    B, S, V = 3, 20, 8192
+    base = seeded_logits((B, S, V), dtype, seed=21).to(DEV)
+    t = seeded_targets((B, S), V, seed=22).to(DEV)
+    g = torch.Generator().manual_seed(23)
+    old = (-torch.rand(B, S, generator=g) * 3).to(DEV)
+    adv = torch.randn(B, generator=g).to(DEV)
+    mask = (torch.rand(B, S, generator=g) < 0.8).to(DEV)
+
+    def bits(x):
+        x = x.detach().contiguous()
+        return x.view({4: torch.int32, 2: torch.int16}[x.element_size()])
+
+    res = []
+    for python_path in (False, True):
+        if python_path:
+            monkeypatch.setattr(grpo_step, "binding", _StepPythonPathOnly)
+        leaf = base.clone().requires_grad_(True)
+        loss, lp, ent = fused_grpo_step(leaf, t, old, adv, mask, loss_type="grpo",
+                                        grad_scale=0.25)
+        (loss * upstream).backward()
+        res.append([bits(loss), bits(lp), bits(ent), bits(leaf.grad), loss.grad_fn.name()])
+    for a, b in zip(res[0][:4], res[1][:4]):
+        assert torch.equal(a, b)
+    assert "FusedGrpoStep" in res[0][4], res[0][4]
+
+
 def test_compiled_grpo_step_backward_once_and_fallback():
     from kernel_opt import fused_grpo_step
     x = seeded_logits((2, 5, 4096), torch.bfloat16, seed=3).to(DEV).requires_grad_(True)

@@ -66,13 +66,14 @@ def oracle_kw(loss_type, beta, B, L=None, normalizer=None):
     return dict(eps_low=0.2, eps_high=0.28, beta=beta, loss_type=kind, norm_const=norm)
 
 
-def run_step(x, t, old, adv, mask, ref, loss_type, beta, temperature=None, **extra):
+def run_step(x, t, old, adv, mask, ref, loss_type, beta, temperature=None, grad_scale=1.0,
+             **extra):
     """klp_grpo_step on the GPU; returns (logp, ent, lse, loss_tok, d) on the GPU."""
     from kernel_opt.grpo_step import grpo_step_launch, grpo_token_weights
     B, S, _ = x.shape
     w = grpo_token_weights(mask.to(DEV), loss_type, **extra).contiguous()
     params = (1.0 if temperature is None else temperature, 0.2, 0.28, beta,
-              int(adv.dim() != 1))
+              int(adv.dim() != 1), grad_scale)
     r = ref.to(DEV) if (beta != 0.0 and ref is not None) else None
     return grpo_step_launch(x.to(DEV), t.to(DEV), old.to(DEV), r, adv.to(DEV), w, params)
 
@@ -289,6 +290,61 @@ def test_scale_by_upstream(dtype):
             assert torch.equal(view.view(bits), exp.view(bits))
             assert torch.equal(buf[:off], base[:off])
             assert torch.equal(buf[off + n:], base[off + n:])
+    # A buffer already scaled by a declared upstream gradient (applied):
+    # g == applied writes nothing, any other g multiplies by fp32(g / applied).
+    for off, n in ((1, 7), (0, 4097), (5, (1 << 20) - 9)):
+        for applied, sc in ((0.125, 0.125), (0.125, 0.3), (0.125, 1.0), (-3.0, -3.0),
+                            (-3.0, 0.7), (1.0 / 3.0, 1.0)):
+            print(f"rescale: dtype={dtype} off={off} n={n} applied={applied} g={sc}", flush=True)
+            buf = base.clone()
+            view = buf[off:off + n]
+            scale_by_upstream(view, torch.tensor(sc, device=DEV), applied)
+            src = base[off:off + n]
+            factor = float(np.float32(np.float32(sc) / np.float32(applied)))
+            exp = src if np.float32(sc) == np.float32(applied) else (src.float() * factor).to(dtype)
+            assert torch.equal(view.view(bits), exp.view(bits))
+            assert torch.equal(buf[:off], base[:off])
+            assert torch.equal(buf[off + n:], base[off + n:])
+
+
+@pytest.mark.parametrize("c", [0.125, -2.0, 1.0 / 3.0])
+def test_grad_scale_folds_the_upstream_gradient(c):
+    """grad_scale c: klp_grpo_step writes d_logits already multiplied by c
+    (the loss terms unscaled); through fused_grpo_step, an upstream gradient
+    equal to c leaves the forward's d_logits as the gradient (nothing
+    written), and any other is applied as the ratio to c."""
+    ko = _ko()
+    B, S, V = 3, 40, 152064
+    print(f"grad_scale {c}", flush=True)
+    x, t, mask, adv = make_case(B, S, V, torch.bfloat16, 41)
+    old = torch.full((B, S), -8.0)
+    lp1, en1, _, lt1, d1 = run_step(x, t, old, adv, mask, None, "grpo", 0.0)
+    lpc, enc, _, ltc, dc = run_step(x, t, old, adv, mask, None, "grpo", 0.0, grad_scale=c)
+    assert torch.equal(lpc, lp1) and torch.equal(enc, en1) and torch.equal(ltc, lt1)
+    ref = (d1.float() * c).to(d1.dtype)
+    if c in (0.125, -2.0):  # a power of two: the same bits either way
+        assert torch.equal(dc, ref)
+    else:  # one rounding against two
+        assert int(ulp_diff(storage_bits(dc), storage_bits(ref), 16).max()) <= 1
+
+    xg = x.to(DEV).requires_grad_(True)
+    loss, _, _ = ko.fused_grpo_step(xg, t.to(DEV), old.to(DEV), adv.to(DEV), mask.to(DEV),
+                                    loss_type="grpo", grad_scale=c)
+    assert torch.equal(loss, lt1.sum())
+    (loss * c).backward()
+    assert torch.equal(xg.grad, dc)
+
+    xg2 = x.to(DEV).requires_grad_(True)
+    loss2, _, _ = ko.fused_grpo_step(xg2, t.to(DEV), old.to(DEV), adv.to(DEV), mask.to(DEV),
+                                     loss_type="grpo", grad_scale=c)
+    loss2.backward()
+    factor = float(np.float32(np.float32(1.0) / np.float32(c)))
+    assert torch.equal(xg2.grad, (dc.float() * factor).to(dc.dtype))
+
+    for bad in (0.0, float("inf"), float("nan"), 1e-60, 1e60):
+        with pytest.raises(ValueError, match="grad_scale"):
+            ko.fused_grpo_step(xg2, t.to(DEV), old.to(DEV), adv.to(DEV), mask.to(DEV),
+                               grad_scale=bad)
 
 
 @pytest.mark.parametrize("loss_type", ["grpo", "dr_grpo"])
@@ -456,8 +512,8 @@ def _step_abi(x, t, old, ref, adv, w, temperature, per_token, sched):
     st = torch.cuda.current_stream().cuda_stream
     check_status(lib.klp_grpo_step(P(x), DTYPE_CODES[x.dtype], N, V, *_C.row_layout(x), P(t),
                                    temperature, P(old), P(ref), P(adv), P(w), S, 0.2, 0.28,
-                                   0.04 if ref is not None else 0.0, per_token, *map(P, outs),
-                                   P(d), P(sched), st))
+                                   0.04 if ref is not None else 0.0, per_token, 1.0,
+                                   *map(P, outs), P(d), P(sched), st))
     return (*outs, d)
 
 

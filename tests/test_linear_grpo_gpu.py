@@ -90,7 +90,7 @@ def test_chunks_match_per_chunk_composition(chunk):
     h2 = h.view(N, D)
     wts = grpo_token_weights(mask, "grpo").reshape(-1).contiguous()
     adv_t = adv.unsqueeze(1).expand(B, S).reshape(-1).contiguous()
-    params = (1.0, 0.2, 0.28, 0.04, 1)
+    params = (1.0, 0.2, 0.28, 0.04, 1, 1.0)
     lps, ents, lts, dhs = [], [], [], []
     dw = None  # float32, accumulated inside the GEMM
     for n0 in range(0, N, chunk):
@@ -179,6 +179,16 @@ def test_frozen_weight_and_scaled_loss():
     assert torch.equal(hb.grad, (ha.grad.float() * 0.5).to(h.dtype))
     with pytest.raises(RuntimeError, match="only once"):
         la.backward()
+    # The same upstream gradient declared as grad_scale: applied in the
+    # forward (a power of two, so the same bits), nothing left for the
+    # backward to write.
+    hc = h.clone().requires_grad_(True)
+    wc = w.clone().requires_grad_(True)
+    lc, _, _ = ko.fused_linear_grpo_step(hc, wc, t, old, adv, mask, ref, chunk_tokens=33,
+                                         grad_scale=0.5, **KW)
+    (lc * 0.5).backward()
+    assert torch.equal(lc, lb)
+    assert torch.equal(hc.grad, hb.grad) and torch.equal(wc.grad, wb.grad)
 
 
 def test_qwen_head_shape_chunks():
