@@ -1304,13 +1304,26 @@ def core_timing(name, dev, K, warmup, timer, fcfg=None, bcfg=None, dtimer=None):
                 bwd_used=bwd_used, ceilings=out_ceil, device_timed=device, d_logits=d_logits)
 
 
+_TRACE_ROLES = (("fwd", "klp_fwd_kernel"), ("bwd", "klp_bwd_kernel"),
+                ("read", "klp_ceiling_read_kernel"), ("copy", "klp_ceiling_copy_kernel"))
+
+
 def trace_agreement(profiles, device_timed):
     """The committed kernel-trace summaries' figures for klp_fwd / klp_bwd
     (average us per phase), and this run's device-timed medians divided by
     the trace's medians of the same phase ("back to back" for warm,
     "flushed" for flushed): `bench_over_trace_median`.  The trace is another
-    run, usually on another box.  None without a summary of this build."""
+    run, usually on another box, whose clock moves both kernels and their
+    ceilings; `ratio_over_trace` compares what a box's clock cancels out of:
+    this run's forward / read and backward / copy over the same ratios in
+    the trace.  None without a summary of this build."""
     out = None
+    medians = {}
+    for prof in profiles:
+        for k, v in prof["kernels"].items():
+            for role, prefix in _TRACE_ROLES:
+                if k.startswith(prefix):
+                    medians.setdefault(role, []).append(v)
     for prof in profiles:
         for k, v in prof["kernels"].items():
             if not (k.startswith("klp_bwd_kernel") or k.startswith("klp_fwd_kernel")):
@@ -1325,6 +1338,19 @@ def trace_agreement(profiles, device_timed):
                     mode: round(dev_t[mode]["ms"] * 1e6 / v[ph]["median_ns"], 4)
                     for mode, ph in (("warm", "back to back"), ("flushed", "flushed"))
                     if ph in v and v[ph].get("median_ns")}
+    if out is not None and device_timed:
+        for name, num, den in (("fwd_over_read", "fwd", "read"), ("bwd_over_copy", "bwd", "copy")):
+            tn, td = medians.get(num, []), medians.get(den, [])
+            bn, bd = device_timed.get(num), device_timed.get(den)
+            if len(tn) != 1 or len(td) != 1 or not bn or not bd:
+                continue  # missing, or several launch shapes of one kernel
+            r = {}
+            for mode, ph in (("warm", "back to back"), ("flushed", "flushed")):
+                a, b = tn[0].get(ph, {}).get("median_ns"), td[0].get(ph, {}).get("median_ns")
+                if a and b and bd[mode]["ms"]:
+                    r[mode] = round((bn[mode]["ms"] / bd[mode]["ms"]) / (a / b), 4)
+            if r:
+                out.setdefault("ratio_over_trace", {})[name] = r
     return out
 
 

@@ -224,6 +224,37 @@ def test_trace_agreement_divides_device_medians_by_the_trace():
     assert bench.trace_agreement([], dev) is None
     no_dev = bench.trace_agreement([prof], None)
     assert "bench_over_trace_median" not in no_dev
+    assert "ratio_over_trace" not in tc  # no read ceiling in the device figures
+
+
+def test_trace_agreement_compares_ratios_to_the_ceilings():
+    """ratio_over_trace: (bench fwd / read) / (trace fwd / read), likewise
+    bwd / copy, per phase; a kernel with two launch shapes in the trace gives
+    no ratio."""
+    prof = {"file": "profiles/x.md", "kernels": {
+        "klp_fwd_kernel<0, 8, 2, false, false>": {
+            "back to back": {"avg_ns": 1.0, "median_ns": 48000.0},
+            "flushed": {"avg_ns": 1.0, "median_ns": 48400.0}},
+        "klp_ceiling_read_kernel<8, 2>": {
+            "back to back": {"avg_ns": 1.0, "median_ns": 45000.0},
+            "flushed": {"avg_ns": 1.0, "median_ns": 45500.0}},
+        "klp_bwd_kernel<0, 4, 2, true, false>": {
+            "flushed": {"avg_ns": 1.0, "median_ns": 98000.0}},
+        "klp_ceiling_copy_kernel<4, 2>": {
+            "flushed": {"avg_ns": 1.0, "median_ns": 104000.0}}}}
+    dev = {"fwd": {"warm": {"ms": 0.0490}, "flushed": {"ms": 0.0495}},
+           "read": {"warm": {"ms": 0.0450}, "flushed": {"ms": 0.0460}},
+           "bwd": {"warm": {"ms": 0.0990}, "flushed": {"ms": 0.0985}},
+           "copy": {"warm": {"ms": 0.1040}, "flushed": {"ms": 0.1050}}}
+    r = bench.trace_agreement([prof], dev)["ratio_over_trace"]
+    assert r["fwd_over_read"] == {
+        "warm": round((0.0490 / 0.0450) / (48000 / 45000), 4),
+        "flushed": round((0.0495 / 0.0460) / (48400 / 45500), 4)}
+    assert r["bwd_over_copy"] == {"flushed": round((0.0985 / 0.1050) / (98000 / 104000), 4)}
+    prof["kernels"]["klp_fwd_kernel<0, 16, 4, false, false>"] = \
+        prof["kernels"]["klp_fwd_kernel<0, 8, 2, false, false>"]
+    r2 = bench.trace_agreement([prof], dev)["ratio_over_trace"]
+    assert "fwd_over_read" not in r2 and "bwd_over_copy" in r2
 
 
 def test_configs_table_ranges_over_runs(tmp_path):
