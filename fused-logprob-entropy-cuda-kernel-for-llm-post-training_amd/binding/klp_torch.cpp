@@ -732,13 +732,21 @@ std::optional<std::vector<at::Tensor>> fused_grpo_step(
     if ((!has_mask || mask_code >= 0) && scale_ok) {
         const at::Tensor mc = has_mask ? m.contiguous() : at::Tensor();
         weight = at::empty({B, S}, at::TensorOptions().dtype(at::kFloat).device(dev));
+        // "bnpo" keeps per-workgroup partial sums between its two launches;
+        // the caching allocator hands back the block in stream order.
+        const at::Tensor ws =
+            weight_kind == KLP_GRPO_LOSS_BNPO
+                ? at::empty({KLP_GRPO_TOKEN_WEIGHTS_WORKSPACE_BYTES},
+                            at::TensorOptions().dtype(at::kByte).device(dev))
+                : at::Tensor();
         const c10::hip::HIPGuard guard(static_cast<c10::DeviceIndex>(dev.index()));
         hipStream_t stream =
             c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(dev.index())).stream();
         check_status(klp_grpo_token_weights(has_mask ? mc.data_ptr() : nullptr,
                                             has_mask ? mask_code : KLP_MASK_U8, B, S,
                                             static_cast<int>(weight_kind), fixed_scale,
-                                            weight.data_ptr<float>(), stream));
+                                            weight.data_ptr<float>(),
+                                            ws.defined() ? ws.data_ptr() : nullptr, stream));
     } else {
         const at::Tensor mf =
             has_mask ? m : at::ones({B, S}, at::TensorOptions().dtype(at::kFloat).device(dev));

@@ -912,7 +912,8 @@ int klp_rescale_inplace(void* data, int dtype, int64_t n, const float* scale, fl
 }
 
 int klp_grpo_token_weights(const void* mask, int mask_dtype, int64_t n_seqs, int64_t seq_len,
-                           int loss_type, float scale, float* weights, void* stream) {
+                           int loss_type, float scale, float* weights, void* workspace,
+                           void* stream) {
     if (n_seqs < 0 || seq_len < 0) return fail(KLP_EINVAL, "n_seqs and seq_len must be >= 0");
     if (loss_type != KLP_GRPO_LOSS_GRPO && loss_type != KLP_GRPO_LOSS_BNPO &&
         loss_type != KLP_GRPO_LOSS_FIXED)
@@ -932,6 +933,10 @@ int klp_grpo_token_weights(const void* mask, int mask_dtype, int64_t n_seqs, int
     if (loss_type == KLP_GRPO_LOSS_FIXED && !(scale > 0.0f && scale < INFINITY))
         return fail(KLP_EINVAL, "scale (1 / normaliser) must be finite and > 0, got %g",
                     static_cast<double>(scale));
+    if (loss_type == KLP_GRPO_LOSS_BNPO && (workspace == nullptr || !aligned(workspace, 8)))
+        return fail(KLP_EINVAL,
+                    "KLP_GRPO_LOSS_BNPO needs a workspace of KLP_GRPO_TOKEN_WEIGHTS_WORKSPACE_BYTES, "
+                    "8-byte aligned");
     klp::TokenWeightsParams p;
     p.mask = mask;
     p.mask_dtype = mask_dtype;
@@ -940,10 +945,15 @@ int klp_grpo_token_weights(const void* mask, int mask_dtype, int64_t n_seqs, int
     p.S = seq_len;
     p.scale = scale;
     p.weights = weights;
+    p.partial = static_cast<int64_t*>(workspace);
     if (injected_failure("grpo_token_weights")) return KLP_ELAUNCH;
     return after_launch(klp::launch_grpo_token_weights(p, static_cast<hipStream_t>(stream)),
                         "grpo_token_weights");
 }
+
+static_assert(KLP_GRPO_TOKEN_WEIGHTS_WORKSPACE_BYTES ==
+                  klp::kGrpoWeightsMaxBlocks * sizeof(int64_t),
+              "the token weights' workspace holds one partial sum per workgroup");
 
 int64_t klp_grpo_step_max_vocab(int dtype) {
     if (dtype != KLP_BF16 && dtype != KLP_FP16 && dtype != KLP_FP32) return 0;

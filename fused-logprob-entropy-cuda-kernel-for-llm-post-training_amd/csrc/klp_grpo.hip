@@ -211,8 +211,11 @@ __global__ __launch_bounds__(kGrpoThreads) void klp_grpo_bwd_kernel(GrpoParams p
 
 namespace {
 
-constexpr int kWeightThreads = 1024;
+constexpr int kWeightThreads = 256;
 constexpr int kWeightWaves = kWeightThreads / 64;
+// Elements a thread handles per step of the grid-wide loops (their loads are
+// issued together).
+constexpr int kWeightUnroll = 4;
 
 // Mask element i as an integer: M is the mask's element type, void for no
 // mask (all ones).
@@ -237,88 +240,170 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
     return v;
 }
 
+// Sum over the workgroup, returned to every thread.  `part` is reused by the
+// caller's next call only after that call's first barrier, which every
+// thread reaches after reading this call's result.
+__device__ __forceinline__ int64_t block_sum_i64(int64_t v, int64_t* part) {
+    const uint32_t tid = threadIdx.x;
+    v = wave_sum_i64(v);
+    __syncthreads();  // the previous call's readers are done with `part`
+    if ((tid & 63u) == 0) part[tid >> 6] = v;
+    __syncthreads();
+    int64_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWeightWaves; ++w) tot += part[w];
+    return tot;
+}
+
+// Sum of mask[i] over the indices i = first + k * stride < n.
+template <typename M>
+__device__ __forceinline__ int64_t strided_mask_sum(const void* mask, int64_t first, int64_t stride,
+                                                    int64_t n) {
+    int64_t v = 0;
+    int64_t i = first;
+    for (; i + (kWeightUnroll - 1) * stride < n; i += kWeightUnroll * stride) {
+        int64_t m[kWeightUnroll];
+#pragma unroll
+        for (int k = 0; k < kWeightUnroll; ++k) m[k] = mask_value<M>(mask, i + k * stride);
+#pragma unroll
+        for (int k = 0; k < kWeightUnroll; ++k) v += m[k];
+    }
+    for (; i < n; i += stride) v += mask_value<M>(mask, i);
+    return v;
+}
+
+// weights[i] = mask[i] * r over the indices i = first + k * stride < n.
+template <typename M>
+__device__ __forceinline__ void strided_weights(const void* mask, float* weights, float r,
+                                                int64_t first, int64_t stride, int64_t n) {
+    int64_t i = first;
+    for (; i + (kWeightUnroll - 1) * stride < n; i += kWeightUnroll * stride) {
+        int64_t m[kWeightUnroll];
+#pragma unroll
+        for (int k = 0; k < kWeightUnroll; ++k) m[k] = mask_value<M>(mask, i + k * stride);
+#pragma unroll
+        for (int k = 0; k < kWeightUnroll; ++k)
+            weights[i + k * stride] = static_cast<float>(m[k]) * r;
+    }
+    for (; i < n; i += stride) weights[i] = static_cast<float>(mask_value<M>(mask, i)) * r;
+}
+
 }  // namespace
 
-// The GRPO step's token weights w = m / normaliser in one workgroup:
-//   Kind 0 ("grpo"): m * (1 / (max(row sum of m, 1) * B)), row by row,
-//   Kind 1 ("bnpo"): m * (1 / max(sum of m, 1)),
-//   Kind 2 (fixed):  m * scale.
-// The mask's sums are taken exactly in 64-bit integers and rounded once to
-// float32, then the same float32 operations as the eager statement
+// The GRPO step's token weights w = m / normaliser:
+//   "grpo":  m * (1 / (max(row sum of m, 1) * B)), one workgroup per row
+//            (klp_grpo_weights_rows_kernel);
+//   "bnpo":  m * (1 / max(sum of m, 1)): per-workgroup partial sums into the
+//            caller's workspace (klp_grpo_weights_partial_kernel), then every
+//            workgroup adds the partials and writes its share
+//            (klp_grpo_weights_kernel<.., kFromPartials>); a grid of one
+//            workgroup sums and writes in one launch (kOwnSum);
+//   fixed:   m * scale (klp_grpo_weights_kernel<.., kScaleGiven>).
+// The mask's sums are taken exactly in 64-bit integers (so every workgroup of
+// the "bnpo" pass gets the same total, in any order) and rounded once to
+// float32; then the same float32 operations as the eager statement
 // (grpo_step.grpo_token_weights) follow: the weights are its bits whenever
 // those sums are below 2^24, as the sums of any 0 / 1 mask of fewer than
 // 2^24 tokens are (the eager float32 sums of integers are exact there, in
-// any order).  One wave per row for kind 0; a fixed-order block sum for
-// kind 1.  One instance per (kind, mask element type): each is a single
-// straight loop nest, and every 64-bit index starts from the zero-extended
-// thread id.
-template <int Kind, typename M>
-__global__ __launch_bounds__(kWeightThreads) void klp_grpo_token_weights_kernel(
+// any order).  One instance per mask element type; every 64-bit index starts
+// from the zero-extended thread and workgroup ids.
+template <typename M>
+__global__ __launch_bounds__(kWeightThreads) void klp_grpo_weights_rows_kernel(
     TokenWeightsParams p) {
-    const uint32_t tid = threadIdx.x;
-    const int64_t lane = static_cast<int64_t>(tid & 63u);
-    const int64_t wave = static_cast<int64_t>(tid >> 6);
-    if constexpr (Kind == 0) {
-        for (int64_t b = wave; b < p.B; b += kWeightWaves) {
-            const int64_t base = b * p.S;
-            int64_t v = 0;
-            for (int64_t s = lane; s < p.S; s += 64) v += mask_value<M>(p.mask, base + s);
-            v = wave_sum_i64(v);
-            const float den = fmaxf(static_cast<float>(v), 1.0f) * static_cast<float>(p.B);
-            const float r = 1.0f / den;
-            for (int64_t s = lane; s < p.S; s += 64)
-                p.weights[base + s] = static_cast<float>(mask_value<M>(p.mask, base + s)) * r;
-        }
-    } else {
-        const int64_t n = p.B * p.S;
-        const int64_t first = static_cast<int64_t>(tid);
-        float r = p.scale;
-        if constexpr (Kind == 1) {
-            __shared__ int64_t part[kWeightWaves];
-            int64_t v = 0;
-            for (int64_t i = first; i < n; i += kWeightThreads) v += mask_value<M>(p.mask, i);
-            v = wave_sum_i64(v);
-            if (lane == 0) part[wave] = v;
-            __syncthreads();
-            int64_t tot = 0;
-#pragma unroll
-            for (int w = 0; w < kWeightWaves; ++w) tot += part[w];
-            r = 1.0f / fmaxf(static_cast<float>(tot), 1.0f);
-        }
-        for (int64_t i = first; i < n; i += kWeightThreads)
-            p.weights[i] = static_cast<float>(mask_value<M>(p.mask, i)) * r;
+    __shared__ int64_t part[kWeightWaves];
+    const int64_t tid = static_cast<int64_t>(threadIdx.x);
+    for (int64_t b = static_cast<int64_t>(blockIdx.x); b < p.B; b += gridDim.x) {
+        const int64_t base = b * p.S;
+        const void* row_mask = p.mask == nullptr
+                                   ? nullptr
+                                   : static_cast<const char*>(p.mask) + base * sizeof(
+                                         std::conditional_t<std::is_void_v<M>, char, M>);
+        const int64_t v = block_sum_i64(
+            strided_mask_sum<M>(row_mask, tid, kWeightThreads, p.S), part);
+        const float den = fmaxf(static_cast<float>(v), 1.0f) * static_cast<float>(p.B);
+        const float r = 1.0f / den;
+        strided_weights<M>(row_mask, p.weights + base, r, tid, kWeightThreads, p.S);
     }
+}
+
+template <typename M>
+__global__ __launch_bounds__(kWeightThreads) void klp_grpo_weights_partial_kernel(
+    TokenWeightsParams p) {
+    __shared__ int64_t part[kWeightWaves];
+    const int64_t n = p.B * p.S;
+    const int64_t first =
+        static_cast<int64_t>(blockIdx.x) * kWeightThreads + static_cast<int64_t>(threadIdx.x);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kWeightThreads;
+    const int64_t v = block_sum_i64(strided_mask_sum<M>(p.mask, first, stride, n), part);
+    if (threadIdx.x == 0) p.partial[blockIdx.x] = v;
+}
+
+// How klp_grpo_weights_kernel gets its factor: the fixed scale; 1 / the
+// total of the partial sums a previous launch left (one per workgroup of the
+// same grid); or 1 / the mask's total summed by the one workgroup itself.
+enum WeightsTotal { kScaleGiven = 0, kFromPartials = 1, kOwnSum = 2 };
+
+template <typename M, int kTotal>
+__global__ __launch_bounds__(kWeightThreads) void klp_grpo_weights_kernel(TokenWeightsParams p) {
+    const int64_t n = p.B * p.S;
+    const int64_t first =
+        static_cast<int64_t>(blockIdx.x) * kWeightThreads + static_cast<int64_t>(threadIdx.x);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kWeightThreads;
+    float r = p.scale;
+    if constexpr (kTotal != kScaleGiven) {
+        __shared__ int64_t part[kWeightWaves];
+        int64_t v = 0;
+        if constexpr (kTotal == kFromPartials) {
+            for (uint32_t j = threadIdx.x; j < gridDim.x; j += kWeightThreads) v += p.partial[j];
+        } else {
+            v = strided_mask_sum<M>(p.mask, first, stride, n);  // gridDim.x == 1
+        }
+        r = 1.0f / fmaxf(static_cast<float>(block_sum_i64(v, part)), 1.0f);
+    }
+    strided_weights<M>(p.mask, p.weights, r, first, stride, n);
 }
 
 namespace {
 
-template <int Kind>
-hipError_t launch_token_weights_kind(const TokenWeightsParams& p, hipStream_t stream) {
-    const dim3 grid(1), block(kWeightThreads);
-    if (p.mask == nullptr)
-        return launch_kernel(klp_grpo_token_weights_kernel<Kind, void>, grid, block, stream, p);
-    switch (p.mask_dtype) {
-        case KLP_MASK_U8:
-            return launch_kernel(klp_grpo_token_weights_kernel<Kind, uint8_t>, grid, block,
-                                 stream, p);
-        case KLP_MASK_I32:
-            return launch_kernel(klp_grpo_token_weights_kernel<Kind, int32_t>, grid, block,
-                                 stream, p);
-        case KLP_MASK_I64:
-            return launch_kernel(klp_grpo_token_weights_kernel<Kind, int64_t>, grid, block,
-                                 stream, p);
-        default:
-            return hipErrorInvalidValue;
+// Workgroups of the grid-wide passes: one step of kWeightUnroll elements
+// per thread (its loads in flight together), at most kGrpoWeightsMaxBlocks;
+// larger inputs loop.
+unsigned weights_blocks(int64_t n) {
+    const int64_t per_block = int64_t{kWeightThreads} * kWeightUnroll;
+    int64_t g = (n + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > kGrpoWeightsMaxBlocks) g = kGrpoWeightsMaxBlocks;
+    return static_cast<unsigned>(g);
+}
+
+template <typename M>
+hipError_t launch_token_weights_mask(const TokenWeightsParams& p, hipStream_t stream) {
+    const dim3 block(kWeightThreads);
+    if (p.kind == 0) {
+        const unsigned rows = static_cast<unsigned>(p.B < 65535 ? p.B : 65535);
+        return launch_kernel(klp_grpo_weights_rows_kernel<M>, dim3(rows), block, stream, p);
     }
+    const dim3 grid(weights_blocks(p.B * p.S));
+    if (p.kind == 1) {
+        if (grid.x == 1)  // one workgroup: it sums the mask itself, one launch
+            return launch_kernel(klp_grpo_weights_kernel<M, kOwnSum>, grid, block, stream, p);
+        const hipError_t e =
+            launch_kernel(klp_grpo_weights_partial_kernel<M>, grid, block, stream, p);
+        if (e != hipSuccess) return e;
+        return launch_kernel(klp_grpo_weights_kernel<M, kFromPartials>, grid, block, stream, p);
+    }
+    return launch_kernel(klp_grpo_weights_kernel<M, kScaleGiven>, grid, block, stream, p);
 }
 
 }  // namespace
 
 hipError_t launch_grpo_token_weights(const TokenWeightsParams& p, hipStream_t stream) {
-    switch (p.kind) {
-        case 0: return launch_token_weights_kind<0>(p, stream);
-        case 1: return launch_token_weights_kind<1>(p, stream);
-        case 2: return launch_token_weights_kind<2>(p, stream);
+    if (p.kind < 0 || p.kind > 2) return hipErrorInvalidValue;
+    if (p.mask == nullptr) return launch_token_weights_mask<void>(p, stream);
+    switch (p.mask_dtype) {
+        case KLP_MASK_U8: return launch_token_weights_mask<uint8_t>(p, stream);
+        case KLP_MASK_I32: return launch_token_weights_mask<int32_t>(p, stream);
+        case KLP_MASK_I64: return launch_token_weights_mask<int64_t>(p, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -141,7 +141,11 @@ struct TokenWeightsParams {
     int64_t S;
     float scale;       // kind 2: the normaliser's float32 reciprocal
     float* weights;    // [B, S]
+    int64_t* partial;  // kind 1: one mask sum per workgroup (kGrpoWeightsMaxBlocks)
 };
+// Workgroups of the token-weights kernels' grid-wide passes at most; kind 1
+// keeps one 64-bit partial sum per workgroup in the caller's workspace.
+constexpr int kGrpoWeightsMaxBlocks = 1024;
 
 // Row counter of the persistent GRPO step kernel (klp_grpo_step's `sched`):
 // zero before a launch, and left zero by it.

@@ -41,6 +41,8 @@ KLP_GRPO_TOKEN, KLP_GRPO_SEQUENCE = 0, 1
 KLP_FWD_NOALLOC_SCRATCH_BYTES = 65536
 # klp_grpo_step's row counter (KLP_GRPO_STEP_SCHED_BYTES).
 KLP_GRPO_STEP_SCHED_BYTES = 16
+# klp_grpo_token_weights' workspace ("bnpo": per-workgroup partial sums).
+KLP_GRPO_TOKEN_WEIGHTS_WORKSPACE_BYTES = 8192
 
 # Every symbol the public headers declare, with its ctypes signature.
 _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
@@ -74,7 +76,8 @@ SIGNATURES = {
     "klp_grpo_step_max_vocab": (_i64, [_i32]),
     "klp_scale_inplace": (_i32, [_vp, _i32, _i64, _vp, _vp]),
     "klp_rescale_inplace": (_i32, [_vp, _i32, _i64, _vp, ctypes.c_float, _vp]),
-    "klp_grpo_token_weights": (_i32, [_vp, _i32, _i64, _i64, _i32, ctypes.c_float, _vp, _vp]),
+    "klp_grpo_token_weights": (_i32, [_vp, _i32, _i64, _i64, _i32, ctypes.c_float, _vp, _vp,
+                                      _vp]),
     "klp_grpo_step": (_i32, _ROWS + [_vp, ctypes.c_float] + [_vp] * 4 + [_i64]
                       + [ctypes.c_float] * 3 + [_i32, ctypes.c_float] + [_vp] * 7),
     # include/kernel_opt_hip_tuning.h

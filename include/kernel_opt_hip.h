@@ -375,6 +375,12 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
  * integer sums rounded once to float32, so the weights equal the float32
  * eager computation's bits whenever those sums are below 2^24 (any 0 / 1
  * mask of fewer than 2^24 tokens).  Floating-point masks are not taken.
+ * workspace: KLP_GRPO_TOKEN_WEIGHTS_WORKSPACE_BYTES of device memory, 8-byte
+ * aligned, for KLP_GRPO_LOSS_BNPO (per-workgroup partial sums of the mask;
+ * its contents on entry do not matter); NULL is accepted for the other loss
+ * types.  Calls that share one must be ordered (one stream).  The work is
+ * spread over the device: one workgroup per row for KLP_GRPO_LOSS_GRPO, a
+ * grid-wide pass (two for KLP_GRPO_LOSS_BNPO) otherwise.
  */
 enum klp_mask_dtype {
     KLP_MASK_U8 = 0,
@@ -382,8 +388,11 @@ enum klp_mask_dtype {
     KLP_MASK_I64 = 2
 };
 
+#define KLP_GRPO_TOKEN_WEIGHTS_WORKSPACE_BYTES 8192
+
 int klp_grpo_token_weights(const void* mask, int mask_dtype, int64_t n_seqs, int64_t seq_len,
-                           int loss_type, float scale, float* weights, void* stream);
+                           int loss_type, float scale, float* weights, void* workspace,
+                           void* stream);
 
 /*
  * data[i] *= *scale for i in [0, n), in place, on the stream: each element is

@@ -475,6 +475,20 @@ def test_rescale_inplace_validation_errors():
         lib.klp_debug_fail_next_launches(0)
 
 
+def test_header_constants_match_the_python_names():
+    """Every #define KLP_<NAME> <int> of include/*.h that kernel_opt._library
+    names has the same value there."""
+    from kernel_opt import _library
+    found = 0
+    for name in ("kernel_opt_hip.h", "kernel_opt_hip_tuning.h"):
+        with open(os.path.join(ROOT, "include", name)) as f:
+            for k, v in re.findall(r"^#define (KLP_[A-Z0-9_]+) (\d+)\s*$", f.read(), re.M):
+                if hasattr(_library, k):
+                    assert getattr(_library, k) == int(v), k
+                    found += 1
+    assert found >= 2
+
+
 def test_grpo_token_weights_validation_errors():
     """klp_grpo_token_weights rejects bad arguments before any launch; an
     empty batch is a no-op; an injected launch failure is reported."""
@@ -482,10 +496,10 @@ def test_grpo_token_weights_validation_errors():
     A = ctypes.c_void_p(0x100000)
 
     def tw(**kw):
-        a = dict(m=A, md=1, B=4, S=8, kind=0, scale=1.0, w=A)
+        a = dict(m=A, md=1, B=4, S=8, kind=0, scale=1.0, w=A, ws=None)
         a.update(kw)
         return lib.klp_grpo_token_weights(a["m"], a["md"], a["B"], a["S"], a["kind"],
-                                          a["scale"], a["w"], None)
+                                          a["scale"], a["w"], a["ws"], None)
     assert tw(B=0) == 0 and tw(S=0, m=None, w=None) == 0
     assert tw(B=-1) == KLP_EINVAL and "n_seqs" in _err()
     assert tw(kind=3) == KLP_EINVAL and "loss_type" in _err()
@@ -497,6 +511,9 @@ def test_grpo_token_weights_validation_errors():
     assert tw(kind=2, scale=0.0) == KLP_EINVAL and "scale" in _err()
     assert tw(kind=2, scale=float("inf")) == KLP_EINVAL and "scale" in _err()
     assert tw(B=1 << 62, S=8) == KLP_EINVAL and "overflows" in _err()
+    assert tw(kind=1) == KLP_EINVAL and "workspace" in _err()  # "bnpo" needs one
+    assert tw(kind=1, ws=ctypes.c_void_p(0x100004)) == KLP_EINVAL and "workspace" in _err()
+    assert tw(kind=1, B=0) == 0
     lib.klp_debug_fail_next_launches(1)
     try:
         assert tw(md=0, m=ctypes.c_void_p(0x100001)) == KLP_ELAUNCH and "token_weights" in _err()

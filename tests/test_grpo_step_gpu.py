@@ -589,15 +589,18 @@ def test_persistent_rows_only_where_they_pay():
         assert lib.klp_grpo_step_persistent_min_rows(KLP_BF16, 155656, scaled) == 0
 
 
-@pytest.mark.parametrize("B,S", [(1, 1), (3, 1000), (4, 256), (16, 2048), (2, 70001)])
+@pytest.mark.parametrize("B,S", [(1, 1), (3, 1000), (4, 256), (16, 2048), (2, 70001),
+                                 (64, 8192), (300, 4001), (70001, 3)])
 @pytest.mark.parametrize("mask_kind", ["bool", "uint8", "int32", "int64", "none"])
 def test_token_weights_kernel_matches_eager(B, S, mask_kind):
-    """klp_grpo_token_weights (one launch) writes the bits of the eager
-    statement grpo_step.grpo_token_weights for every loss type: bool / uint8
-    / int32 / int64 0 / 1 masks (one all-zero row, whose normaliser clamps
-    to 1) and no mask."""
+    """klp_grpo_token_weights writes the bits of the eager statement
+    grpo_step.grpo_token_weights for every loss type: bool / uint8 / int32 /
+    int64 0 / 1 masks (one all-zero row, whose normaliser clamps to 1) and no
+    mask.  The shapes cover one and many workgroups, grid-wide passes that
+    loop (1.2 M tokens over 1024 workgroups) and more rows than the per-row
+    grid's 65 535 workgroups; the workspace starts with garbage."""
     import ctypes
-    from kernel_opt._library import check_status, lib
+    from kernel_opt._library import KLP_GRPO_TOKEN_WEIGHTS_WORKSPACE_BYTES, check_status, lib
     from kernel_opt.grpo_step import grpo_token_weights
     print(f"token weights B={B} S={S} mask={mask_kind}", flush=True)
     g = torch.Generator().manual_seed(B * 7919 + S)
@@ -617,9 +620,11 @@ def test_token_weights_kernel_matches_eager(B, S, mask_kind):
             den = float(B * S) if loss_type == "dr_grpo" else kw["normalizer"]
             scale = float(np.float32(1.0) / np.float32(den))
         w = torch.full((B, S), -1.0, device=DEV)
+        ws = torch.full((KLP_GRPO_TOKEN_WEIGHTS_WORKSPACE_BYTES // 8,), -7, dtype=torch.int64,
+                        device=DEV)
         check_status(lib.klp_grpo_token_weights(
             mask.data_ptr() if mask is not None else None, codes.get(mask_kind, 0), B, S, kind,
-            ctypes.c_float(scale), w.data_ptr(), st))
+            ctypes.c_float(scale), w.data_ptr(), ws.data_ptr(), st))
         torch.cuda.synchronize()
         assert torch.equal(w.view(torch.int32), eager.float().contiguous().view(torch.int32)), \
             f"{loss_type}: max |diff| {float((w - eager).abs().max()):.3g}"
