@@ -228,6 +228,16 @@ __device__ __forceinline__ int64_t mask_value(const void* mask, int64_t i) {
     }
 }
 
+// The mask from element `offset` on (no mask stays none).
+template <typename M>
+__device__ __forceinline__ const void* mask_from(const void* mask, int64_t offset) {
+    if constexpr (std::is_void_v<M>) {
+        return nullptr;
+    } else {
+        return static_cast<const M*>(mask) + offset;
+    }
+}
+
 // 64-bit integer sum over a wave (xor tree on the two 32-bit halves).
 __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
 #pragma unroll
@@ -314,10 +324,7 @@ __global__ __launch_bounds__(kWeightThreads) void klp_grpo_weights_rows_kernel(
     const int64_t tid = static_cast<int64_t>(threadIdx.x);
     for (int64_t b = static_cast<int64_t>(blockIdx.x); b < p.B; b += gridDim.x) {
         const int64_t base = b * p.S;
-        const void* row_mask = p.mask == nullptr
-                                   ? nullptr
-                                   : static_cast<const char*>(p.mask) + base * sizeof(
-                                         std::conditional_t<std::is_void_v<M>, char, M>);
+        const void* row_mask = mask_from<M>(p.mask, base);
         const int64_t v = block_sum_i64(
             strided_mask_sum<M>(row_mask, tid, kWeightThreads, p.S), part);
         const float den = fmaxf(static_cast<float>(v), 1.0f) * static_cast<float>(p.B);
