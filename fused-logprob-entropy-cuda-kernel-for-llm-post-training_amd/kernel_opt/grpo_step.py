@@ -41,8 +41,9 @@ import numpy as np
 import torch
 
 from . import _C
-from ._library import (DTYPE_CODES, KLP_GRPO_STEP_SCHED_BYTES, binding, capturing,
-                       check_status, device_guard, keep_for_capture, lib, ptr, stream_handle)
+from ._library import (DTYPE_CODES, KLP_GRPO_LOSS_BNPO, KLP_GRPO_STEP_SCHED_BYTES,
+                       KLP_GRPO_TOKEN_WEIGHTS_WORKSPACE_BYTES, binding, capturing, check_status,
+                       device_guard, keep_for_capture, lib, ptr, stream_handle)
 from .grpo import fused_grpo_loss
 from .ops import fused_logprob_entropy
 
@@ -281,6 +282,34 @@ def fused_grpo_step(logits: torch.Tensor, targets: torch.Tensor, old_logp: torch
     return (loss, logp, ent, stats) if return_stats else (loss, logp, ent)
 
 
+# Mask dtypes klp_grpo_token_weights reads (KLP_MASK_U8 / _I32 / _I64).
+_MASK_CODES = {torch.bool: 0, torch.uint8: 0, torch.int32: 1, torch.int64: 2}
+
+
+def _device_token_weights(mask, B, S, dev, kind, scale):
+    """grpo_token_weights' bits by klp_grpo_token_weights (a bool / integer
+    mask, or none), or None where the eager statement has to run: a floating
+    mask, or a fixed normaliser whose float32 reciprocal is not finite and
+    > 0.  Under graph capture the workspace is the captured call's own."""
+    if mask is not None and (mask.dtype not in _MASK_CODES or mask.device != dev
+                             or tuple(mask.shape) != (B, S)):
+        return None
+    if kind == 2 and not (0.0 < float(np.float32(scale)) < float("inf")):
+        return None
+    m = None if mask is None else mask.detach().contiguous()
+    weight = torch.empty((B, S), dtype=torch.float32, device=dev)
+    ws = None
+    if kind == KLP_GRPO_LOSS_BNPO:
+        ws = torch.empty(KLP_GRPO_TOKEN_WEIGHTS_WORKSPACE_BYTES, dtype=torch.uint8, device=dev)
+        if capturing():
+            ws = keep_for_capture(ws)
+    with device_guard(dev.index):
+        check_status(lib.klp_grpo_token_weights(
+            ptr(m), 0 if m is None else _MASK_CODES[m.dtype], B, S, kind, float(scale),
+            ptr(weight), ptr(ws), stream_handle(dev.index)))
+    return weight
+
+
 def _check_grad_scale(grad_scale) -> float:
     """``grad_scale`` as a float, finite and non-zero in float32 (the
     kernels take it as float32)."""
@@ -328,9 +357,12 @@ def _fused_python(logits, targets, old_logp, advantages, mask, ref_logp, t, eps_
     old = f32(old_logp, "old_logp", (B, S))
     per_token = advantages.dim() != 1
     adv = f32(advantages, "advantages", (B, S) if per_token else (B,))
-    m = (f32(mask, "mask", (B, S)) if mask is not None
-         else torch.ones((B, S), dtype=torch.float32, device=dev))
     ref = f32(ref_logp, "ref_logp", (B, S)) if (beta != 0.0 and ref_logp is not None) else None
-    weight = grpo_token_weights(m, loss_type, max_completion_length, normalizer).contiguous()
+    kind, scale = _weight_kind(B, S, loss_type, max_completion_length, normalizer)
+    weight = _device_token_weights(mask, B, S, dev, kind, scale)
+    if weight is None:
+        m = (f32(mask, "mask", (B, S)) if mask is not None
+             else torch.ones((B, S), dtype=torch.float32, device=dev))
+        weight = grpo_token_weights(m, loss_type, max_completion_length, normalizer).contiguous()
     params = (t, eps_low, eps_high, beta, int(per_token), grad_scale)
     return _FusedGrpoStep.apply(logits, targets, old, ref, adv, weight, params)

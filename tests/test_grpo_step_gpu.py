@@ -347,23 +347,26 @@ def test_grad_scale_folds_the_upstream_gradient(c):
                                grad_scale=bad)
 
 
-@pytest.mark.parametrize("loss_type", ["grpo", "dr_grpo"])
-def test_hip_graph_capture_of_loss_and_backward(loss_type):
+@pytest.mark.parametrize("loss_type", ["grpo", "dr_grpo", "bnpo"])
+@pytest.mark.parametrize("mask_kind", ["float", "int32"])
+def test_hip_graph_capture_of_loss_and_backward(loss_type, mask_kind):
     """fused_grpo_step's forward and (0.5 * loss).backward() captured in one
     HIP graph: nothing on the way reads a device value on the host (the
     upstream gradient is applied by klp_scale_inplace, the token weights'
     normalisers are host floats).  Every replay, with new logits, eager work
     and synchronisations between replays, equals the eager step on the same
-    logits bit for bit."""
+    logits bit for bit.  An int32 mask takes klp_grpo_token_weights into the
+    graph (1200 tokens: "bnpo" in two launches through its workspace)."""
     ko = _ko()
-    B, S, V = 2, 40, 8192
+    B, S, V = 2, (40 if mask_kind == "float" else 600), 8192
     gen = torch.Generator(device=DEV).manual_seed(17)
 
     def logits():
         return (torch.randn(B, S, V, generator=gen, device=DEV) * 2).to(torch.bfloat16)
     x = logits().requires_grad_(True)
     t = torch.randint(0, V, (B, S), generator=gen, device=DEV)
-    mask = (torch.rand(B, S, generator=gen, device=DEV) < 0.9).float()
+    mask = torch.rand(B, S, generator=gen, device=DEV) < 0.9
+    mask = mask.float() if mask_kind == "float" else mask.to(torch.int32)
     adv = torch.randn(B, generator=gen, device=DEV)
     old = torch.full((B, S), -9.0, device=DEV)
     kw = dict(eps_low=0.2, eps_high=0.28, loss_type=loss_type)
@@ -385,7 +388,7 @@ def test_hip_graph_capture_of_loss_and_backward(loss_type):
     with torch.cuda.graph(g, stream=s):
         out = step(x)
     for rep in range(3):
-        print(f"graph replay {rep} ({loss_type})", flush=True)
+        print(f"graph replay {rep} ({loss_type}, {mask_kind} mask)", flush=True)
         with torch.no_grad():
             x.copy_(logits())
         junk = torch.randn(1000, device=DEV).sum()  # unrelated eager work
