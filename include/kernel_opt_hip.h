@@ -361,7 +361,7 @@ int klp_grpo_step(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                   void* d_logits, void* sched, void* stream);
 
 /*
- * The fused GRPO step's token weights from a mask, in one launch: weights
+ * The fused GRPO step's token weights from a mask, on the device: weights
  * [n_seqs, seq_len] float32 = m / normaliser with m the mask (NULL: all
  * ones) and the normaliser of `loss_type` (KLP_GRPO_LOSS_GRPO: n_seqs *
  * max(row sum of m, 1), row by row; KLP_GRPO_LOSS_BNPO: max(sum of m, 1);
